@@ -1,0 +1,286 @@
+"""Benchmark: 24-layer DeBERTa-v3-large encoder + GLiNER classifier head on one
+MI355X, B=32 rows of L=256 tokens per step (synthetic seeded inputs and
+random-init fp16 weights of the real architecture).
+
+One step = one `classify` of a 32-row batch (embedding, 24 layers, classifier)
+with inputs resident in HBM.  Prints ONE JSON line on stdout (logs on stderr):
+rows/s over exactly --steps timed steps, the roofline of the dominant kernel
+(measured live with HIP events on the launch stream) and a CPU baseline (the
+numpy port of the reference graph on a bounded sample, this host's cores).
+
+Kernel timings use rotating buffer sets larger than the 256 MB Infinity Cache
+so that HBM, not the cache, serves the reads.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "gliner-decide-metal_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
+FP16_DENSE_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
+ROTATE_BYTES = 600 << 20  # > 2x the 256 MB MALL
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--workload", default="classify", choices=["classify", "long_context"])
+    p.add_argument("--compiled", action="store_true", help="replay a captured hipGraph per step")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
+    p.add_argument("--kernel-iters", type=int, default=60)
+    return p.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# live kernel timing
+# ---------------------------------------------------------------------------
+def time_launches(fn, sets, iters):
+    """Average duration (us) of fn(set) over `iters` launches cycling through
+    the buffer sets, between two events on the launch stream."""
+    import torch
+    for s in sets[:2]:
+        fn(s)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(iters):
+        fn(sets[i % len(sets)])
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) * 1000.0 / iters
+
+
+def measure_kernels(model_cfg, iters):
+    import torch
+    from gliner_decide.fused_kernels import FusedKernels
+    from gliner_decide.synthetic import normal16, relbias_inputs
+
+    fk = FusedKernels()
+    dev = torch.device("cuda")
+    out = {}
+
+    # residual-add LayerNorm, 8192 x 1024 (the model's shape at B=32, L=256)
+    rows, cols = 8192, 1024
+    nbytes = 3 * rows * cols * 2 + 2 * cols * 2
+    nsets = max(2, ROTATE_BYTES // (3 * rows * cols * 2) + 1)
+    g = torch.from_numpy(normal16(2, "gamma", (cols,), 1.0, 0.1)).to(dev)
+    b = torch.from_numpy(normal16(2, "beta", (cols,), 0.0, 0.1)).to(dev)
+    x0 = torch.from_numpy(normal16(2, "x", (rows, cols))).to(dev)
+    r0 = torch.from_numpy(normal16(2, "residual", (rows, cols))).to(dev)
+    sets = [(x0.roll(i, 0).contiguous(), r0.roll(i, 0).contiguous(), torch.empty_like(x0)) for i in range(nsets)]
+    from gliner_decide import _native as N
+    from gliner_decide.device import stream_handle
+    lib = N.lib()
+
+    def ln(s):
+        N.check(lib.gd_residual_layer_norm(s[0].data_ptr(), s[1].data_ptr(), g.data_ptr(), b.data_ptr(),
+                                           s[2].data_ptr(), rows, cols, 1e-7, N.GD_LN_SUM_F16, stream_handle()))
+
+    us = time_launches(ln, sets, iters)
+    out["residual_layernorm"] = dict(kernel="residual_ln_kernel<2>", shape=[rows, cols], us=us, bytes=nbytes,
+                                     gbs=nbytes / us / 1e3, bound="hbm", launches_per_step=48)
+    del sets
+
+    # relative bias + masked softmax, B=32 H=16 L=256 D=64 -> P [32,16,256,256]
+    d = relbias_inputs(seed=3)
+    B, H, L, D = 32, 16, 256, 64
+    pk = torch.from_numpy(d["pos_key"]).to(dev).view(512, H, D).permute(1, 0, 2)
+    pq = torch.from_numpy(d["pos_query"]).to(dev).view(512, H, D).permute(1, 0, 2)
+    mask = torch.from_numpy(d["mask"]).to(dev)
+    q0 = torch.from_numpy(d["q"]).to(dev)
+    k0 = torch.from_numpy(d["k"]).to(dev)
+    per_set = (2 * B * H * L * D + B * H * L * L) * 2
+    nsets = max(2, ROTATE_BYTES // per_set + 1)
+    sets = [(q0.roll(i, 0).contiguous(), k0.roll(i, 0).contiguous(),
+             torch.empty((B, H, L, L), dtype=torch.float16, device=dev)) for i in range(nsets)]
+    nbytes = 2 * B * H * L * D * 2 + 2 * 512 * H * D * 2 + B * 4 + B * H * L * L * 2
+
+    def rb(s):
+        fk.deberta_attention(s[0], s[1], None, pk, pq, mask, output="probs", out=s[2])
+
+    us = time_launches(rb, sets, iters)
+    out["relbias_softmax"] = dict(kernel="deberta_attention_kernel<16,PROBS>", shape=[B, H, L, L], us=us,
+                                  bytes=nbytes, gbs=nbytes / us / 1e3, bound="hbm", launches_per_step=0)
+    del sets
+
+    # attention as the encoder runs it: context output from the fused QKV layout
+    T = B * L
+    qkv = torch.randn((T, 3 * H * D), device=dev, dtype=torch.float16)
+    ctx = torch.empty((T, H * D), device=dev, dtype=torch.float16)
+    amask = torch.from_numpy(d["mask"]).to(dev)
+    v5 = qkv.view(B, L, 3, H, D)
+    qv, kv_, vv = (v5[:, :, i].permute(0, 2, 1, 3) for i in range(3))
+    us = time_launches(lambda s: fk.deberta_attention(qv, kv_, vv, pk, pq, amask, output="context", out=ctx), [0],
+                       iters)
+    flops = 2 * B * H * L * L * D * 2  # QK^T and PV (bias terms counted separately below)
+    out["attention_context"] = dict(kernel="deberta_attention_kernel<16,CONTEXT>", shape=[B, H, L, D], us=us,
+                                    flops=flops, bytes=(4 * T * H * D) * 2, bound="mfma", launches_per_step=24,
+                                    tflops=flops / us / 1e6)
+    del qkv, ctx
+
+    # the four projections at T = 8192
+    C, F = 1024, 4096
+    for name, (n, k, epi) in {"qkv_proj": (3 * C, C, "bias"), "out_proj": (C, C, "bias"),
+                              "ffn_up_gelu": (F, C, "gelu"), "ffn_down": (C, F, "bias")}.items():
+        a = torch.randn((T, k), device=dev, dtype=torch.float16)
+        w = torch.randn((n, k), device=dev, dtype=torch.float16) * 0.02
+        bias = torch.randn((n,), device=dev, dtype=torch.float16)
+        c = torch.empty((T, n), device=dev, dtype=torch.float16)
+
+        def lin(s, a=a, w=w, bias=bias, c=c, n=n, k=k, epi=epi):
+            N.check(lib.gd_linear(a.data_ptr(), w.data_ptr(), bias.data_ptr(), c.data_ptr(), T, n, k, k, n, None, 0,
+                                  {"bias": N.GD_EPI_BIAS, "gelu": N.GD_EPI_BIAS_GELU}[epi], stream_handle()))
+
+        us = time_launches(lin, [0], iters)
+        flops = 2 * T * n * k
+        out[name] = dict(kernel="gemm_nt_kernel<256,128>", shape=[T, n, k], us=us, flops=flops,
+                         tflops=flops / us / 1e6, bound="mfma", launches_per_step=24,
+                         bytes=(T * k + n * k + T * n) * 2)
+        del a, w, c
+    torch.cuda.synchronize()
+    return out
+
+
+def roofline_of(kernels):
+    """The kernel with the largest time share of one forward step."""
+    best = max((v for v in kernels.values() if v["launches_per_step"] > 0),
+               key=lambda v: v["us"] * v["launches_per_step"])
+    if best["bound"] == "hbm":
+        ach, peak, unit = best["gbs"], HBM_PEAK_GBS, "GB/s"
+    else:
+        ach, peak, unit = best["tflops"], FP16_DENSE_TFLOPS, "TFLOP/s"
+    name = [k for k, v in kernels.items() if v is best][0]
+    return dict(kernel=name, bound=best["bound"], achieved=round(ach, 2), peak=peak, unit=unit,
+                frac=round(ach / peak, 4), traffic=None, avg_us=round(best["us"], 2),
+                algorithmic_per_launch=best.get("flops", best.get("bytes")))
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the numpy port of the reference graph (oracle), fp32
+# ---------------------------------------------------------------------------
+def cpu_baseline(weights, cfg, batch, budget_s):
+    import numpy as np
+    from oracle import deberta as O
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:
+        cores = os.cpu_count() or 1
+    oc = O.Config(**{k: getattr(cfg, k) for k in O.Config.__dataclass_fields__})
+    w32 = {k: v.astype(np.float32) for k, v in weights.items()}
+    om = O.OracleModel(O.ModelWeights.from_store(w32, oc), oc, round16=False, dtype=np.float32)
+    a = batch.arrays()
+    done, t0 = 0, time.perf_counter()
+    while done < a["input_ids"].shape[0]:
+        s = slice(done, done + 1)
+        om.forward(a["input_ids"][s], a["attention_mask"][s], a["marker_indices"][s], a["marker_mask"][s])
+        done += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    el = time.perf_counter() - t0
+    return dict(value=round(done / el, 3), unit="rows/s", cores=int(cores), kind="port",
+                sample=f"{done} row(s) of the B=32 L=256 batch through the numpy fp32 port of the reference graph "
+                       f"(24 layers + classifier), {el:.1f} s")
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (this path is data-parallel "
+              "over independent rows and runs on a single MI355X)", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+    from gliner_decide import DecisionInput, GLiNERDecideClassifier
+    from gliner_decide.config import DeBERTaV2Configuration
+    from gliner_decide.synthetic import classification_batch, long_context_batch, synthetic_weights
+
+    torch.cuda.set_device(0)
+    cfg = DeBERTaV2Configuration(vocab_size=128100)
+    t = time.perf_counter()
+    weights = synthetic_weights(cfg, seed=4)
+    log(f"weights generated in {time.perf_counter() - t:.1f} s")
+    model = GLiNERDecideClassifier(weights, cfg, use_compiled_graph=args.compiled)
+    log(f"model on device: {model.device_bytes / 2**20:.0f} MiB")
+    if args.workload == "classify":
+        batch = classification_batch(seed=4)
+        wl = dict(workload="24L DeBERTa-v3-large encoder + GLiNER classifier head, B=32 L=256 "
+                           "(lengths U[40,256], 1 task x 5 labels)", global_batch=32, seq_len=256)
+    else:
+        batch = long_context_batch(seed=6)
+        wl = dict(workload="24L encoder + classifier, B=64 L=512 full rows, 3 heads (20/20/8 labels)",
+                  global_batch=64, seq_len=512)
+    ids, mask, markers, mmask = DecisionInput(**batch.arrays()).to_device()
+    B, L = ids.shape
+    _, Hh, O_ = markers.shape
+    model.reserve(B, L, Hh, O_)
+    logits = torch.empty((B, Hh, O_), dtype=torch.float16, device=ids.device)
+    for _ in range(args.warmup):
+        model.classify_device(ids, mask, markers, mmask, logits)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        model.classify_device(ids, mask, markers, mmask, logits)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed * 1000 / args.steps
+    rows_s = B * args.steps / elapsed
+    assert torch.isfinite(logits.float()).all()
+    log(f"e2e: {ms:.3f} ms/step, {rows_s:.1f} rows/s")
+
+    kernels = measure_kernels(cfg, args.kernel_iters)
+    for k, v in kernels.items():
+        extra = f"{v['gbs']:.0f} GB/s" if "gbs" in v and v["bound"] == "hbm" else f"{v.get('tflops', 0):.0f} TFLOP/s"
+        log(f"  {k:20s} {v['us']:9.2f} us  {extra}")
+    roof = roofline_of(kernels)
+
+    cpu = None
+    if not args.no_cpu_baseline and args.workload == "classify":
+        cpu = cpu_baseline(weights, cfg, batch, args.cpu_seconds)
+        log(f"cpu baseline: {cpu}")
+
+    line = {
+        "metric": "rows/s, 24L encoder+cls head B=32 L=256; fused LN/rel-bias GB/s vs HBM peak",
+        "value": round(rows_s, 2),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded ids/lengths; random-init N(0,0.02) fp16 weights of DeBERTa-v3-large + GLiNER head)",
+        "config": dict(wl, parallelism="single GPU", compiled_graph=args.compiled),
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                    for k, v in kernels.items()},
+        "fused_ln_gbs": round(kernels["residual_layernorm"]["gbs"], 1),
+        "fused_ln_frac_hbm": round(kernels["residual_layernorm"]["gbs"] / HBM_PEAK_GBS, 4),
+        "relbias_softmax_gbs": round(kernels["relbias_softmax"]["gbs"], 1),
+        "relbias_softmax_frac_hbm": round(kernels["relbias_softmax"]["gbs"] / HBM_PEAK_GBS, 4),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,86 @@
+"""Builds libgliner_decide_hip.so for gfx950 with hipcc.
+
+Every source under csrc/ is compiled as HIP (device code for gfx950 only,
+packed-fp32 instructions disabled) into objects under _build/, then linked
+into lib/libgliner_decide_hip.so.  Run `python build.py` or call `build()`.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+REPO = PKG_DIR.parent
+CSRC = PKG_DIR / "csrc"
+BUILD_DIR = PKG_DIR / "_build"
+LIB_DIR = PKG_DIR / "lib"
+LIB_PATH = LIB_DIR / "libgliner_decide_hip.so"
+ARCH = "gfx950"
+
+COMMON_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-fvisibility=hidden",
+    "-Wall",
+    "-Wno-unused-function",
+    "-Wno-unused-variable",
+    "-Wno-unused-command-line-argument",
+    # Packed fp32 VALU forms are not to be generated on this hardware pool.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{REPO / 'include'}",
+    f"-I{CSRC}",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (ROCm is required to build the library)")
+
+
+def _compile(src: Path, obj: Path) -> tuple[Path, int, str]:
+    cmd = [hipcc(), "-x", "hip", "-c", str(src), "-o", str(obj), *COMMON_FLAGS]
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    log = p.stdout + p.stderr
+    # hipcc's host pass does not know the packed-fp32 feature; drop that note.
+    log = "\n".join(line for line in log.splitlines() if "packed-fp32-ops" not in line)
+    return src, p.returncode, log
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    BUILD_DIR.mkdir(exist_ok=True)
+    LIB_DIR.mkdir(exist_ok=True)
+    sources = sorted([*CSRC.glob("*.hip"), *CSRC.glob("*.cpp")])
+    if not sources:
+        raise RuntimeError(f"no sources under {CSRC}")
+    objs = [BUILD_DIR / (s.name + ".o") for s in sources]
+    jobs = jobs or min(len(sources), max(1, min(os.cpu_count() or 1, 8)))
+    failures = []
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        for src, rc, log in ex.map(lambda a: _compile(*a), zip(sources, objs)):
+            if rc != 0:
+                failures.append(f"--- {src.name} ---\n{log}")
+            elif verbose and log.strip():
+                print(f"--- {src.name} ---\n{log}", file=sys.stderr)
+    if failures:
+        raise RuntimeError("HIP compilation failed:\n" + "\n".join(failures))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc(), "-shared", f"--offload-arch={ARCH}", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError("link failed:\n" + p.stdout + p.stderr)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    path = build(verbose="-v" in sys.argv)
+    print(path)

@@ -1,0 +1,136 @@
+// Shared helpers for the gfx950 kernels and the C-ABI: status codes, error
+// reporting, fp16 vector types, wave64 reductions and MFMA wrappers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "gliner_decide.h"
+
+namespace gd {
+
+// ---------------------------------------------------------------------------
+// Error reporting: every C-ABI call returns a gd_status; the message of the
+// last failure on the calling thread is kept for gd_last_error().
+// ---------------------------------------------------------------------------
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+const char* last_error();
+void clear_error();
+
+inline int fail(int code, const char* msg) {
+  set_error("%s", msg);
+  return code;
+}
+
+#define GD_CHECK_ARG(cond, ...)                  \
+  do {                                           \
+    if (!(cond)) {                               \
+      ::gd::set_error(__VA_ARGS__);              \
+      return GD_ERR_INVALID_ARGUMENT;            \
+    }                                            \
+  } while (0)
+
+#define GD_CHECK_SHAPE(cond, ...)                \
+  do {                                           \
+    if (!(cond)) {                               \
+      ::gd::set_error(__VA_ARGS__);              \
+      return GD_ERR_SHAPE;                       \
+    }                                            \
+  } while (0)
+
+#define GD_HIP_CHECK(expr)                                                        \
+  do {                                                                            \
+    hipError_t gd_hip_err_ = (expr);                                              \
+    if (gd_hip_err_ != hipSuccess) {                                              \
+      ::gd::set_error("HIP error %s (%d) at %s:%d: %s", hipGetErrorName(gd_hip_err_), \
+                      (int)gd_hip_err_, __FILE__, __LINE__, #expr);               \
+      return GD_ERR_HIP;                                                          \
+    }                                                                             \
+  } while (0)
+
+// After a kernel launch: report launch failures as GD_ERR_HIP.
+#define GD_LAUNCH_CHECK() GD_HIP_CHECK(hipGetLastError())
+
+#define GD_RETURN_IF_ERROR(expr)      \
+  do {                                \
+    int gd_status_ = (expr);          \
+    if (gd_status_ != GD_OK) return gd_status_; \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// Device-side types
+// ---------------------------------------------------------------------------
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t uint4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// Round-trip through fp16 (round to nearest even), staying in fp32.
+__device__ __forceinline__ float round_f16(float x) { return (float)(half_t)x; }
+
+// Butterfly reductions across the 64 lanes of a wave.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+// Make this wave's LDS writes visible to its other lanes (no s_barrier).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// MFMA wrappers (gfx950 double-rate fp16 forms).
+//  16x16x32: A lane l -> row l%16, k = 8*(l/16)+[0,8); B lane l -> col l%16,
+//            same k; C lane l -> col l%16, rows 4*(l/16)+[0,4).
+//  32x32x16: A lane l -> row l%32, k = 8*(l/32)+[0,8); B likewise; C lane l
+//            -> col l%32, rows 8*(i/4) + 4*(l/32) + i%4 for acc index i.
+__device__ __forceinline__ float4_t mfma16x16x32(half8_t a, half8_t b, float4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ float16_t mfma32x32x16(half8_t a, half8_t b, float16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// DeBERTa log-bucket relative position -> index into the 2*span relative
+// tables: clip(bucket(r) + span, 0, 2*span - 1).  Evaluated in fp32.  For
+// bucket_size 256 / max_position 512 and |r| <= 511 the exact value
+// x = ln(|r|/128) / ln(511/128) * 127 is either an integer (only at
+// |r| = 511, x = 127) or at least 0.003 away from one, so ceil(x - 1e-3)
+// reproduces the float64 reference exactly even when the two logs are
+// rounded differently (e.g. one constant-folded at compile time).
+__device__ __forceinline__ int relative_index(int r, int bucket_size, int max_position) {
+  const int mid = bucket_size >> 1;
+  int bucket;
+  const int a = r < 0 ? -r : r;
+  if (a <= mid) {
+    bucket = r;
+  } else {
+    const float x = logf((float)a / (float)mid) / logf((float)(max_position - 1) / (float)mid) * (float)(mid - 1);
+    const int lp = (int)ceilf(x - 1e-3f) + mid;
+    bucket = r < 0 ? -lp : lp;
+  }
+  int idx = bucket + bucket_size;
+  idx = idx < 0 ? 0 : idx;
+  idx = idx > 2 * bucket_size - 1 ? 2 * bucket_size - 1 : idx;
+  return idx;
+}
+
+}  // namespace gd

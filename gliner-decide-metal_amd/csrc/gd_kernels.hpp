@@ -1,0 +1,60 @@
+// Internal launchers (C++), called by the C-ABI layer and the classifier
+// context after argument validation.  All return a gd_status.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace gd {
+
+int launch_residual_layer_norm(const void* x, const void* residual, const void* gamma, const void* beta, void* out,
+                               int64_t rows, int64_t cols, float eps, uint32_t flags, hipStream_t stream);
+
+int launch_embedding_layer_norm(const int32_t* ids, const void* mask, const void* table, const void* gamma,
+                                const void* beta, void* out, int64_t tokens, int64_t cols, int64_t vocab, float eps,
+                                int32_t* error_flag, hipStream_t stream);
+
+int launch_linear(const void* a, const void* w, const void* bias, void* c, int64_t m, int64_t n, int64_t k, int64_t lda,
+                  int64_t ldc, const int32_t* a_rows, int64_t a_row_count, int epilogue_kind, hipStream_t stream);
+
+struct AttentionArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  int64_t qsb, qsh, qsl, ksb, ksh, ksl, vsb, vsh, vsl;
+  const void* pk;
+  const void* pq;
+  int64_t pksh, pksp, pqsh, pqsp;
+  const void* mask;
+  int mask_kind;
+  int64_t B, H, L, P;
+  int bucket_size;
+  float scale_qk;  // 1 / sqrt(3 D) in fp32 (applied to q.k)
+  float scale16;   // fp16(sqrt(3 D)) (divides the relative bias)
+  int output;      // GD_ATTN_OUT_*
+  void* out;
+  int64_t ldo;
+};
+
+int launch_deberta_attention(const AttentionArgs& args, hipStream_t stream);
+
+int launch_relative_bias_general(const void* q, const void* k, const void* pos_key, const void* pos_query,
+                                 const int32_t* c2p, const int32_t* p2c, const void* key_mask, float scale, int64_t B,
+                                 int64_t H, int64_t L, int64_t D, int64_t P, void* out, int32_t* error_flag,
+                                 hipStream_t stream);
+
+int launch_fused_attention_general(const void* q, const void* k, const void* v, const void* pos_key,
+                                   const void* pos_query, const int32_t* c2p, const int32_t* p2c, const void* key_mask,
+                                   float scale, int64_t B, int64_t H, int64_t L, int64_t D, int64_t P, void* out,
+                                   int32_t* error_flag, hipStream_t stream);
+
+int launch_relative_index_table(int32_t* out, int n, int bucket_size, int max_position, hipStream_t stream);
+
+// Classifier head helpers (head.hip).
+int launch_marker_rows(const int32_t* marker_indices, int32_t* rows_out, int64_t batch, int64_t seq_len,
+                       int64_t markers_per_row, int32_t* error_flag, hipStream_t stream);
+int launch_head_output(const void* inner, const void* w2, const void* b2, const float* marker_mask, void* logits,
+                       int64_t rows, int64_t width, hipStream_t stream);
+
+}  // namespace gd

@@ -1,0 +1,502 @@
+// GLiNERDecideClassifier on gfx950: weights resident in HBM, the per-layer
+// relative projections precomputed at load, and the encoder forward as a
+// fixed sequence of the library's kernels on one stream.
+//
+// Reference: GLiNERDecideClassifier (DeBERTa.swift:156-447).
+//   init      :188-242  weight assembly (fused QKV and rel-QK weights), rel
+//                        table LayerNorm, 24 relative projections
+//   classify  :244-272  compiled (MLX compile) or eager forward, eval = sync
+//   forward   :274-447  embedding -> 24 x layer -> classifier
+//   profile   :466-496  per-stage eval + wall time
+//
+// HBM layout (all fp16 unless noted), one allocation per tensor family:
+//   word_embeddings [V, C]; emb LN gamma/beta [C]
+//   per layer: qkv_w [3C, C] (query;key;value rows, as FusedProjectionWeight
+//   concatenates them), qkv_b [3C], out_w [C, C], out_b, ln1 g/b,
+//   inter_w [F, C], inter_b [F], ffn_w [C, F], ffn_b [C], ln2 g/b,
+//   pos_qk [512, 2C] = LN(rel) [Wq;Wk]^T + [bq;bk]: columns [0, C) are the
+//   relative queries (head h at h*D), [C, 2C) the relative keys.
+//   classifier: cls0_w [2048, C], cls0_b, cls2_w [1, 2048], cls2_b [1].
+// Workspace for T = B*L tokens: hidden [T, C], qkv [T, 3C] (Q | K | V per
+// token, so head h of Q is at column h*D with row stride 3C), ctx [T, C],
+// tmp [T, C], ffn [T, F], plus the marker rows / classifier inner buffers.
+#include "model.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "gd_common.hpp"
+#include "gd_kernels.hpp"
+
+namespace gd {
+
+namespace {
+
+struct HipDeviceGuard {
+  int prev = -1;
+  explicit HipDeviceGuard(int dev) {
+    if (hipGetDevice(&prev) == hipSuccess && prev != dev) (void)hipSetDevice(dev);
+  }
+  ~HipDeviceGuard() {
+    if (prev >= 0) (void)hipSetDevice(prev);
+  }
+};
+
+}  // namespace
+
+Classifier::~Classifier() {
+  release_graphs();
+  for (void* p : allocations_) (void)hipFree(p);
+  for (void* p : workspace_allocs_) (void)hipFree(p);
+}
+
+void Classifier::release_graphs() {
+  for (auto& kv : graphs_) {
+    if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
+    if (kv.second.graph) (void)hipGraphDestroy(kv.second.graph);
+  }
+  graphs_.clear();
+}
+
+int Classifier::device_alloc(size_t bytes, void** out, std::vector<void*>& owner) {
+  void* p = nullptr;
+  if (bytes == 0) bytes = 256;
+  hipError_t e = hipMalloc(&p, bytes);
+  if (e != hipSuccess) {
+    set_error("hipMalloc(%zu) failed: %s", bytes, hipGetErrorName(e));
+    (void)hipGetLastError();
+    return GD_ERR_OUT_OF_MEMORY;
+  }
+  owner.push_back(p);
+  device_bytes_ += (int64_t)bytes;
+  *out = p;
+  return GD_OK;
+}
+
+int Classifier::upload(const WeightStore& store, const std::string& key, const std::vector<int64_t>& shape,
+                       void** out, hipStream_t stream) {
+  const HostTensor* t = nullptr;
+  GD_RETURN_IF_ERROR(store.require(key, shape, GD_F16, &t));
+  GD_RETURN_IF_ERROR(device_alloc(t->data.size(), out, allocations_));
+  GD_HIP_CHECK(hipMemcpyAsync(*out, t->data.data(), t->data.size(), hipMemcpyHostToDevice, stream));
+  return GD_OK;
+}
+
+// Concatenates several [rows_i, cols] fp16 tensors along dim 0 into one
+// device tensor (FusedProjectionWeight, DeBERTa.swift:78-87).
+int Classifier::upload_concat(const WeightStore& store, const std::vector<std::string>& keys,
+                              const std::vector<std::vector<int64_t>>& shapes, void** out, hipStream_t stream) {
+  size_t total = 0;
+  std::vector<const HostTensor*> parts;
+  for (size_t i = 0; i < keys.size(); ++i) {
+    const HostTensor* t = nullptr;
+    GD_RETURN_IF_ERROR(store.require(keys[i], shapes[i], GD_F16, &t));
+    parts.push_back(t);
+    total += t->data.size();
+  }
+  GD_RETURN_IF_ERROR(device_alloc(total, out, allocations_));
+  size_t off = 0;
+  for (const HostTensor* t : parts) {
+    GD_HIP_CHECK(hipMemcpyAsync(static_cast<uint8_t*>(*out) + off, t->data.data(), t->data.size(),
+                                hipMemcpyHostToDevice, stream));
+    off += t->data.size();
+  }
+  return GD_OK;
+}
+
+std::vector<std::pair<std::string, std::vector<int64_t>>> required_weights(const gd_config& cfg) {
+  const int64_t C = cfg.hidden_size, F = cfg.intermediate_size, V = cfg.vocab_size, CH = cfg.classifier_hidden;
+  std::vector<std::pair<std::string, std::vector<int64_t>>> r = {
+      {"encoder.embeddings.word_embeddings.weight", {V, C}},
+      {"encoder.embeddings.LayerNorm.weight", {C}},
+      {"encoder.embeddings.LayerNorm.bias", {C}},
+      {"encoder.encoder.rel_embeddings.weight", {Classifier::kPositions, C}},
+      {"encoder.encoder.LayerNorm.weight", {C}},
+      {"encoder.encoder.LayerNorm.bias", {C}},
+  };
+  for (int i = 0; i < cfg.num_hidden_layers; ++i) {
+    const std::string p = "encoder.encoder.layer." + std::to_string(i);
+    for (const char* n : {"query", "key", "value"}) {
+      r.push_back({p + ".attention.self." + n + "_proj.weight", {C, C}});
+      r.push_back({p + ".attention.self." + n + "_proj.bias", {C}});
+    }
+    r.push_back({p + ".attention.output.dense.weight", {C, C}});
+    r.push_back({p + ".attention.output.dense.bias", {C}});
+    r.push_back({p + ".attention.output.LayerNorm.weight", {C}});
+    r.push_back({p + ".attention.output.LayerNorm.bias", {C}});
+    r.push_back({p + ".intermediate.dense.weight", {F, C}});
+    r.push_back({p + ".intermediate.dense.bias", {F}});
+    r.push_back({p + ".output.dense.weight", {C, F}});
+    r.push_back({p + ".output.dense.bias", {C}});
+    r.push_back({p + ".output.LayerNorm.weight", {C}});
+    r.push_back({p + ".output.LayerNorm.bias", {C}});
+  }
+  r.push_back({"classifier.0.weight", {CH, C}});
+  r.push_back({"classifier.0.bias", {CH}});
+  r.push_back({"classifier.2.weight", {1, CH}});
+  r.push_back({"classifier.2.bias", {1}});
+  return r;
+}
+
+int Classifier::init(const WeightStore& store, const gd_config& cfg, uint32_t flags, hipStream_t stream) {
+  cfg_ = cfg;
+  flags_ = flags;
+  const int64_t C = cfg.hidden_size, F = cfg.intermediate_size, H = cfg.num_attention_heads;
+  const int64_t V = cfg.vocab_size, CH = cfg.classifier_hidden;
+  GD_CHECK_ARG(C > 0 && H > 0 && C % H == 0, "hidden_size %lld must be a positive multiple of heads %lld",
+               (long long)C, (long long)H);
+  GD_CHECK_ARG(C / H == 64, "head size must be 64 (got %lld)", (long long)(C / H));
+  GD_CHECK_ARG(C % 128 == 0 && F % 128 == 0 && CH % 128 == 0 && C % 64 == 0 && F % 64 == 0,
+               "hidden/intermediate/classifier widths must be multiples of 128");
+  GD_CHECK_ARG(cfg.num_hidden_layers > 0, "num_hidden_layers must be positive");
+  GD_CHECK_ARG(V > 0, "vocab_size must be positive");
+  GD_CHECK_ARG(cfg.position_buckets == 256, "position_buckets must be 256 (the graph hard-codes 256/512)");
+  GD_CHECK_ARG(cfg.layer_norm_eps > 0.f, "layer_norm_eps must be positive");
+  if (flags & GD_USE_GENERIC_ATTENTION)
+    return fail(GD_ERR_UNSUPPORTED, "the explicit-score attention path (useFastAttention=false) is not built");
+
+  // Host-side check of every key, shape and dtype before any device work, so
+  // a bad checkpoint fails without allocating (WeightStore.array checks,
+  // Weights.swift:83-106).
+  for (const auto& req : required_weights(cfg)) {
+    const HostTensor* t = nullptr;
+    GD_RETURN_IF_ERROR(store.require(req.first, req.second, GD_F16, &t));
+  }
+  GD_HIP_CHECK(hipGetDevice(&device_));
+
+  // ---- weights (DeBERTa.swift:197-229) ----
+  GD_RETURN_IF_ERROR(upload(store, "encoder.embeddings.word_embeddings.weight", {V, C}, &word_emb_, stream));
+  GD_RETURN_IF_ERROR(upload(store, "encoder.embeddings.LayerNorm.weight", {C}, &emb_g_, stream));
+  GD_RETURN_IF_ERROR(upload(store, "encoder.embeddings.LayerNorm.bias", {C}, &emb_b_, stream));
+  void *rel = nullptr, *rel_g = nullptr, *rel_b = nullptr;
+  GD_RETURN_IF_ERROR(upload(store, "encoder.encoder.rel_embeddings.weight", {kPositions, C}, &rel, stream));
+  GD_RETURN_IF_ERROR(upload(store, "encoder.encoder.LayerNorm.weight", {C}, &rel_g, stream));
+  GD_RETURN_IF_ERROR(upload(store, "encoder.encoder.LayerNorm.bias", {C}, &rel_b, stream));
+  layers_.resize(cfg.num_hidden_layers);
+  for (int i = 0; i < cfg.num_hidden_layers; ++i) {
+    const std::string p = "encoder.encoder.layer." + std::to_string(i);
+    Layer& L = layers_[i];
+    GD_RETURN_IF_ERROR(upload_concat(store,
+                                     {p + ".attention.self.query_proj.weight", p + ".attention.self.key_proj.weight",
+                                      p + ".attention.self.value_proj.weight"},
+                                     {{C, C}, {C, C}, {C, C}}, &L.qkv_w, stream));
+    GD_RETURN_IF_ERROR(upload_concat(store,
+                                     {p + ".attention.self.query_proj.bias", p + ".attention.self.key_proj.bias",
+                                      p + ".attention.self.value_proj.bias"},
+                                     {{C}, {C}, {C}}, &L.qkv_b, stream));
+    GD_RETURN_IF_ERROR(upload(store, p + ".attention.output.dense.weight", {C, C}, &L.out_w, stream));
+    GD_RETURN_IF_ERROR(upload(store, p + ".attention.output.dense.bias", {C}, &L.out_b, stream));
+    GD_RETURN_IF_ERROR(upload(store, p + ".attention.output.LayerNorm.weight", {C}, &L.ln1_g, stream));
+    GD_RETURN_IF_ERROR(upload(store, p + ".attention.output.LayerNorm.bias", {C}, &L.ln1_b, stream));
+    GD_RETURN_IF_ERROR(upload(store, p + ".intermediate.dense.weight", {F, C}, &L.inter_w, stream));
+    GD_RETURN_IF_ERROR(upload(store, p + ".intermediate.dense.bias", {F}, &L.inter_b, stream));
+    GD_RETURN_IF_ERROR(upload(store, p + ".output.dense.weight", {C, F}, &L.ffn_w, stream));
+    GD_RETURN_IF_ERROR(upload(store, p + ".output.dense.bias", {C}, &L.ffn_b, stream));
+    GD_RETURN_IF_ERROR(upload(store, p + ".output.LayerNorm.weight", {C}, &L.ln2_g, stream));
+    GD_RETURN_IF_ERROR(upload(store, p + ".output.LayerNorm.bias", {C}, &L.ln2_b, stream));
+  }
+  GD_RETURN_IF_ERROR(upload(store, "classifier.0.weight", {CH, C}, &cls0_w_, stream));
+  GD_RETURN_IF_ERROR(upload(store, "classifier.0.bias", {CH}, &cls0_b_, stream));
+  GD_RETURN_IF_ERROR(upload(store, "classifier.2.weight", {1, CH}, &cls2_w_, stream));
+  GD_RETURN_IF_ERROR(upload(store, "classifier.2.bias", {1}, &cls2_b_, stream));
+  GD_RETURN_IF_ERROR(device_alloc(sizeof(int32_t), reinterpret_cast<void**>(&err_flag_), allocations_));
+  GD_HIP_CHECK(hipMemsetAsync(err_flag_, 0, sizeof(int32_t), stream));
+
+  // ---- relative precompute (DeBERTa.swift:208-227) ----
+  void* rel_n = nullptr;
+  std::vector<void*> scratch;
+  GD_RETURN_IF_ERROR(device_alloc((size_t)kPositions * C * 2, &rel_n, scratch));
+  int st = launch_residual_layer_norm(rel, nullptr, rel_g, rel_b, rel_n, kPositions, C, cfg.layer_norm_eps, 0, stream);
+  for (int i = 0; st == GD_OK && i < cfg.num_hidden_layers; ++i) {
+    st = device_alloc((size_t)kPositions * 2 * C * 2, &layers_[i].pos_qk, allocations_);
+    if (st != GD_OK) break;
+    // [posQ | posK] = relN [Wq; Wk]^T + [bq; bk]: the first 2C rows of qkv_w.
+    st = launch_linear(rel_n, layers_[i].qkv_w, layers_[i].qkv_b, layers_[i].pos_qk, kPositions, 2 * C, C, C, 2 * C,
+                       nullptr, 0, GD_EPI_BIAS, stream);
+  }
+  // The upload buffers are host memory: wait before returning.
+  hipError_t e = hipStreamSynchronize(stream);
+  for (void* p : scratch) (void)hipFree(p);
+  device_bytes_ -= (int64_t)kPositions * C * 2;
+  if (st != GD_OK) return st;
+  if (e != hipSuccess) {
+    set_error("relative precompute failed: %s", hipGetErrorName(e));
+    return GD_ERR_HIP;
+  }
+  return GD_OK;
+}
+
+int Classifier::reserve(int64_t B, int64_t L, int64_t Hh, int64_t O) {
+  const int64_t T = B * L, M = B * Hh * O;
+  if (T <= ws_tokens_ && M <= ws_markers_) return GD_OK;
+  const int64_t C = cfg_.hidden_size, F = cfg_.intermediate_size, CH = cfg_.classifier_hidden;
+  const int64_t nt = std::max(T, ws_tokens_), nm = std::max(M, ws_markers_);
+  release_graphs();  // captured graphs reference the old workspace
+  HipDeviceGuard guard(device_);
+  (void)hipDeviceSynchronize();
+  for (void* p : workspace_allocs_) {
+    (void)hipFree(p);
+  }
+  workspace_allocs_.clear();
+  device_bytes_ -= ws_bytes_;
+  const int64_t before = device_bytes_;
+  ws_ = Workspace{};
+  ws_tokens_ = ws_markers_ = 0;
+  auto A = [&](size_t bytes, void** p) { return device_alloc(bytes, p, workspace_allocs_); };
+  GD_RETURN_IF_ERROR(A((size_t)nt * C * 2, &ws_.hidden));
+  GD_RETURN_IF_ERROR(A((size_t)nt * 3 * C * 2, &ws_.qkv));
+  GD_RETURN_IF_ERROR(A((size_t)nt * C * 2, &ws_.ctx));
+  GD_RETURN_IF_ERROR(A((size_t)nt * C * 2, &ws_.tmp));
+  GD_RETURN_IF_ERROR(A((size_t)nt * F * 2, &ws_.ffn));
+  GD_RETURN_IF_ERROR(A((size_t)nm * 4, &ws_.marker_rows));
+  GD_RETURN_IF_ERROR(A((size_t)nm * CH * 2, &ws_.inner));
+  // staging for graph replays (inputs copied in, logits copied out)
+  GD_RETURN_IF_ERROR(A((size_t)nt * 4, &ws_.ids));
+  GD_RETURN_IF_ERROR(A((size_t)nt * 2, &ws_.mask));
+  GD_RETURN_IF_ERROR(A((size_t)nm * 4, &ws_.markers));
+  GD_RETURN_IF_ERROR(A((size_t)nm * 4, &ws_.marker_mask));
+  GD_RETURN_IF_ERROR(A((size_t)nm * 2, &ws_.logits));
+  ws_bytes_ = device_bytes_ - before;
+  ws_tokens_ = nt;
+  ws_markers_ = nm;
+  return GD_OK;
+}
+
+// One encoder layer (DeBERTa.swift:296-428).
+int Classifier::layer_forward(int li, const void* mask, int64_t B, int64_t L, hipStream_t stream, StageHook* hook) {
+  const Layer& Ly = layers_[li];
+  const int64_t C = cfg_.hidden_size, F = cfg_.intermediate_size, H = cfg_.num_attention_heads, D = C / H;
+  const int64_t T = B * L;
+  const float eps = cfg_.layer_norm_eps;
+  const uint32_t ln_flags = (flags_ & GD_USE_FUSED_KERNELS) ? 0u : GD_LN_SUM_F16;
+  char name[48];
+
+  if (hook) hook->begin(stream);
+  // QKV projection (:298-320)
+  GD_RETURN_IF_ERROR(launch_linear(ws_.hidden, Ly.qkv_w, Ly.qkv_b, ws_.qkv, T, 3 * C, C, C, 3 * C, nullptr, 0,
+                                   GD_EPI_BIAS, stream));
+  if (hook) {
+    std::snprintf(name, sizeof name, "layer_%d_attention_projection", li);
+    hook->end(name, stream);
+    hook->begin(stream);
+  }
+  // relative bias + masked softmax + P.V (:322-410)
+  AttentionArgs a{};
+  const half_t* qkv = static_cast<const half_t*>(ws_.qkv);
+  a.q = qkv;
+  a.k = qkv + C;
+  a.v = qkv + 2 * C;
+  a.qsb = a.ksb = a.vsb = L * 3 * C;
+  a.qsh = a.ksh = a.vsh = D;
+  a.qsl = a.ksl = a.vsl = 3 * C;
+  const half_t* pos = static_cast<const half_t*>(Ly.pos_qk);
+  a.pq = pos;
+  a.pk = pos + C;
+  a.pqsh = a.pksh = D;
+  a.pqsp = a.pksp = 2 * C;
+  a.mask = mask;
+  a.mask_kind = GD_MASK_ATTENTION;
+  a.B = B;
+  a.H = H;
+  a.L = L;
+  a.P = kPositions;
+  a.bucket_size = cfg_.position_buckets;
+  a.scale_qk = 1.0f / std::sqrt((float)(3 * D));
+  a.scale16 = (float)(_Float16)std::sqrt((float)(3 * D));
+  a.output = GD_ATTN_OUT_CONTEXT;
+  a.out = ws_.ctx;
+  a.ldo = C;
+  GD_RETURN_IF_ERROR(launch_deberta_attention(a, stream));
+  if (hook) {
+    std::snprintf(name, sizeof name, "layer_%d_attention", li);
+    hook->end(name, stream);
+    hook->begin(stream);
+  }
+  // output projection + residual LayerNorm (:412-418)
+  GD_RETURN_IF_ERROR(
+      launch_linear(ws_.ctx, Ly.out_w, Ly.out_b, ws_.tmp, T, C, C, C, C, nullptr, 0, GD_EPI_BIAS, stream));
+  GD_RETURN_IF_ERROR(
+      launch_residual_layer_norm(ws_.tmp, ws_.hidden, Ly.ln1_g, Ly.ln1_b, ws_.hidden, T, C, eps, ln_flags, stream));
+  if (hook) {
+    std::snprintf(name, sizeof name, "layer_%d_attention_output", li);
+    hook->end(name, stream);
+    hook->begin(stream);
+  }
+  // feed-forward + residual LayerNorm (:420-427)
+  GD_RETURN_IF_ERROR(launch_linear(ws_.hidden, Ly.inter_w, Ly.inter_b, ws_.ffn, T, F, C, C, F, nullptr, 0,
+                                   GD_EPI_BIAS_GELU, stream));
+  GD_RETURN_IF_ERROR(
+      launch_linear(ws_.ffn, Ly.ffn_w, Ly.ffn_b, ws_.tmp, T, C, F, F, C, nullptr, 0, GD_EPI_BIAS, stream));
+  GD_RETURN_IF_ERROR(
+      launch_residual_layer_norm(ws_.tmp, ws_.hidden, Ly.ln2_g, Ly.ln2_b, ws_.hidden, T, C, eps, ln_flags, stream));
+  if (hook) {
+    std::snprintf(name, sizeof name, "layer_%d_feed_forward", li);
+    hook->end(name, stream);
+  }
+  return GD_OK;
+}
+
+int Classifier::encode_into_workspace(const int32_t* ids, const void* mask, int64_t B, int64_t L, int num_layers,
+                                      hipStream_t stream, StageHook* hook) {
+  const int64_t T = B * L;
+  if (hook) hook->begin(stream);
+  GD_RETURN_IF_ERROR(launch_embedding_layer_norm(ids, mask, word_emb_, emb_g_, emb_b_, ws_.hidden, T,
+                                                 cfg_.hidden_size, cfg_.vocab_size, cfg_.layer_norm_eps, err_flag_,
+                                                 stream));
+  if (hook) hook->end("embedding", stream);
+  for (int i = 0; i < num_layers; ++i) GD_RETURN_IF_ERROR(layer_forward(i, mask, B, L, stream, hook));
+  return GD_OK;
+}
+
+int Classifier::forward(const int32_t* ids, const void* mask, const int32_t* markers, const float* marker_mask,
+                        int64_t B, int64_t L, int64_t Hh, int64_t O, void* logits, hipStream_t stream,
+                        StageHook* hook) {
+  const int64_t C = cfg_.hidden_size, CH = cfg_.classifier_hidden;
+  const int64_t M = B * Hh * O;
+  GD_RETURN_IF_ERROR(encode_into_workspace(ids, mask, B, L, cfg_.num_hidden_layers, stream, hook));
+  // classifier (:430-444)
+  if (hook) hook->begin(stream);
+  GD_RETURN_IF_ERROR(launch_marker_rows(markers, static_cast<int32_t*>(ws_.marker_rows), B, L, Hh * O, err_flag_,
+                                        stream));
+  GD_RETURN_IF_ERROR(launch_linear(ws_.hidden, cls0_w_, cls0_b_, ws_.inner, M, CH, C, C, CH,
+                                   static_cast<const int32_t*>(ws_.marker_rows), B * L, GD_EPI_BIAS_RELU, stream));
+  GD_RETURN_IF_ERROR(launch_head_output(ws_.inner, cls2_w_, cls2_b_, marker_mask, logits, M, CH, stream));
+  if (hook) hook->end("classifier", stream);
+  return GD_OK;
+}
+
+int Classifier::classify(const int32_t* ids, const void* mask, const int32_t* markers, const float* marker_mask,
+                         int64_t B, int64_t L, int64_t Hh, int64_t O, void* logits, hipStream_t stream) {
+  GD_RETURN_IF_ERROR(reserve(B, L, Hh, O));
+  if (!(flags_ & GD_USE_COMPILED_GRAPH))
+    return forward(ids, mask, markers, marker_mask, B, L, Hh, O, logits, stream, nullptr);
+
+  // Compiled path (MLX compile, DeBERTa.swift:175-186, 249-261): the forward
+  // for one shape is captured once into a hipGraph over the context's staging
+  // buffers; each call copies the inputs in, replays it and copies the
+  // logits out.
+  const int64_t T = B * L, M = B * Hh * O;
+  GD_HIP_CHECK(hipMemcpyAsync(ws_.ids, ids, (size_t)T * 4, hipMemcpyDeviceToDevice, stream));
+  GD_HIP_CHECK(hipMemcpyAsync(ws_.mask, mask, (size_t)T * 2, hipMemcpyDeviceToDevice, stream));
+  GD_HIP_CHECK(hipMemcpyAsync(ws_.markers, markers, (size_t)M * 4, hipMemcpyDeviceToDevice, stream));
+  GD_HIP_CHECK(hipMemcpyAsync(ws_.marker_mask, marker_mask, (size_t)M * 4, hipMemcpyDeviceToDevice, stream));
+  const ShapeKey key{B, L, Hh, O};
+  auto it = graphs_.find(key);
+  if (it == graphs_.end()) {
+    GraphEntry ge;
+    GD_HIP_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+    int st = forward(static_cast<const int32_t*>(ws_.ids), ws_.mask, static_cast<const int32_t*>(ws_.markers),
+                     static_cast<const float*>(ws_.marker_mask), B, L, Hh, O, ws_.logits, stream, nullptr);
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(stream, &graph);
+    if (st != GD_OK) {
+      if (graph) (void)hipGraphDestroy(graph);
+      return st;
+    }
+    if (e != hipSuccess) {
+      set_error("graph capture failed: %s", hipGetErrorName(e));
+      return GD_ERR_HIP;
+    }
+    ge.graph = graph;
+    e = hipGraphInstantiate(&ge.exec, graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+      (void)hipGraphDestroy(graph);
+      set_error("graph instantiate failed: %s", hipGetErrorName(e));
+      return GD_ERR_HIP;
+    }
+    it = graphs_.emplace(key, ge).first;
+  }
+  GD_HIP_CHECK(hipGraphLaunch(it->second.exec, stream));
+  GD_HIP_CHECK(hipMemcpyAsync(logits, ws_.logits, (size_t)M * 2, hipMemcpyDeviceToDevice, stream));
+  return GD_OK;
+}
+
+int Classifier::encode(const int32_t* ids, const void* mask, int64_t B, int64_t L, int num_layers, void* hidden_out,
+                       hipStream_t stream) {
+  GD_RETURN_IF_ERROR(reserve(B, L, 1, 1));
+  const int n = num_layers < 0 ? cfg_.num_hidden_layers : std::min(num_layers, cfg_.num_hidden_layers);
+  GD_RETURN_IF_ERROR(encode_into_workspace(ids, mask, B, L, n, stream, nullptr));
+  GD_HIP_CHECK(hipMemcpyAsync(hidden_out, ws_.hidden, (size_t)B * L * cfg_.hidden_size * 2, hipMemcpyDeviceToDevice,
+                              stream));
+  return GD_OK;
+}
+
+int Classifier::layer(int li, const void* hidden_in, const void* mask, int64_t B, int64_t L, void* hidden_out,
+                      hipStream_t stream) {
+  GD_CHECK_ARG(li >= 0 && li < cfg_.num_hidden_layers, "layer index %d out of range", li);
+  GD_RETURN_IF_ERROR(reserve(B, L, 1, 1));
+  const size_t bytes = (size_t)B * L * cfg_.hidden_size * 2;
+  GD_HIP_CHECK(hipMemcpyAsync(ws_.hidden, hidden_in, bytes, hipMemcpyDeviceToDevice, stream));
+  GD_RETURN_IF_ERROR(layer_forward(li, mask, B, L, stream, nullptr));
+  GD_HIP_CHECK(hipMemcpyAsync(hidden_out, ws_.hidden, bytes, hipMemcpyDeviceToDevice, stream));
+  return GD_OK;
+}
+
+namespace {
+
+struct EventHook : StageHook {
+  struct Rec {
+    std::string name;
+    hipEvent_t a, b;
+  };
+  std::vector<Rec> recs;
+  hipEvent_t pending = nullptr;
+  int status = GD_OK;
+  void begin(hipStream_t s) override {
+    if (hipEventCreate(&pending) != hipSuccess || hipEventRecord(pending, s) != hipSuccess) status = GD_ERR_HIP;
+  }
+  void end(const char* name, hipStream_t s) override {
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess || hipEventRecord(e, s) != hipSuccess) {
+      status = GD_ERR_HIP;
+      return;
+    }
+    recs.push_back({name, pending, e});
+    pending = nullptr;
+  }
+  ~EventHook() override {
+    for (auto& r : recs) {
+      (void)hipEventDestroy(r.a);
+      (void)hipEventDestroy(r.b);
+    }
+    if (pending) (void)hipEventDestroy(pending);
+  }
+};
+
+}  // namespace
+
+int Classifier::classify_profiled(const int32_t* ids, const void* mask, const int32_t* markers,
+                                  const float* marker_mask, int64_t B, int64_t L, int64_t Hh, int64_t O, void* logits,
+                                  gd_profile_event* events, int capacity, int* count, hipStream_t stream) {
+  GD_RETURN_IF_ERROR(reserve(B, L, Hh, O));
+  EventHook hook;
+  GD_RETURN_IF_ERROR(forward(ids, mask, markers, marker_mask, B, L, Hh, O, logits, stream, &hook));
+  if (hook.status != GD_OK) return fail(GD_ERR_HIP, "event record failed");
+  GD_HIP_CHECK(hipStreamSynchronize(stream));
+  int n = 0;
+  for (auto& r : hook.recs) {
+    if (n >= capacity) break;
+    float ms = 0.f;
+    GD_HIP_CHECK(hipEventElapsedTime(&ms, r.a, r.b));
+    std::snprintf(events[n].name, sizeof events[n].name, "%s", r.name.c_str());
+    events[n].milliseconds = ms;
+    ++n;
+  }
+  *count = n;
+  return GD_OK;
+}
+
+int Classifier::check_device_errors(hipStream_t stream) {
+  int32_t host = 0;
+  GD_HIP_CHECK(hipMemcpyAsync(&host, err_flag_, sizeof host, hipMemcpyDeviceToHost, stream));
+  GD_HIP_CHECK(hipStreamSynchronize(stream));
+  if (host) {
+    GD_HIP_CHECK(hipMemsetAsync(err_flag_, 0, sizeof(int32_t), stream));
+    GD_HIP_CHECK(hipStreamSynchronize(stream));
+    return fail(GD_ERR_DEVICE_INDEX, "an input id or marker index was out of range (row 0 / position 0 was used)");
+  }
+  return GD_OK;
+}
+
+}  // namespace gd

@@ -1,0 +1,93 @@
+// GLiNERDecideClassifier context (DeBERTa.swift:156-447).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <map>
+#include <string>
+#include <tuple>
+#include <utility>
+#include <vector>
+
+#include "gliner_decide.h"
+#include "weights.hpp"
+
+namespace gd {
+
+// Every (key, shape) the classifier needs, in checkpoint names.
+std::vector<std::pair<std::string, std::vector<int64_t>>> required_weights(const gd_config& cfg);
+
+// Per-stage timing hook (the reference `stage` / `stage3` wrappers).
+struct StageHook {
+  virtual ~StageHook() = default;
+  virtual void begin(hipStream_t s) = 0;
+  virtual void end(const char* name, hipStream_t s) = 0;
+};
+
+class Classifier {
+ public:
+  static constexpr int64_t kPositions = 512;  // DeBERTa.swift:205-206, :505
+
+  ~Classifier();
+  int init(const WeightStore& store, const gd_config& cfg, uint32_t flags, hipStream_t stream);
+  int reserve(int64_t B, int64_t L, int64_t Hh, int64_t O);
+  int classify(const int32_t* ids, const void* mask, const int32_t* markers, const float* marker_mask, int64_t B,
+               int64_t L, int64_t Hh, int64_t O, void* logits, hipStream_t stream);
+  int classify_profiled(const int32_t* ids, const void* mask, const int32_t* markers, const float* marker_mask,
+                        int64_t B, int64_t L, int64_t Hh, int64_t O, void* logits, gd_profile_event* events,
+                        int capacity, int* count, hipStream_t stream);
+  int encode(const int32_t* ids, const void* mask, int64_t B, int64_t L, int num_layers, void* hidden_out,
+             hipStream_t stream);
+  int layer(int li, const void* hidden_in, const void* mask, int64_t B, int64_t L, void* hidden_out,
+            hipStream_t stream);
+  int check_device_errors(hipStream_t stream);
+  int64_t device_bytes() const { return device_bytes_; }
+  const gd_config& config() const { return cfg_; }
+
+ private:
+  struct Layer {
+    void *qkv_w = nullptr, *qkv_b = nullptr, *out_w = nullptr, *out_b = nullptr, *ln1_g = nullptr, *ln1_b = nullptr;
+    void *inter_w = nullptr, *inter_b = nullptr, *ffn_w = nullptr, *ffn_b = nullptr, *ln2_g = nullptr,
+         *ln2_b = nullptr;
+    void* pos_qk = nullptr;
+  };
+  struct Workspace {
+    void *hidden = nullptr, *qkv = nullptr, *ctx = nullptr, *tmp = nullptr, *ffn = nullptr;
+    void *marker_rows = nullptr, *inner = nullptr;
+    void *ids = nullptr, *mask = nullptr, *markers = nullptr, *marker_mask = nullptr, *logits = nullptr;
+  };
+  using ShapeKey = std::tuple<int64_t, int64_t, int64_t, int64_t>;
+  struct GraphEntry {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+  };
+
+  int device_alloc(size_t bytes, void** out, std::vector<void*>& owner);
+  int upload(const WeightStore& store, const std::string& key, const std::vector<int64_t>& shape, void** out,
+             hipStream_t stream);
+  int upload_concat(const WeightStore& store, const std::vector<std::string>& keys,
+                    const std::vector<std::vector<int64_t>>& shapes, void** out, hipStream_t stream);
+  int layer_forward(int li, const void* mask, int64_t B, int64_t L, hipStream_t stream, StageHook* hook);
+  int encode_into_workspace(const int32_t* ids, const void* mask, int64_t B, int64_t L, int num_layers,
+                            hipStream_t stream, StageHook* hook);
+  int forward(const int32_t* ids, const void* mask, const int32_t* markers, const float* marker_mask, int64_t B,
+              int64_t L, int64_t Hh, int64_t O, void* logits, hipStream_t stream, StageHook* hook);
+  void release_graphs();
+
+  gd_config cfg_{};
+  uint32_t flags_ = 0;
+  int device_ = 0;
+  std::vector<void*> allocations_;
+  std::vector<void*> workspace_allocs_;
+  int64_t device_bytes_ = 0;
+  int64_t ws_bytes_ = 0;
+  void *word_emb_ = nullptr, *emb_g_ = nullptr, *emb_b_ = nullptr;
+  std::vector<Layer> layers_;
+  void *cls0_w_ = nullptr, *cls0_b_ = nullptr, *cls2_w_ = nullptr, *cls2_b_ = nullptr;
+  int32_t* err_flag_ = nullptr;
+  Workspace ws_;
+  int64_t ws_tokens_ = 0, ws_markers_ = 0;
+  std::map<ShapeKey, GraphEntry> graphs_;
+};
+
+}  // namespace gd

@@ -1,0 +1,96 @@
+"""Host-side rules around the encoder: label decode, batch chunking, buckets.
+
+References: `decode` (RawCLI.swift:182-223), `makeBatchChunk`
+(main.swift:7-51), bucket selection (NativeTokenizer.swift:85-88, 134-138)
+and grouping by shape (RawCLI.swift:135-163).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+
+DEFAULT_BUCKETS = (32, 64, 96, 128, 256, 512)
+
+
+@dataclass(frozen=True)
+class DecisionTask:
+    """A task head: its label names and whether it is multi-label."""
+
+    name: str
+    labels: tuple
+    multi_label: bool = False
+
+
+@dataclass
+class Prediction:
+    task: str
+    labels: list
+    probabilities: list
+
+
+def decode(logits, row: int, tasks) -> list:
+    """RawCLI.swift:182-223.  logits: [B, Hh, O] (any float type).
+    Single-label: max-shifted softmax over the task's labels, argmax (first
+    maximum).  Multi-label: sigmoid, labels with p >= 0.5, argmax if none."""
+    arr = np.asarray(logits, dtype=np.float32)
+    out = []
+    for head, task in enumerate(tasks):
+        probs = [float(arr[row, head, i]) for i in range(len(task.labels))]
+        if task.multi_label:
+            probs = [1.0 / (1.0 + math.exp(-x)) for x in probs]
+            selected = [i for i, p in enumerate(probs) if p >= 0.5]
+            if not selected:
+                selected = [_first_argmax(probs)]
+            out.append(Prediction(task.name, [task.labels[i] for i in selected], probs))
+        else:
+            m = max(probs) if probs else 0.0
+            ex = [math.exp(x - m) for x in probs]
+            total = sum(ex)
+            probs = [e / total for e in ex]
+            best = _first_argmax(probs)
+            out.append(Prediction(task.name, [task.labels[best]], probs))
+    return out
+
+
+def _first_argmax(values) -> int:
+    """Swift `max(by:)` keeps the first of equal maxima."""
+    best = 0
+    for i, v in enumerate(values):
+        if v > values[best]:
+            best = i
+    return best
+
+
+def select_bucket(length: int, buckets=DEFAULT_BUCKETS) -> int:
+    """Smallest bucket >= length (NativeTokenizer.swift:134-138)."""
+    ordered = sorted(set(buckets))
+    if not ordered:
+        raise ValueError("no buckets")
+    for b in ordered:
+        if b >= length:
+            return b
+    raise ValueError(f"input of length {length} does not fit buckets {ordered}")
+
+
+def make_batch_chunk(arrays: dict, start: int, end: int, pad_to: int):
+    """main.swift:7-51: rows [start, end), padded to pad_to rows with copies
+    of the last valid row.  Returns (chunk, valid_count)."""
+    valid = end - start
+    if valid <= 0:
+        raise ValueError("empty chunk")
+    chunk = {k: np.asarray(v)[start:end] for k, v in arrays.items()}
+    if valid >= pad_to:
+        return chunk, valid
+    pad = pad_to - valid
+    return {k: np.concatenate([v, np.repeat(v[valid - 1:valid], pad, axis=0)], axis=0) for k, v in chunk.items()}, valid
+
+
+def group_by_shape(items, key=lambda x: x):
+    """RawCLI.swift:135-139: group requests by (L, Hh, O); insertion order."""
+    groups: dict = {}
+    for it in items:
+        groups.setdefault(key(it), []).append(it)
+    return groups

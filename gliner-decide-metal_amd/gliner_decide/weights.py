@@ -1,0 +1,60 @@
+"""`WeightStore` (Weights.swift:23-58) over the native store.
+
+Keys follow the fp16 checkpoint written by Tools/prepare_model.py:82-113
+(`encoder.*` and `classifier.*`).  The store copies host arrays; the
+classifier uploads them to HBM at construction.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+from . import _native as N
+
+_NP_TO_GD = {np.dtype(np.float16): N.GD_F16, np.dtype(np.float32): N.GD_F32, np.dtype(np.int32): N.GD_I32,
+             np.dtype(np.int64): N.GD_I64}
+
+
+class WeightStore:
+    def __init__(self, arrays: dict | None = None, url: str | Path | None = None):
+        self._lib = N.lib()
+        h = C.c_void_p()
+        N.check(self._lib.gd_weight_store_create(C.byref(h)))
+        self._h = h
+        if url is not None:
+            self.load_safetensors(url)
+        if arrays:
+            for k, v in arrays.items():
+                self.add(k, v)
+
+    def add(self, key: str, array) -> None:
+        a = np.ascontiguousarray(array)
+        if a.dtype not in _NP_TO_GD:
+            raise TypeError(f"{key}: unsupported dtype {a.dtype}")
+        shape = (C.c_int64 * max(a.ndim, 1))(*a.shape)
+        N.check(self._lib.gd_weight_store_add(self._h, key.encode(), a.ctypes.data_as(C.c_void_p),
+                                              _NP_TO_GD[a.dtype], shape, a.ndim))
+
+    def load_safetensors(self, path: str | Path) -> None:
+        N.check(self._lib.gd_weight_store_load_safetensors(self._h, str(path).encode()))
+
+    def __len__(self) -> int:
+        return int(self._lib.gd_weight_store_count(self._h))
+
+    @property
+    def handle(self) -> C.c_void_p:
+        return self._h
+
+    def close(self) -> None:
+        if self._h:
+            self._lib.gd_weight_store_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

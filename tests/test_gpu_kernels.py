@@ -1,0 +1,324 @@
+"""GPU parity of the standalone kernels against the oracle (through the C-ABI).
+
+Tolerances (fp16 outputs, fp32 arithmetic on the GPU vs float64 in the
+oracle with the same fp16 rounding points): an element may differ by at most
+one fp16 ulp of the expected value, because fp32 vs float64 accumulation can
+move a value across a rounding boundary; integer/index outputs are exact.
+Attention probabilities: |dP| <= 1e-3 absolute.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import deberta as O
+
+pytestmark = pytest.mark.gpu
+
+
+def fk():
+    from gliner_decide.fused_kernels import FusedKernels
+    return FusedKernels()
+
+
+def dev(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    return t.to(dtype) if dtype is not None else t
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def ulp16(x):
+    x = np.abs(np.asarray(x, np.float64))
+    x = np.maximum(x, 2.0 ** -14)
+    return 2.0 ** (np.floor(np.log2(x)) - 10)
+
+
+def assert_within_ulp(got, want, n_ulp=1.0, max_frac_off=None):
+    diff = np.abs(got - want)
+    bound = n_ulp * ulp16(want) + 1e-12
+    bad = diff > bound
+    assert not bad.any(), f"{bad.sum()} elements off by > {n_ulp} ulp; worst {diff.max():.3g}"
+    if max_frac_off is not None:
+        frac = np.mean(diff > 0)
+        assert frac <= max_frac_off, f"{frac:.2e} of elements differ"
+
+
+# ---------------------------------------------------------------------------
+# relative index table (DeBERTa.swift:498-551) -- exact
+# ---------------------------------------------------------------------------
+def test_relative_index_table_exact(golden):
+    table = golden("relative_bucket_256_512.npy")
+    got = fk().relative_index_table(512).cpu().numpy()
+    np.testing.assert_array_equal(got, np.clip(table + 256, 0, 511))
+    got32 = fk().relative_index_table(32).cpu().numpy()
+    np.testing.assert_array_equal(got32, np.clip(O.relative_bucket(np.arange(-31, 32)) + 256, 0, 511))
+
+
+# ---------------------------------------------------------------------------
+# residual LayerNorm (FusedKernels.swift:125-155, DeBERTa.swift:463)
+# ---------------------------------------------------------------------------
+def test_layer_norm_known_answer(golden):
+    g = golden("ln_known_answer.npz")
+    x = dev(g["x"].reshape(1, 1024))
+    ones = torch.ones(1024, dtype=torch.float16, device="cuda")
+    zeros = torch.zeros(1024, dtype=torch.float16, device="cuda")
+    out = host(fk().residual_layer_norm(x, torch.zeros_like(x), ones, zeros, 1e-7))
+    np.testing.assert_array_equal(out[0], g["expected"].astype(np.float16).astype(np.float64))
+
+
+@pytest.mark.parametrize("round_sum", [False, True])
+def test_residual_ln_full_size(round_sum):
+    from gliner_decide.synthetic import residual_ln_inputs
+    d = residual_ln_inputs(seed=2)
+    args = [dev(d[k]) for k in ("x", "residual", "gamma", "beta")]
+    out = host(fk().residual_layer_norm(*args, 1e-7, round_sum_f16=round_sum))
+    ref_fn = O.residual_layer_norm_default if round_sum else O.residual_layer_norm_kernel
+    want = ref_fn(d["x"], d["residual"], d["gamma"], d["beta"], 1e-7)
+    assert_within_ulp(out, want, 1.0, max_frac_off=1e-3)
+
+
+@pytest.mark.parametrize("rows,cols", [(0, 1024), (1, 1024), (7, 512), (5, 2048), (3, 72), (9, 8), (33, 1000)])
+def test_residual_ln_shapes(rows, cols):
+    r = np.random.default_rng(rows * 7 + cols)
+    x = r.standard_normal((rows, cols)).astype(np.float16)
+    res = r.standard_normal((rows, cols)).astype(np.float16)
+    g = (1 + 0.1 * r.standard_normal(cols)).astype(np.float16)
+    b = (0.1 * r.standard_normal(cols)).astype(np.float16)
+    out = host(fk().residual_layer_norm(dev(x), dev(res), dev(g), dev(b), 1e-7))
+    assert_within_ulp(out, O.residual_layer_norm_kernel(x, res, g, b, 1e-7), 1.0)
+    plain = host(fk().residual_layer_norm(dev(x), None, dev(g), dev(b), 1e-7))
+    assert_within_ulp(plain, O.layer_norm(x, g, b, 1e-7), 1.0)
+
+
+def test_residual_ln_in_place():
+    """out aliasing residual (how the encoder updates its hidden state)."""
+    from gliner_decide import _native as N
+    from gliner_decide.device import stream_handle
+    r = np.random.default_rng(1)
+    x = r.standard_normal((64, 1024)).astype(np.float16)
+    res = r.standard_normal((64, 1024)).astype(np.float16)
+    g = np.ones(1024, np.float16)
+    b = np.zeros(1024, np.float16)
+    tx, tr, tg, tb = dev(x), dev(res), dev(g), dev(b)
+    N.check(N.lib().gd_residual_layer_norm(tx.data_ptr(), tr.data_ptr(), tg.data_ptr(), tb.data_ptr(), tr.data_ptr(),
+                                           64, 1024, 1e-7, N.GD_LN_SUM_F16, stream_handle()))
+    assert_within_ulp(host(tr), O.residual_layer_norm_default(x, res, g, b, 1e-7), 1.0)
+
+
+# ---------------------------------------------------------------------------
+# embedding (DeBERTa.swift:285-292)
+# ---------------------------------------------------------------------------
+def test_embedding_layer_norm():
+    r = np.random.default_rng(4)
+    V, C, B, L = 3000, 1024, 3, 48
+    table = (0.02 * r.standard_normal((V, C))).astype(np.float16)
+    g = (1 + 0.02 * r.standard_normal(C)).astype(np.float16)
+    b = (0.02 * r.standard_normal(C)).astype(np.float16)
+    ids = r.integers(0, V, size=(B, L)).astype(np.int32)
+    mask = np.ones((B, L), np.float16)
+    mask[1, 30:] = 0
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    out = host(fk().embedding_layer_norm(dev(ids), dev(mask), dev(table), dev(g), dev(b), 1e-7, flag))
+    assert_within_ulp(out, O.embedding(ids, mask, table, g, b, 1e-7), 1.0)
+    assert int(flag.item()) == 0
+    ids[0, 0] = V + 5  # out of range: reads row 0 and raises the flag
+    out = host(fk().embedding_layer_norm(dev(ids), dev(mask), dev(table), dev(g), dev(b), 1e-7, flag))
+    assert int(flag.item()) == 1
+    ids[0, 0] = 0
+    assert_within_ulp(out, O.embedding(ids, mask, table, g, b, 1e-7), 1.0)
+
+
+# ---------------------------------------------------------------------------
+# linear (DeBERTa.swift:60-92, 421, 437)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("m,n,k", [(1, 128, 64), (65, 256, 128), (300, 1024, 1024), (1000, 384, 192),
+                                   (4096, 1024, 256), (8192, 3072, 1024)])
+@pytest.mark.parametrize("epi", ["bias", "gelu", "relu", "none"])
+def test_linear(m, n, k, epi):
+    if m * n * k > 2 ** 31 and epi != "bias":
+        pytest.skip("large shape checked with the bias epilogue only")
+    r = np.random.default_rng(m + n + k)
+    x = r.standard_normal((m, k)).astype(np.float16)
+    w = (r.standard_normal((n, k)) / np.sqrt(k)).astype(np.float16)
+    b = r.standard_normal(n).astype(np.float16)
+    out = host(fk().linear(dev(x), dev(w), dev(b) if epi != "none" else None, epilogue=epi))
+    y = x.astype(np.float64) @ w.astype(np.float64).T
+    if epi == "none":
+        want = O.f16(y)
+    else:
+        want = O.f16(y + b)
+        if epi == "gelu":
+            want = O.gelu(want)
+        elif epi == "relu":
+            want = np.maximum(want, 0)
+    # fp32 accumulation order differs from float64: allow 2 ulp before GELU's rounding
+    assert_within_ulp(out, want, 2.0 if epi == "gelu" else 1.0, max_frac_off=5e-3)
+
+
+def test_linear_row_gather():
+    r = np.random.default_rng(8)
+    x = r.standard_normal((500, 1024)).astype(np.float16)
+    w = (r.standard_normal((2048, 1024)) / 32).astype(np.float16)
+    b = r.standard_normal(2048).astype(np.float16)
+    rows = r.integers(0, 500, size=77).astype(np.int32)
+    out = host(fk().linear(dev(x), dev(w), dev(b), epilogue="relu", rows=dev(rows)))
+    want = np.maximum(O.f16(x[rows].astype(np.float64) @ w.astype(np.float64).T + b), 0)
+    assert_within_ulp(out, want, 1.0, max_frac_off=5e-3)
+
+
+# ---------------------------------------------------------------------------
+# fused relative bias + masked softmax (+ P.V) -- DeBERTa.swift:322-395
+# ---------------------------------------------------------------------------
+def _attn_case(seed, B, H, L, min_len=None):
+    r = np.random.default_rng(seed)
+    D, P = 64, 512
+    q = r.standard_normal((B, H, L, D)).astype(np.float16)
+    k = r.standard_normal((B, H, L, D)).astype(np.float16)
+    v = r.standard_normal((B, H, L, D)).astype(np.float16)
+    pk = r.standard_normal((P, H * D)).astype(np.float16)  # [P, H*D] as the projection writes it
+    pq = r.standard_normal((P, H * D)).astype(np.float16)
+    lengths = r.integers(min_len or max(1, L // 2), L + 1, size=B)
+    lengths[0] = L
+    mask = (np.arange(L)[None, :] < lengths[:, None]).astype(np.float16)
+    return q, k, v, pk, pq, mask
+
+
+def _tables(pk, pq, H):
+    P = pk.shape[0]
+    return pk.reshape(P, H, 64).transpose(1, 0, 2), pq.reshape(P, H, 64).transpose(1, 0, 2)
+
+
+def _oracle_probs(q, k, pk, pq, mask):
+    H, L = q.shape[1], q.shape[2]
+    pkh, pqh = _tables(pk, pq, H)
+    c2p, p2c = O.relative_indices(L)
+    bias = O.relative_bias_default(q, k, pkh, pqh, c2p, p2c, 64)
+    return bias, O.attention_probs_default(q, k, bias, mask, 64)
+
+
+def _gpu_tables(pk, pq, H):
+    tpk, tpq = dev(pk), dev(pq)
+    P = pk.shape[0]
+    return tpk.view(P, H, 64).permute(1, 0, 2), tpq.view(P, H, 64).permute(1, 0, 2)
+
+
+@pytest.mark.parametrize("L", [16, 32, 48, 96, 128, 160, 256, 512])
+def test_attention_probs_and_bias(L):
+    B, H = 2, 3
+    q, k, v, pk, pq, mask = _attn_case(L, B, H, L)
+    gpk, gpq = _gpu_tables(pk, pq, H)
+    bias, probs = _oracle_probs(q, k, pk, pq, mask)
+    got = host(fk().deberta_attention(dev(q), dev(k), None, gpk, gpq, dev(mask), output="probs"))
+    assert np.max(np.abs(got - probs)) <= 1e-3
+    valid = mask[:, None, None, :] > 0
+    assert np.all(got[~np.broadcast_to(valid, got.shape)] == 0)  # masked keys get exactly 0
+    np.testing.assert_allclose(got.sum(-1), 1.0, atol=3e-3)
+    gb = host(fk().deberta_attention(dev(q), dev(k), None, gpk, gpq, dev(mask), output="bias"))
+    want_b = O.f16(bias + O.additive_key_mask(mask))
+    fin = np.isfinite(want_b)
+    np.testing.assert_array_equal(np.isfinite(gb), fin)
+    assert_within_ulp(gb[fin], want_b[fin], 2.0, max_frac_off=2e-2)
+
+
+@pytest.mark.parametrize("L", [32, 96, 256, 512])
+def test_attention_context(L):
+    B, H = 2, 2
+    q, k, v, pk, pq, mask = _attn_case(100 + L, B, H, L)
+    gpk, gpq = _gpu_tables(pk, pq, H)
+    pkh, pqh = _tables(pk, pq, H)
+    c2p, p2c = O.relative_indices(L)
+    bias = O.relative_bias_default(q, k, pkh, pqh, c2p, p2c, 64)
+    want = O.attention_default(q, k, v, bias, mask, 64)
+    got = host(fk().deberta_attention(dev(q), dev(k), dev(v), gpk, gpq, dev(mask), output="context"))
+    assert got.shape == (B, L, H * 64)
+    assert np.max(np.abs(got - want)) <= 4e-3, np.max(np.abs(got - want))
+
+
+def test_attention_strided_fused_projection_layout():
+    """Q, K, V as views of one [B, L, 3, H, D] projection (the encoder's layout)."""
+    B, H, L = 2, 4, 128
+    r = np.random.default_rng(21)
+    qkv = r.standard_normal((B, L, 3, H, 64)).astype(np.float16)
+    pk = r.standard_normal((512, H * 64)).astype(np.float16)
+    pq = r.standard_normal((512, H * 64)).astype(np.float16)
+    mask = np.ones((B, L), np.float16)
+    mask[1, 100:] = 0
+    t = dev(qkv)
+    q, k, v = (t[:, :, i].permute(0, 2, 1, 3) for i in range(3))
+    gpk, gpq = _gpu_tables(pk, pq, H)
+    got = host(fk().deberta_attention(q, k, v, gpk, gpq, dev(mask), output="context"))
+    qn, kn, vn = (np.ascontiguousarray(qkv[:, :, i].transpose(0, 2, 1, 3)) for i in range(3))
+    want = host(fk().deberta_attention(dev(qn), dev(kn), dev(vn), gpk, gpq, dev(mask), output="context"))
+    np.testing.assert_array_equal(got, want)
+
+
+def test_attention_full_size_relbias_workload():
+    """B=32, H=16, L=256 with lengths in [16, 256]: size-independent
+    properties on the whole output, oracle parity on sampled (b, h) slices."""
+    from gliner_decide.synthetic import relbias_inputs
+    d = relbias_inputs(seed=3)
+    H = 16
+    gpk, gpq = _gpu_tables(d["pos_key"], d["pos_query"], H)
+    got_t = fk().deberta_attention(dev(d["q"]), dev(d["k"]), None, gpk, gpq, dev(d["mask"]), output="probs")
+    got = host(got_t)
+    valid = d["mask"][:, None, None, :] > 0
+    assert np.all(got[~np.broadcast_to(valid, got.shape)] == 0)
+    np.testing.assert_allclose(got.sum(-1), 1.0, atol=3e-3)
+    for b, h in [(0, 0), (5, 7), (17, 15), (31, 3)]:
+        _, probs = _oracle_probs(d["q"][b:b + 1, h:h + 1], d["k"][b:b + 1, h:h + 1],
+                                 d["pos_key"].reshape(512, H, 64)[:, h], d["pos_query"].reshape(512, H, 64)[:, h],
+                                 d["mask"][b:b + 1])
+        assert np.max(np.abs(got[b, h] - probs[0, 0])) <= 1e-3, (b, h)
+
+
+def test_attention_rejects_bad_shapes():
+    from gliner_decide import GlinerDecideError
+    q = torch.zeros((1, 1, 40, 64), dtype=torch.float16, device="cuda")
+    t = torch.zeros((1, 512, 64), dtype=torch.float16, device="cuda")
+    m = torch.ones((1, 40), dtype=torch.float16, device="cuda")
+    with pytest.raises(GlinerDecideError):
+        fk().deberta_attention(q, q, q, t, t, m)  # L = 40 is not a multiple of 16
+
+
+# ---------------------------------------------------------------------------
+# FusedKernels general-index API (FusedKernels.swift:83-123, 13-81)
+# ---------------------------------------------------------------------------
+def test_relative_bias_known_answer(golden):
+    g = golden("relbias_known_answer.npz")
+    out = host(fk().relative_bias(dev(g["q"], torch.float16), dev(g["k"], torch.float16),
+                                  dev(g["pos_key"], torch.float16), dev(g["pos_query"], torch.float16),
+                                  dev(g["c2p"]), dev(g["p2c"]), dev(g["key_mask"], torch.float16),
+                                  float(g["scale"]), 1, 2, 8, 4, 8))
+    assert_within_ulp(out, g["kernel"].astype(np.float16).astype(np.float64), 1.0)
+
+
+def test_fused_attention_known_answer(golden):
+    g = golden("relbias_known_answer.npz")
+    out = host(fk().fused_attention(dev(g["q"], torch.float16), dev(g["k"], torch.float16),
+                                    dev(g["v"], torch.float16), dev(g["pos_key"], torch.float16),
+                                    dev(g["pos_query"], torch.float16), dev(g["c2p"]), dev(g["p2c"]),
+                                    dev(g["key_mask"], torch.float16), float(g["scale"]), 1, 2, 8, 4, 8))
+    assert_within_ulp(out, g["fused"].astype(np.float16).astype(np.float64), 1.0)
+
+
+def test_general_index_kernels_vs_oracle_closed_form():
+    B, H, L = 2, 2, 64
+    q, k, v, pk, pq, mask = _attn_case(55, B, H, L)
+    pkh, pqh = _tables(pk, pq, H)
+    c2p, p2c = O.relative_indices(L)
+    key_mask = np.where(mask > 0, 0.0, -65504.0).astype(np.float16)
+    scale = O.scale_f32(64)
+    want = O.relative_bias_kernel(q, k, pkh, pqh, c2p, p2c, key_mask, scale)
+    got = host(fk().relative_bias(dev(q), dev(k), dev(np.ascontiguousarray(pkh)), dev(np.ascontiguousarray(pqh)),
+                                  dev(c2p.astype(np.int32)), dev(p2c.astype(np.int32)), dev(key_mask), scale, B, H, L,
+                                  64, 512))
+    assert_within_ulp(got, want, 1.0)
+    want = O.fused_attention_kernel(q, k, v, pkh, pqh, c2p, p2c, key_mask, scale)
+    got = host(fk().fused_attention(dev(q), dev(k), dev(v), dev(np.ascontiguousarray(pkh)),
+                                    dev(np.ascontiguousarray(pqh)), dev(c2p.astype(np.int32)),
+                                    dev(p2c.astype(np.int32)), dev(key_mask), scale, B, H, L, 64, 512))
+    assert np.max(np.abs(got - want)) <= 2e-3

@@ -1,0 +1,95 @@
+"""Host-side logic of the package (no GPU): decode, buckets, batch chunking,
+configuration and the synthetic workloads."""
+
+import math
+
+import numpy as np
+import pytest
+
+from gliner_decide import DeBERTaV2Configuration, DecisionTask, decode, make_batch_chunk, select_bucket
+from gliner_decide import synthetic as S
+from oracle import deberta as O
+
+
+def test_configuration_default():
+    c = DeBERTaV2Configuration.default()
+    assert (c.hidden_size, c.intermediate_size, c.num_hidden_layers, c.num_attention_heads, c.head_size) == (
+        1024, 4096, 24, 16, 64)
+    assert c.layer_norm_eps == 1e-7 and c.position_buckets == 256 and c.hidden_act == "gelu"
+
+
+def test_decode_matches_oracle_and_rules():
+    r = np.random.default_rng(0)
+    logits = r.standard_normal((4, 2, 6)).astype(np.float32)
+    tasks = [DecisionTask("a", tuple("uvwxyz"), False), DecisionTask("b", tuple("pqrs"), True)]
+    for row in range(4):
+        got = decode(logits, row, tasks)
+        want = O.decode(logits[row], [(6, False), (4, True)])
+        for p, (sel, probs) in zip(got, want):
+            np.testing.assert_allclose(p.probabilities, probs, rtol=1e-12)
+            assert len(p.labels) == len(sel)
+    # multi-label: nothing >= 0.5 -> argmax fallback; ties -> first
+    out = decode(np.array([[[-3.0, -1.0, -2.0]]]), 0, [DecisionTask("t", ("a", "b", "c"), True)])
+    assert out[0].labels == ["b"]
+    out = decode(np.array([[[1.0, 1.0]]]), 0, [DecisionTask("t", ("a", "b"), False)])
+    assert out[0].labels == ["a"] and math.isclose(out[0].probabilities[0], 0.5)
+
+
+def test_buckets_and_chunks():
+    assert [select_bucket(n) for n in (1, 32, 33, 64, 65, 96, 97, 128, 129, 256, 257, 512)] == [
+        32, 32, 64, 64, 96, 96, 128, 128, 256, 256, 512, 512]
+    assert select_bucket(40, buckets=[256, 64, 64]) == 64
+    with pytest.raises(ValueError):
+        select_bucket(600)
+    arrays = {"x": np.arange(12).reshape(6, 2)}
+    chunk, valid = make_batch_chunk(arrays, 4, 6, 5)
+    assert valid == 2 and chunk["x"].shape == (5, 2) and (chunk["x"][2:] == [10, 11]).all()
+    chunk, valid = make_batch_chunk(arrays, 0, 4, 4)
+    assert valid == 4 and chunk["x"].shape == (4, 2)
+
+
+def test_synthetic_weights_are_subset_stable():
+    cfg = DeBERTaV2Configuration(hidden_size=128, intermediate_size=256, num_hidden_layers=3, num_attention_heads=2,
+                                 vocab_size=64, classifier_hidden=128)
+    full = S.synthetic_weights(cfg, seed=3)
+    one = S.synthetic_weights(cfg, seed=3, layers=[1])
+    for k, v in one.items():
+        np.testing.assert_array_equal(v, full[k])
+    g = full["encoder.encoder.layer.0.output.LayerNorm.weight"].astype(np.float64)
+    assert abs(g.mean() - 1) < 0.01 and 0.01 < g.std() < 0.03
+    assert all(v.dtype == np.float16 for v in full.values())
+
+
+def test_classification_workload_layout():
+    b = S.classification_batch(seed=4)
+    assert b.shape == (32, 256, 1, 5)
+    lengths = b.attention_mask.sum(1)
+    assert lengths.min() >= 40 and lengths.max() <= 256
+    assert (b.input_ids[:, 0] == S.CLS_ID).all()
+    assert (b.input_ids[np.arange(32), lengths.astype(int) - 1] == S.SEP_ID).all()
+    assert (b.input_ids[:, 1:6] == S.LABEL_MARKER_ID).all()
+    assert (b.input_ids[b.attention_mask == 0] == 0).all()
+
+
+def test_long_context_workload_layout():
+    b = S.long_context_batch(seed=6)
+    assert b.shape == (64, 512, 3, 20) and (b.attention_mask == 1).all()
+    assert b.marker_mask[:, 2].sum(1).tolist() == [8] * 64
+    for row in range(64):
+        for h in range(3):
+            pos = b.marker_indices[row, h][b.marker_mask[row, h] > 0]
+            assert (b.input_ids[row, pos] == S.LABEL_MARKER_ID).all()
+
+
+def test_bucket_mix_workload():
+    batches = S.bucket_mix(seed=5)
+    assert sum(x.valid_rows for x in batches) == 4096
+    for x in batches:
+        B, L, Hh, O_ = x.shape
+        assert B == 32 and L in (32, 64, 96, 128, 256, 512) and Hh <= 2 and O_ <= 10
+        lengths = x.attention_mask.sum(1)
+        assert lengths.max() <= L and (L == 32 or lengths[:x.valid_rows].max() > {64: 32, 96: 64, 128: 96, 256: 128,
+                                                                                  512: 256}[L])
+        # padded rows copy the last valid row (main.swift:22-49)
+        if x.valid_rows < 32:
+            assert (x.input_ids[x.valid_rows:] == x.input_ids[x.valid_rows - 1]).all()

@@ -1,0 +1,313 @@
+"""Pins the CPU oracle (oracle/deberta.py) before it is trusted as the checker.
+
+Each oracle function is checked against something it does not share code
+with: the golden fixtures (HF transformers DeBERTa-v2, brute-force loops over
+the reference's known-answer generators, closed forms), torch routines, and
+invariants of the mathematics.  A planted-mistake test at the end confirms
+the checks would catch a transposed p2c index or a dropped bias term.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import deberta as O
+
+
+# ---------------------------------------------------------------------------
+# Config -- ConfigurationTests.swift:4-11
+# ---------------------------------------------------------------------------
+def test_config_matches_checkpoint():
+    c = O.Config()
+    assert (c.hidden_size, c.intermediate_size, c.num_hidden_layers, c.num_attention_heads, c.head_size) == (
+        1024, 4096, 24, 16, 64)
+    assert c.layer_norm_eps == 1e-7 and c.position_buckets == 256 and c.max_relative_positions == -1
+
+
+# ---------------------------------------------------------------------------
+# Log buckets -- DeBERTa.swift:521-551
+# ---------------------------------------------------------------------------
+def test_bucket_matches_hf_table(golden):
+    table = golden("relative_bucket_256_512.npy")
+    r = np.arange(-511, 512)
+    np.testing.assert_array_equal(O.relative_bucket(r), table)
+
+
+def test_bucket_invariants():
+    r = np.arange(-511, 512)
+    b = O.relative_bucket(r)
+    np.testing.assert_array_equal(b, -b[::-1])  # odd
+    lin = np.abs(r) <= 128
+    np.testing.assert_array_equal(b[lin], r[lin])  # identity near zero
+    assert np.all(np.diff(b) >= 0) and b.min() == -255 and b.max() == 255
+    # log zone: consecutive integers (no gaps), so c2p windows are contiguous
+    assert set(np.unique(b[r > 128])) == set(range(129, 256))
+    for L, distinct in [(32, 63), (64, 127), (96, 191), (128, 255), (256, 385), (512, 511)]:
+        assert len(np.unique(O.relative_positions(L))) == distinct
+
+
+def test_bucket_scalar_brute_force():
+    """Element-wise evaluation with Python's math module (a separate code
+    path from the vectorised numpy one)."""
+    mid, mp = 128, 512
+    for r in range(-511, 512):
+        a = mid - 1 if -mid < r < mid else abs(r)
+        if a <= mid:
+            want = r
+        else:
+            lp = math.ceil(math.log(a / mid) / math.log((mp - 1) / mid) * (mid - 1)) + mid
+            want = lp if r > 0 else -lp
+        assert O.relative_bucket(r) == want
+
+
+def test_relative_indices_transpose_semantics():
+    for L in (32, 96, 256, 512):
+        c2p, p2c = O.relative_indices(L)
+        # p2c[k, q] == c2p[q, k] because the bucket is odd (DeBERTa.swift:511 identity transpose)
+        np.testing.assert_array_equal(p2c.T, c2p)
+        assert c2p.min() >= 0 and c2p.max() <= 511
+    c2p, _ = O.relative_indices(256)
+    assert c2p.min() == 64 and c2p.max() == 448
+
+
+# ---------------------------------------------------------------------------
+# LayerNorm -- main.swift:194-225 known answer, torch
+# ---------------------------------------------------------------------------
+def test_layer_norm_known_answer(golden):
+    g = golden("ln_known_answer.npz")
+    ones, zeros = np.ones(1024), np.zeros(1024)
+    got = O.layer_norm(g["x"].astype(np.float64), ones, zeros, 1e-7, round16=False)
+    np.testing.assert_allclose(got, g["expected"], rtol=0, atol=1e-12)
+    got16 = O.residual_layer_norm_kernel(g["x"], np.zeros(1024, np.float16), ones, zeros, 1e-7)
+    np.testing.assert_array_equal(got16, g["expected"].astype(np.float16).astype(np.float64))
+
+
+def test_layer_norm_vs_torch():
+    r = np.random.default_rng(0)
+    x = r.standard_normal((64, 1024)) * 3 + 1
+    g = 1 + 0.1 * r.standard_normal(1024)
+    b = 0.1 * r.standard_normal(1024)
+    want = torch.nn.functional.layer_norm(torch.from_numpy(x), (1024,), torch.from_numpy(g), torch.from_numpy(b),
+                                          1e-7).numpy()
+    np.testing.assert_allclose(O.layer_norm(x, g, b, 1e-7, round16=False), want, atol=1e-12)
+
+
+def test_residual_ln_default_rounds_sum():
+    # 1 + 2^-11 is not representable in fp16: the default path (DeBERTa.swift:463)
+    # rounds it to 1 before the norm, the Metal kernel keeps it.
+    x = np.full((1, 8), 1.0)
+    x[0, 1] = 3.0
+    res = np.zeros((1, 8))
+    res[0, 0] = 2.0 ** -11
+    g, b = np.ones(8), np.zeros(8)
+    d = O.residual_layer_norm_default(x, res, g, b, 1e-7)
+    k = O.residual_layer_norm_kernel(x, res, g, b, 1e-7)
+    np.testing.assert_array_equal(d, O.layer_norm(np.where(res > 0, 1.0, x), g, b, 1e-7))
+    exact = torch.nn.functional.layer_norm(torch.from_numpy(x + res), (8,), eps=1e-7).numpy()
+    np.testing.assert_array_equal(k, exact.astype(np.float16).astype(np.float64))
+    assert not np.array_equal(d, k)
+
+
+def test_gelu_vs_torch():
+    x = np.linspace(-6, 6, 10001)
+    want = torch.nn.functional.gelu(torch.from_numpy(x), approximate="none").numpy()
+    np.testing.assert_allclose(O.gelu(x, round16=False), want, atol=1e-12)
+    np.testing.assert_allclose(O.gelu(x[:100], round16=False), want[:100], atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# Relative bias -- FusedKernels.swift:83-123 (main.swift:141-192 generators)
+# ---------------------------------------------------------------------------
+def test_relative_bias_kernel_known_answer(golden):
+    g = golden("relbias_known_answer.npz")
+    got = O.relative_bias_kernel(g["q"], g["k"], g["pos_key"], g["pos_query"], g["c2p"], g["p2c"], g["key_mask"],
+                                 float(g["scale"]))
+    np.testing.assert_array_equal(got, g["kernel"].astype(np.float16).astype(np.float64))
+
+
+def test_relative_bias_default_general_indices_known_answer(golden):
+    g = golden("relbias_known_answer.npz")
+    # default-graph semantics with the test's general indices, per head
+    q, k = g["q"], g["k"]
+    out = np.zeros_like(g["graph"])
+    for h in range(2):
+        bias = O.relative_bias_default(q[:, h:h + 1], k[:, h:h + 1], g["pos_key"][h:h + 1], g["pos_query"][h:h + 1],
+                                       g["c2p"][h], g["p2c"][h], head_size=4)
+        out[:, h] = bias[:, 0]
+    valid = g["key_mask"][0] > -60000
+    np.testing.assert_array_equal(out[..., valid], g["graph"][..., valid])
+
+
+def test_fused_attention_kernel_known_answer(golden):
+    g = golden("relbias_known_answer.npz")
+    got = O.fused_attention_kernel(g["q"], g["k"], g["v"], g["pos_key"], g["pos_query"], g["c2p"], g["p2c"],
+                                   g["key_mask"], float(g["scale"]))
+    np.testing.assert_array_equal(got, g["fused"].astype(np.float16).astype(np.float64))
+
+
+def test_relative_bias_default_brute_force():
+    """Closed-form indices, random inputs: every element recomputed with
+    scalar loops and explicit fp16 rounding."""
+    r = np.random.default_rng(3)
+    B, H, L, D, P = 1, 2, 24, 8, 512
+    q = r.standard_normal((B, H, L, D)).astype(np.float16)
+    k = r.standard_normal((B, H, L, D)).astype(np.float16)
+    pk = r.standard_normal((H, P, D)).astype(np.float16)
+    pq = r.standard_normal((H, P, D)).astype(np.float16)
+    c2p, p2c = O.relative_indices(L)
+    got = O.relative_bias_default(q, k, pk, pq, c2p, p2c, head_size=D)
+    s16 = float(np.float16(math.sqrt(3 * D)))
+    for h in range(H):
+        for i in range(L):
+            for j in range(L):
+                idx = int(np.clip(O.relative_bucket(i - j) + 256, 0, 511))
+                a = float(np.float16(np.dot(q[0, h, i].astype(np.float64), pk[h, idx].astype(np.float64))))
+                c = float(np.float16(np.dot(k[0, h, j].astype(np.float64), pq[h, idx].astype(np.float64))))
+                want = float(np.float16(float(np.float16(a + c)) / s16))
+                assert got[0, h, i, j] == want
+
+
+# ---------------------------------------------------------------------------
+# Attention -- torch SDPA
+# ---------------------------------------------------------------------------
+def test_attention_vs_torch_sdpa():
+    r = np.random.default_rng(5)
+    B, H, L, D = 2, 3, 40, 64
+    q, k, v = (r.standard_normal((B, H, L, D)) for _ in range(3))
+    bias = r.standard_normal((B, H, L, L))
+    mask = np.ones((B, L))
+    mask[1, 25:] = 0
+    got = O.attention_default(q, k, v, bias, mask, D, round16=False)
+    add = np.where(mask[:, None, None, :] > 0, 0.0, -np.inf)
+    want = torch.nn.functional.scaled_dot_product_attention(
+        torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v),
+        attn_mask=torch.from_numpy(bias + add), scale=O.scale_f32(D)).numpy()
+    want = np.transpose(want, (0, 2, 1, 3)).reshape(B, L, H * D)
+    np.testing.assert_allclose(got, want, atol=1e-6)  # the fp16 add of a -65504 mask vs -inf: identical probs
+
+
+# ---------------------------------------------------------------------------
+# Whole layers -- HF transformers DeBERTa-v2 (float64, same fp16 weights)
+# ---------------------------------------------------------------------------
+def _oracle_for(cfg_kwargs, seed):
+    import sys
+    from pathlib import Path
+    sys.path.insert(0, str(Path(__file__).resolve().parents[1] / "gliner-decide-metal_amd"))
+    from gliner_decide.config import DeBERTaV2Configuration
+    from gliner_decide.synthetic import synthetic_weights
+    pc = DeBERTaV2Configuration(**cfg_kwargs)
+    w = synthetic_weights(pc, seed=seed)
+    oc = O.Config(**{k: getattr(pc, k) for k in O.Config.__dataclass_fields__})
+    hf_scale = float(np.float32(math.sqrt(3 * oc.head_size)))
+    return O.OracleModel(O.ModelWeights.from_store(w, oc), oc, round16=False, bias_scale=hf_scale), oc
+
+
+def test_layer_matches_hf_full_width(golden):
+    g = golden("hf_layer_c1024_l32.npz")
+    m, _ = _oracle_for(dict(num_hidden_layers=1, vocab_size=2048), seed=1)
+    emb = m.embed(g["ids"], g["mask"])
+    np.testing.assert_allclose(emb, g["embed"], atol=2e-6)  # fixture stored as fp32
+    out = m.encode(g["ids"], g["mask"])
+    np.testing.assert_allclose(out, g["out"], atol=2e-5)
+
+
+def test_encoder_matches_hf_log_buckets_valid_rows(golden):
+    """L = 256 exercises the log-bucket zone; row 1 is padded (keys masked by
+    both; HF also masks padded queries, so only valid rows are compared)."""
+    g = golden("hf_encoder_c128_l256.npz")
+    m, _ = _oracle_for(dict(hidden_size=128, intermediate_size=256, num_hidden_layers=2, num_attention_heads=2,
+                            vocab_size=512, classifier_hidden=256), seed=7)
+    out = m.encode(g["ids"], g["mask"])
+    for b, n in enumerate(g["lengths"]):
+        np.testing.assert_allclose(out[b, :n], g["out"][b, :n], atol=2e-5)
+
+
+def test_reference_rounding_stays_near_exact(golden):
+    """The fp16-rounding oracle (the one the GPU is compared with) stays
+    within fp16 noise of the exact computation on the full-width layer."""
+    g = golden("hf_layer_c1024_l32.npz")
+    m16, _ = _oracle_for(dict(num_hidden_layers=1, vocab_size=2048), seed=1)
+    m16.round16 = True
+    m16.bias_scale = None
+    m16.tables = O.relative_tables(m16.w, m16.config, True)
+    out16 = m16.encode(g["ids"], g["mask"])
+    assert np.max(np.abs(out16 - g["out"])) < 0.05
+
+
+# ---------------------------------------------------------------------------
+# Classifier head, decode, chunking
+# ---------------------------------------------------------------------------
+def test_classifier_head_brute_force():
+    r = np.random.default_rng(9)
+    B, L, C, CH = 2, 16, 32, 24
+    hidden = r.standard_normal((B, L, C))
+    w = O.ModelWeights(None, None, None, None, None, None, [],
+                       cls0_w=r.standard_normal((CH, C)) * 0.2, cls0_b=r.standard_normal(CH) * 0.2,
+                       cls2_w=r.standard_normal((1, CH)) * 0.2, cls2_b=r.standard_normal(1) * 0.2)
+    mi = np.array([[[1, 2, 3], [4, 0, 0]], [[5, 6, 7], [8, 9, 0]]])
+    mm = np.array([[[1, 1, 1], [1, 0, 0]], [[1, 1, 1], [1, 1, 0]]], np.float32)
+    got = O.classifier_head(hidden, mi, mm, w, round16=False)
+    for b in range(B):
+        for h in range(2):
+            for o in range(3):
+                if mm[b, h, o] == 0:
+                    assert got[b, h, o] == -10000.0
+                    continue
+                x = hidden[b, mi[b, h, o]]
+                z = np.maximum(w.cls0_w @ x + w.cls0_b, 0)
+                assert abs(got[b, h, o] - (w.cls2_w[0] @ z + w.cls2_b[0])) < 1e-9
+
+
+def test_decode_cases():
+    logits = np.array([[[2.0, 1.0, 0.0], [0.1, -3.0, 5.0]]])
+    (sel0, p0), (sel1, p1) = O.decode(logits[0], [(3, False), (3, True)])
+    assert sel0 == [0]
+    np.testing.assert_allclose(p0, np.exp([2, 1, 0]) / np.exp([2, 1, 0]).sum())
+    assert sel1 == [0, 2]  # sigmoid(0.1) = 0.525 >= 0.5, sigmoid(5) >= 0.5
+    (sel2, _), = O.decode(np.array([[-1.0, -2.0, -0.5]]), [(3, True)])
+    assert sel2 == [2]  # none >= 0.5 -> argmax fallback
+    (sel3, _), = O.decode(np.array([[1.0, 1.0]]), [(2, False)])
+    assert sel3 == [0]  # first of equal maxima
+
+
+def test_bucket_and_chunk_rules():
+    assert O.select_bucket(1) == 32 and O.select_bucket(32) == 32 and O.select_bucket(33) == 64
+    assert O.select_bucket(97) == 128 and O.select_bucket(512) == 512
+    with pytest.raises(ValueError):
+        O.select_bucket(513)
+    arrays = {"a": np.arange(10).reshape(5, 2)}
+    chunk, valid = O.make_batch_chunk(arrays, 3, 5, 4)
+    assert valid == 2
+    np.testing.assert_array_equal(chunk["a"], [[6, 7], [8, 9], [8, 9], [8, 9]])
+
+
+# ---------------------------------------------------------------------------
+# The checks above catch plausible mistakes (planted in the oracle, on CPU)
+# ---------------------------------------------------------------------------
+def test_planted_mistakes_are_caught(golden, monkeypatch):
+    g = golden("hf_layer_c1024_l32.npz")
+    m, _ = _oracle_for(dict(num_hidden_layers=1, vocab_size=2048), seed=1)
+    good = m.encode(g["ids"], g["mask"])
+    assert np.max(np.abs(good - g["out"])) < 2e-5
+
+    real = O.relative_indices
+
+    def mirrored(L, bucket_size=256):  # misreading MLX transposed(0,1) as a swap
+        c2p, p2c = real(L, bucket_size)
+        return c2p, p2c.T.copy() * 0 + (511 - c2p.T + 1).clip(0, 511)
+
+    monkeypatch.setattr(O, "relative_indices", mirrored)
+    bad = m.encode(g["ids"], g["mask"])
+    assert np.max(np.abs(bad - g["out"])) > 1e-3
+    monkeypatch.setattr(O, "relative_indices", real)
+
+    real_bias = O.relative_bias_default
+
+    def no_p2c(q, k, pk, pq, c2p, p2c, head_size, round16=True, dtype=np.float64, bias_scale=None):
+        return real_bias(q, k * 0, pk, pq, c2p, p2c, head_size, round16, dtype, bias_scale)
+
+    monkeypatch.setattr(O, "relative_bias_default", no_p2c)
+    bad = m.encode(g["ids"], g["mask"])
+    assert np.max(np.abs(bad - g["out"])) > 1e-3
