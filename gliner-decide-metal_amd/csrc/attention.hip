@@ -288,11 +288,17 @@ __global__ __launch_bounds__(256) void deberta_attention_kernel(
       for (int tt = 0; tt < 4; tt += 2) {
         const int T = 4 * c + tt;
         if (T < nt) {
-          half8_t pa;
+          // P = P_hi + P_lo, both fp16: two MFMAs make P.V exact to ~2^-22
+          // relative instead of rounding the probabilities to fp16 first.
+          half8_t pa, pl;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            pa[i] = (half_t)(sc[T][i] * inv);
-            pa[4 + i] = (T + 1 < nt) ? (half_t)(sc[T + 1][i] * inv) : (half_t)0.f;
+            const float p0 = sc[T][i] * inv;
+            const float p1 = (T + 1 < nt) ? sc[T + 1][i] * inv : 0.f;
+            pa[i] = (half_t)p0;
+            pa[4 + i] = (half_t)p1;
+            pl[i] = (half_t)(p0 - (float)pa[i]);
+            pl[4 + i] = (half_t)(p1 - (float)pa[4 + i]);
           }
 #pragma unroll
           for (int dt = 0; dt < 4; ++dt) {
@@ -306,6 +312,7 @@ __global__ __launch_bounds__(256) void deberta_attention_kernel(
               vb[4 + i] = v1[i];
             }
             o[dt] = mfma16x16x32(pa, vb, o[dt]);
+            o[dt] = mfma16x16x32(pl, vb, o[dt]);
           }
         }
       }

@@ -69,11 +69,12 @@ void gd_config_default(gd_config* c) {
 int gd_residual_layer_norm(const void* x, const void* residual, const void* gamma, const void* beta, void* out,
                            int64_t rows, int64_t cols, float eps, uint32_t flags, void* stream) {
   clear_error();
-  GD_CHECK_ARG(x && gamma && beta && out, "null tensor pointer");
   GD_CHECK_SHAPE(rows >= 0, "rows must be >= 0 (got %lld)", (long long)rows);
   GD_CHECK_SHAPE(cols > 0 && cols % 8 == 0, "cols must be a positive multiple of 8 (got %lld)", (long long)cols);
   GD_CHECK_ARG(eps > 0.f && std::isfinite(eps), "eps must be positive and finite");
   GD_CHECK_ARG((flags & ~GD_LN_SUM_F16) == 0, "unknown flags 0x%x", flags);
+  if (rows == 0) return GD_OK;  // nothing to do; empty tensors may carry null pointers
+  GD_CHECK_ARG(x && gamma && beta && out, "null tensor pointer");
   return launch_residual_layer_norm(x, residual, gamma, beta, out, rows, cols, eps, flags, as_stream(stream));
 }
 
@@ -81,12 +82,13 @@ int gd_embedding_layer_norm(const int32_t* ids, const void* attention_mask, cons
                             const void* beta, void* out, int64_t batch, int64_t seq_len, int64_t hidden,
                             int64_t vocab, float eps, int32_t* error_flag, void* stream) {
   clear_error();
-  GD_CHECK_ARG(ids && attention_mask && table && gamma && beta && out, "null tensor pointer");
   GD_CHECK_SHAPE(batch >= 0 && seq_len >= 0, "negative batch or sequence length");
   GD_CHECK_SHAPE(hidden > 0 && hidden % 8 == 0, "hidden must be a positive multiple of 8 (got %lld)",
                  (long long)hidden);
   GD_CHECK_SHAPE(vocab > 0, "vocab must be positive");
   GD_CHECK_ARG(eps > 0.f && std::isfinite(eps), "eps must be positive and finite");
+  if (batch * seq_len == 0) return GD_OK;
+  GD_CHECK_ARG(ids && attention_mask && table && gamma && beta && out, "null tensor pointer");
   return launch_embedding_layer_norm(ids, attention_mask, table, gamma, beta, out, batch * seq_len, hidden, vocab, eps,
                                      error_flag, as_stream(stream));
 }
@@ -94,7 +96,7 @@ int gd_embedding_layer_norm(const int32_t* ids, const void* attention_mask, cons
 int gd_linear(const void* a, const void* w, const void* bias, void* c, int64_t m, int64_t n, int64_t k, int64_t lda,
               int64_t ldc, const int32_t* a_rows, int64_t a_row_count, int32_t epilogue, void* stream) {
   clear_error();
-  GD_CHECK_ARG(a && w && c, "null tensor pointer");
+  GD_CHECK_ARG(m == 0 || (a && w && c), "null tensor pointer");
   GD_CHECK_ARG(epilogue >= GD_EPI_NONE && epilogue <= GD_EPI_BIAS_RELU, "unknown epilogue %d", epilogue);
   GD_CHECK_ARG(epilogue == GD_EPI_NONE || bias, "epilogue %d needs a bias", epilogue);
   GD_CHECK_SHAPE(m >= 0 && m <= 0x7fffffff, "m out of range (%lld)", (long long)m);

@@ -42,10 +42,14 @@ inline int fail(int code, const char* msg) {
     }                                            \
   } while (0)
 
+// On failure the thread's HIP error state is cleared (hipGetLastError), so a
+// failed call is reported once, by its own entry point, and not again by the
+// next launch check.
 #define GD_HIP_CHECK(expr)                                                        \
   do {                                                                            \
     hipError_t gd_hip_err_ = (expr);                                              \
     if (gd_hip_err_ != hipSuccess) {                                              \
+      (void)hipGetLastError();                                                    \
       ::gd::set_error("HIP error %s (%d) at %s:%d: %s", hipGetErrorName(gd_hip_err_), \
                       (int)gd_hip_err_, __FILE__, __LINE__, #expr);               \
       return GD_ERR_HIP;                                                          \
@@ -90,11 +94,15 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-// Make this wave's LDS writes visible to its other lanes (no s_barrier).
+// Orders this wave's LDS writes before its later LDS reads by other lanes of
+// the same wave.  LDS operations of one wavefront execute in issue order, so
+// wavefront-scope fences emit no wait; they only stop the compiler from
+// moving the accesses across this point.  Outstanding global loads are left
+// in flight (a workgroup-scope fence would drain them).
 __device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // MFMA wrappers (gfx950 double-rate fp16 forms).

@@ -49,6 +49,7 @@ Classifier::~Classifier() {
   release_graphs();
   for (void* p : allocations_) (void)hipFree(p);
   for (void* p : workspace_allocs_) (void)hipFree(p);
+  if (capture_stream_) (void)hipStreamDestroy(capture_stream_);
 }
 
 void Classifier::release_graphs() {
@@ -385,11 +386,16 @@ int Classifier::classify(const int32_t* ids, const void* mask, const int32_t* ma
   auto it = graphs_.find(key);
   if (it == graphs_.end()) {
     GraphEntry ge;
-    GD_HIP_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+    // Capture on the context's own stream: the caller's stream may be the
+    // legacy null stream, which cannot be captured.  Capturing enqueues no
+    // work; the instantiated graph is launched on the caller's stream below.
+    if (!capture_stream_) GD_HIP_CHECK(hipStreamCreateWithFlags(&capture_stream_, hipStreamNonBlocking));
+    GD_HIP_CHECK(hipStreamBeginCapture(capture_stream_, hipStreamCaptureModeThreadLocal));
     int st = forward(static_cast<const int32_t*>(ws_.ids), ws_.mask, static_cast<const int32_t*>(ws_.markers),
-                     static_cast<const float*>(ws_.marker_mask), B, L, Hh, O, ws_.logits, stream, nullptr);
+                     static_cast<const float*>(ws_.marker_mask), B, L, Hh, O, ws_.logits, capture_stream_, nullptr);
     hipGraph_t graph = nullptr;
-    hipError_t e = hipStreamEndCapture(stream, &graph);
+    hipError_t e = hipStreamEndCapture(capture_stream_, &graph);
+    (void)hipGetLastError();
     if (st != GD_OK) {
       if (graph) (void)hipGraphDestroy(graph);
       return st;

@@ -88,6 +88,7 @@ class Classifier {
   Workspace ws_;
   int64_t ws_tokens_ = 0, ws_markers_ = 0;
   std::map<ShapeKey, GraphEntry> graphs_;
+  hipStream_t capture_stream_ = nullptr;  // default priority, non-blocking
 };
 
 }  // namespace gd

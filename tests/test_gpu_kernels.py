@@ -146,17 +146,34 @@ def test_linear(m, n, k, epi):
     w = (r.standard_normal((n, k)) / np.sqrt(k)).astype(np.float16)
     b = r.standard_normal(n).astype(np.float16)
     out = host(fk().linear(dev(x), dev(w), dev(b) if epi != "none" else None, epilogue=epi))
-    y = x.astype(np.float64) @ w.astype(np.float64).T
-    if epi == "none":
-        want = O.f16(y)
-    else:
-        want = O.f16(y + b)
-        if epi == "gelu":
-            want = O.gelu(want)
-        elif epi == "relu":
-            want = np.maximum(want, 0)
-    # fp32 accumulation order differs from float64: allow 2 ulp before GELU's rounding
-    assert_within_ulp(out, want, 2.0 if epi == "gelu" else 1.0, max_frac_off=5e-3)
+    check_linear(out, x, w, b, epi)
+
+
+def check_linear(out, x, w, b, epi):
+    """|gpu - exact| <= fp16 output rounding + fp32 accumulation error.
+
+    The accumulation term is the standard dot-product bound with a
+    sqrt(K) growth factor: 4 sqrt(K) 2^-24 sum_k |x_k w_k|.  Near-zero
+    outputs (cancellation) are judged by the size of their terms, not by the
+    ulp of the tiny result."""
+    K = x.shape[1]
+    x64, w64 = x.astype(np.float64), w.astype(np.float64)
+    y = x64 @ w64.T + (b.astype(np.float64) if epi != "none" else 0.0)
+    acc = 4.0 * np.sqrt(K) * 2.0 ** -24 * (np.abs(x64) @ np.abs(w64).T)
+    half = 0.5 * np.maximum(ulp16(y), ulp16(out))
+    if epi in ("none", "bias"):
+        bound, want = half + acc, y
+    elif epi == "relu":
+        bound, want = half + acc, np.maximum(y, 0)
+    else:  # gelu(fp16(y)): |gelu'| <= 1.13, two roundings
+        want = O.gelu(y, round16=False)
+        bound = 0.5 * np.maximum(ulp16(want), ulp16(out)) + 1.13 * (half + acc)
+    err = np.abs(out - want)
+    worst = np.argmax(err - bound)
+    assert np.all(err <= bound + 1e-12), f"err {err.flat[worst]:.3g} > bound {bound.flat[worst]:.3g}"
+    # the common case is exact agreement with the once-rounded reference value
+    if epi in ("none", "bias"):
+        assert np.mean(out != O.f16(y)) < 5e-3
 
 
 def test_linear_row_gather():
@@ -166,8 +183,7 @@ def test_linear_row_gather():
     b = r.standard_normal(2048).astype(np.float16)
     rows = r.integers(0, 500, size=77).astype(np.int32)
     out = host(fk().linear(dev(x), dev(w), dev(b), epilogue="relu", rows=dev(rows)))
-    want = np.maximum(O.f16(x[rows].astype(np.float64) @ w.astype(np.float64).T + b), 0)
-    assert_within_ulp(out, want, 1.0, max_frac_off=5e-3)
+    check_linear(out, x[rows], w, b, "relu")
 
 
 # ---------------------------------------------------------------------------
@@ -200,6 +216,17 @@ def _oracle_probs(q, k, pk, pq, mask):
     return bias, O.attention_probs_default(q, k, bias, mask, 64)
 
 
+def _bias_terms(q, k, pk, pq):
+    """The fp16 c2p and p2c terms of the default graph, gathered to [B,H,L,L]."""
+    H, L = q.shape[1], q.shape[2]
+    pkh, pqh = _tables(pk, pq, H)
+    c2p, p2c = O.relative_indices(L)
+    c2p_raw = O.f16(np.einsum("bhld,hpd->bhlp", q.astype(np.float64), pkh.astype(np.float64), optimize=True))
+    p2c_raw = O.f16(np.einsum("bhld,hpd->bhlp", k.astype(np.float64), pqh.astype(np.float64), optimize=True))
+    rows = np.arange(L)[:, None]
+    return c2p_raw[:, :, rows, c2p], np.swapaxes(p2c_raw[:, :, rows, p2c], -1, -2)
+
+
 def _gpu_tables(pk, pq, H):
     tpk, tpq = dev(pk), dev(pq)
     P = pk.shape[0]
@@ -221,7 +248,15 @@ def test_attention_probs_and_bias(L):
     want_b = O.f16(bias + O.additive_key_mask(mask))
     fin = np.isfinite(want_b)
     np.testing.assert_array_equal(np.isfinite(gb), fin)
-    assert_within_ulp(gb[fin], want_b[fin], 2.0, max_frac_off=2e-2)
+    # fp32 (GPU) vs float64 (oracle) accumulation may flip c2p, p2c or their
+    # fp16 sum by one ulp; each flip moves the bias by ulp / fp16(sqrt(192)).
+    c2p16, p2c16 = _bias_terms(q, k, pk, pq)
+    s16 = O.f16(c2p16 + p2c16)
+    bound = (ulp16(c2p16) + ulp16(p2c16) + ulp16(s16)) / O.scale_f16(64) + ulp16(bias)
+    bound = np.broadcast_to(bound, want_b.shape)
+    err = np.abs(gb - want_b)
+    assert np.all(err[fin] <= bound[fin]), err[fin].max()
+    assert np.mean(err[fin] > 0) < 2e-2
 
 
 @pytest.mark.parametrize("L", [32, 96, 256, 512])
