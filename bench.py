@@ -45,6 +45,11 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     p.add_argument("--kernel-iters", type=int, default=60)
+    p.add_argument("--profile-kernel", default=None,
+                   choices=["residual_layernorm", "relbias_softmax", "attention_context", "qkv_proj", "out_proj",
+                            "ffn_up_gelu", "ffn_down"],
+                   help="only run this kernel (--kernel-iters launches on rotating buffers) followed by a 256 MiB "
+                        "torch copy, for rocprofv3 counter runs; prints the kernel table, no JSON line")
     return p.parse_args()
 
 
@@ -67,78 +72,84 @@ def time_launches(fn, sets, iters):
     return start.elapsed_time(end) * 1000.0 / iters
 
 
-def measure_kernels(model_cfg, iters):
+def measure_kernels(model_cfg, iters, only=None):
+    """Times each kernel of the step at the workload's shapes (or just `only`)."""
     import torch
+    from gliner_decide import _native as N
+    from gliner_decide.device import stream_handle
     from gliner_decide.fused_kernels import FusedKernels
     from gliner_decide.synthetic import normal16, relbias_inputs
 
     fk = FusedKernels()
+    lib = N.lib()
     dev = torch.device("cuda")
     out = {}
+    want = (lambda name: only is None or only == name)
 
     # residual-add LayerNorm, 8192 x 1024 (the model's shape at B=32, L=256)
-    rows, cols = 8192, 1024
-    nbytes = 3 * rows * cols * 2 + 2 * cols * 2
-    nsets = max(2, ROTATE_BYTES // (3 * rows * cols * 2) + 1)
-    g = torch.from_numpy(normal16(2, "gamma", (cols,), 1.0, 0.1)).to(dev)
-    b = torch.from_numpy(normal16(2, "beta", (cols,), 0.0, 0.1)).to(dev)
-    x0 = torch.from_numpy(normal16(2, "x", (rows, cols))).to(dev)
-    r0 = torch.from_numpy(normal16(2, "residual", (rows, cols))).to(dev)
-    sets = [(x0.roll(i, 0).contiguous(), r0.roll(i, 0).contiguous(), torch.empty_like(x0)) for i in range(nsets)]
-    from gliner_decide import _native as N
-    from gliner_decide.device import stream_handle
-    lib = N.lib()
+    if want("residual_layernorm"):
+        rows, cols = 8192, 1024
+        nbytes = 3 * rows * cols * 2 + 2 * cols * 2
+        nsets = max(2, ROTATE_BYTES // (3 * rows * cols * 2) + 1)
+        g = torch.from_numpy(normal16(2, "gamma", (cols,), 1.0, 0.1)).to(dev)
+        b = torch.from_numpy(normal16(2, "beta", (cols,), 0.0, 0.1)).to(dev)
+        x0 = torch.from_numpy(normal16(2, "x", (rows, cols))).to(dev)
+        r0 = torch.from_numpy(normal16(2, "residual", (rows, cols))).to(dev)
+        sets = [(x0.roll(i, 0).contiguous(), r0.roll(i, 0).contiguous(), torch.empty_like(x0)) for i in range(nsets)]
 
-    def ln(s):
-        N.check(lib.gd_residual_layer_norm(s[0].data_ptr(), s[1].data_ptr(), g.data_ptr(), b.data_ptr(),
-                                           s[2].data_ptr(), rows, cols, 1e-7, N.GD_LN_SUM_F16, stream_handle()))
+        def ln(s):
+            N.check(lib.gd_residual_layer_norm(s[0].data_ptr(), s[1].data_ptr(), g.data_ptr(), b.data_ptr(),
+                                               s[2].data_ptr(), rows, cols, 1e-7, N.GD_LN_SUM_F16, stream_handle()))
 
-    us = time_launches(ln, sets, iters)
-    out["residual_layernorm"] = dict(kernel="residual_ln_kernel<2>", shape=[rows, cols], us=us, bytes=nbytes,
-                                     gbs=nbytes / us / 1e3, bound="hbm", launches_per_step=48)
-    del sets
+        us = time_launches(ln, sets, iters)
+        out["residual_layernorm"] = dict(kernel="residual_ln_kernel<2>", shape=[rows, cols], us=us, bytes=nbytes,
+                                         gbs=nbytes / us / 1e3, bound="hbm", launches_per_step=48)
+        del sets
 
     # relative bias + masked softmax, B=32 H=16 L=256 D=64 -> P [32,16,256,256]
-    d = relbias_inputs(seed=3)
     B, H, L, D = 32, 16, 256, 64
+    d = relbias_inputs(seed=3)
     pk = torch.from_numpy(d["pos_key"]).to(dev).view(512, H, D).permute(1, 0, 2)
     pq = torch.from_numpy(d["pos_query"]).to(dev).view(512, H, D).permute(1, 0, 2)
     mask = torch.from_numpy(d["mask"]).to(dev)
-    q0 = torch.from_numpy(d["q"]).to(dev)
-    k0 = torch.from_numpy(d["k"]).to(dev)
-    per_set = (2 * B * H * L * D + B * H * L * L) * 2
-    nsets = max(2, ROTATE_BYTES // per_set + 1)
-    sets = [(q0.roll(i, 0).contiguous(), k0.roll(i, 0).contiguous(),
-             torch.empty((B, H, L, L), dtype=torch.float16, device=dev)) for i in range(nsets)]
-    nbytes = 2 * B * H * L * D * 2 + 2 * 512 * H * D * 2 + B * 4 + B * H * L * L * 2
+    if want("relbias_softmax"):
+        q0 = torch.from_numpy(d["q"]).to(dev)
+        k0 = torch.from_numpy(d["k"]).to(dev)
+        per_set = (2 * B * H * L * D + B * H * L * L) * 2
+        nsets = max(2, ROTATE_BYTES // per_set + 1)
+        sets = [(q0.roll(i, 0).contiguous(), k0.roll(i, 0).contiguous(),
+                 torch.empty((B, H, L, L), dtype=torch.float16, device=dev)) for i in range(nsets)]
+        nbytes = 2 * B * H * L * D * 2 + 2 * 512 * H * D * 2 + B * 4 + B * H * L * L * 2
 
-    def rb(s):
-        fk.deberta_attention(s[0], s[1], None, pk, pq, mask, output="probs", out=s[2])
+        def rb(s):
+            fk.deberta_attention(s[0], s[1], None, pk, pq, mask, output="probs", out=s[2])
 
-    us = time_launches(rb, sets, iters)
-    out["relbias_softmax"] = dict(kernel="deberta_attention_kernel<16,PROBS>", shape=[B, H, L, L], us=us,
-                                  bytes=nbytes, gbs=nbytes / us / 1e3, bound="hbm", launches_per_step=0)
-    del sets
+        us = time_launches(rb, sets, iters)
+        out["relbias_softmax"] = dict(kernel="deberta_attention_kernel<16,PROBS>", shape=[B, H, L, L], us=us,
+                                      bytes=nbytes, gbs=nbytes / us / 1e3, bound="hbm", launches_per_step=0)
+        del sets
 
     # attention as the encoder runs it: context output from the fused QKV layout
     T = B * L
-    qkv = torch.randn((T, 3 * H * D), device=dev, dtype=torch.float16)
-    ctx = torch.empty((T, H * D), device=dev, dtype=torch.float16)
-    amask = torch.from_numpy(d["mask"]).to(dev)
-    v5 = qkv.view(B, L, 3, H, D)
-    qv, kv_, vv = (v5[:, :, i].permute(0, 2, 1, 3) for i in range(3))
-    us = time_launches(lambda s: fk.deberta_attention(qv, kv_, vv, pk, pq, amask, output="context", out=ctx), [0],
-                       iters)
-    flops = 2 * B * H * L * L * D * 2  # QK^T and PV (bias terms counted separately below)
-    out["attention_context"] = dict(kernel="deberta_attention_kernel<16,CONTEXT>", shape=[B, H, L, D], us=us,
-                                    flops=flops, bytes=(4 * T * H * D) * 2, bound="mfma", launches_per_step=24,
-                                    tflops=flops / us / 1e6)
-    del qkv, ctx
+    if want("attention_context"):
+        qkv = torch.randn((T, 3 * H * D), device=dev, dtype=torch.float16)
+        ctx = torch.empty((T, H * D), device=dev, dtype=torch.float16)
+        v5 = qkv.view(B, L, 3, H, D)
+        qv, kv_, vv = (v5[:, :, i].permute(0, 2, 1, 3) for i in range(3))
+        us = time_launches(lambda s: fk.deberta_attention(qv, kv_, vv, pk, pq, mask, output="context", out=ctx),
+                           [0], iters)
+        flops = 4 * (2 * B * H * L * L * D)  # QK^T, c2p, p2c (direct dot products) and PV
+        out["attention_context"] = dict(kernel="deberta_attention_kernel<16,CONTEXT>", shape=[B, H, L, D], us=us,
+                                        flops=flops, bytes=(4 * T * H * D) * 2, bound="mfma", launches_per_step=24,
+                                        tflops=flops / us / 1e6)
+        del qkv, ctx
 
     # the four projections at T = 8192
     C, F = 1024, 4096
     for name, (n, k, epi) in {"qkv_proj": (3 * C, C, "bias"), "out_proj": (C, C, "bias"),
                               "ffn_up_gelu": (F, C, "gelu"), "ffn_down": (C, F, "bias")}.items():
+        if not want(name):
+            continue
         a = torch.randn((T, k), device=dev, dtype=torch.float16)
         w = torch.randn((n, k), device=dev, dtype=torch.float16) * 0.02
         bias = torch.randn((n,), device=dev, dtype=torch.float16)
@@ -158,6 +169,18 @@ def measure_kernels(model_cfg, iters):
     return out
 
 
+def calibration_copy(nbytes=256 << 20):
+    """A plain device copy of known size: rocprofv3 FETCH_SIZE / WRITE_SIZE of
+    this dispatch calibrate the counters against bytes actually moved."""
+    import torch
+    src = torch.empty(nbytes // 2, dtype=torch.float16, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    return nbytes
+
+
 def roofline_of(kernels):
     """The kernel with the largest time share of one forward step."""
     best = max((v for v in kernels.values() if v["launches_per_step"] > 0),
@@ -167,9 +190,23 @@ def roofline_of(kernels):
     else:
         ach, peak, unit = best["tflops"], FP16_DENSE_TFLOPS, "TFLOP/s"
     name = [k for k, v in kernels.items() if v is best][0]
+    traffic, source = profiled_traffic(name)
     return dict(kernel=name, bound=best["bound"], achieved=round(ach, 2), peak=peak, unit=unit,
-                frac=round(ach / peak, 4), traffic=None, avg_us=round(best["us"], 2),
+                frac=round(ach / peak, 4), traffic=traffic, traffic_source=source, avg_us=round(best["us"], 2),
                 algorithmic_per_launch=best.get("flops", best.get("bytes")))
+
+
+def profiled_traffic(kernel):
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary of this kernel (profiles/<kernel>.md), counters calibrated with a
+    256 MiB copy; None when no summary exists."""
+    path = ROOT / "profiles" / f"{kernel}.md"
+    if not path.exists():
+        return None, None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1]), str(path.relative_to(ROOT))
+    return None, None
 
 
 # ---------------------------------------------------------------------------
@@ -214,6 +251,12 @@ def main():
 
     torch.cuda.set_device(0)
     cfg = DeBERTaV2Configuration(vocab_size=128100)
+    if args.profile_kernel:
+        kernels = measure_kernels(cfg, args.kernel_iters, only=args.profile_kernel)
+        nb = calibration_copy()
+        for k, v in kernels.items():
+            log(f"{k}: {v['us']:.2f} us per launch over {args.kernel_iters} launches; calibration copy {nb} B")
+        return
     t = time.perf_counter()
     weights = synthetic_weights(cfg, seed=4)
     log(f"weights generated in {time.perf_counter() - t:.1f} s")
@@ -272,7 +315,8 @@ def main():
         "config": dict(wl, parallelism="single GPU", compiled_graph=args.compiled),
         "roofline": roof,
         "cpu_baseline": cpu,
-        "kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+        "kernels": {k: dict({kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()},
+                            traffic=profiled_traffic(k)[0])
                     for k, v in kernels.items()},
         "fused_ln_gbs": round(kernels["residual_layernorm"]["gbs"], 1),
         "fused_ln_frac_hbm": round(kernels["residual_layernorm"]["gbs"] / HBM_PEAK_GBS, 4),

@@ -21,6 +21,8 @@
 //   * workgroups are dispatched round-robin over the 8 XCDs; the tile order is
 //     remapped so each XCD works on a compact 4-tile-row band and its private
 //     L2 serves the A rows and W columns it shares.
+#include <cstdlib>
+
 #include "gd_common.hpp"
 #include "gd_kernels.hpp"
 
@@ -159,6 +161,192 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(const half_t* __restr
   }
 }
 
+// ---------------------------------------------------------------------------
+// Large-M kernel: 8 waves (two per SIMD), direct global -> LDS loads.
+//
+// Each K step of 64 is fetched with global_load_lds_dwordx4: one instruction
+// moves 1 KiB (64 lanes x 16 B) straight into LDS at M0 + 16*lane, so no
+// VGPRs stage the tiles and the loads of step k+1 run under the MFMAs of step
+// k.  The XOR swizzle is applied on the global side: lane l of a 1 KiB block
+// (8 rows of 128 B) fetches logical chunk (l%8) ^ (l/8) of row l/8, which
+// lands at physical chunk l%8 -- the same layout lds_swz() reads.  One
+// barrier per K step: wait for this thread's step-k loads, barrier (all
+// loads landed, all waves done with step k-1), issue step k+1 into the other
+// buffer, compute step k.  The epilogue stages the fp16 tile through LDS and
+// writes 16-byte coalesced row segments.
+// ---------------------------------------------------------------------------
+constexpr int kThreads8 = 512;
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ void load_lds16(const half_t* g, half_t* lds_block) {
+  __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g), (lds_void_t*)(lds_block), 16, 0, 0);
+}
+
+// vmcnt(N) with lgkmcnt / expcnt left unconstrained (gfx9 s_waitcnt encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (((N >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <int BM, int BN, int WAVES_M, int NSTAGE, int EPI>
+__global__ __launch_bounds__(kThreads8) void gemm_nt_lds_kernel(const half_t* __restrict__ A,
+                                                                const half_t* __restrict__ W,
+                                                                const half_t* __restrict__ bias,
+                                                                half_t* __restrict__ C, int M, int N, int K,
+                                                                int64_t lda, int64_t ldc, int tiles_m, int tiles_n) {
+  constexpr int NW = 8;
+  constexpr int WAVES_N = NW / WAVES_M;
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int A_BLK = BM / 8 / NW, B_BLK = BN / 8 / NW;  // 1 KiB blocks per wave per K step
+  constexpr int STAGE = (BM + BN) * kBK;                   // halfs per buffer
+  static_assert(TM >= 1 && TN >= 1 && A_BLK >= 1 && B_BLK >= 1, "tile shape");
+  constexpr int LPS = A_BLK + B_BLK;                       // loads per thread per K step
+  static_assert(NSTAGE >= 2 && NSTAGE <= 4, "pipeline depth");
+  static_assert(NSTAGE * STAGE >= BM * BN, "epilogue staging must fit in the pipeline buffers");
+  __shared__ __attribute__((aligned(1024))) half_t smem[NSTAGE * STAGE];
+
+  const int nwg = tiles_m * tiles_n;
+  int bid = blockIdx.x;
+  if ((nwg & 7) == 0) bid = (bid & 7) * (nwg >> 3) + (bid >> 3);
+  const int band = bid / (kGroupM * tiles_n);
+  const int first_m = band * kGroupM;
+  const int gm = min(kGroupM, tiles_m - first_m);
+  const int in_band = bid - band * kGroupM * tiles_n;
+  const int tile_m = first_m + in_band % gm;
+  const int tile_n = in_band / gm;
+
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int lr = lane & 31, lk = lane >> 5;
+
+  // Source pointers of this lane's 16-byte pieces (fixed across K).
+  const int blk_row = lane >> 3;                       // row within a 1 KiB block
+  const int blk_chunk = (lane & 7) ^ blk_row;          // logical chunk it fetches
+  const half_t* a_src[A_BLK];
+  const half_t* b_src[B_BLK];
+#pragma unroll
+  for (int j = 0; j < A_BLK; ++j) {
+    int m = tile_m * BM + (wave * A_BLK + j) * 8 + blk_row;
+    m = m < M ? m : M - 1;
+    a_src[j] = A + (int64_t)m * lda + blk_chunk * 8;
+  }
+#pragma unroll
+  for (int j = 0; j < B_BLK; ++j) {
+    const int n = tile_n * BN + (wave * B_BLK + j) * 8 + blk_row;
+    b_src[j] = W + (int64_t)n * K + blk_chunk * 8;
+  }
+  auto issue = [&](int k0, int buf) {
+    half_t* As = smem + buf * STAGE;
+    half_t* Bs = As + BM * kBK;
+#pragma unroll
+    for (int j = 0; j < A_BLK; ++j) load_lds16(a_src[j] + k0, As + (wave * A_BLK + j) * 512);
+#pragma unroll
+    for (int j = 0; j < B_BLK; ++j) load_lds16(b_src[j] + k0, Bs + (wave * B_BLK + j) * 512);
+  };
+
+  float16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  const int nk = K / kBK;
+  // Prologue: NSTAGE - 1 K steps in flight.
+#pragma unroll
+  for (int s = 0; s < NSTAGE - 1; ++s)
+    if (s < nk) issue(s * kBK, s);
+  for (int kt = 0; kt < nk; ++kt) {
+    // Step kt has landed once at most `pending` later steps are outstanding.
+    const int pending = min(NSTAGE - 2, nk - 1 - kt);
+    if (pending <= 0) {
+      wait_vmcnt<0>();
+    } else if (NSTAGE == 3 || pending == 1) {
+      wait_vmcnt<LPS>();
+    } else if (pending == 2) {
+      wait_vmcnt<(NSTAGE >= 4 ? 2 * LPS : 0)>();
+    }
+    __syncthreads();  // all pieces of step kt landed; all waves finished step kt - 1
+    if (kt + NSTAGE - 1 < nk) issue((kt + NSTAGE - 1) * kBK, (kt + NSTAGE - 1) % NSTAGE);
+    const half_t* As = smem + (kt % NSTAGE) * STAGE;
+    const half_t* Bs = As + BM * kBK;
+#pragma unroll
+    for (int s = 0; s < kBK / 16; ++s) {
+      half8_t fa[TM], fb[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        fa[i] = *reinterpret_cast<const half8_t*>(As + lds_swz(wm * WM + i * 32 + lr, 2 * s + lk));
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        fb[j] = *reinterpret_cast<const half8_t*>(Bs + lds_swz(wn * WN + j * 32 + lr, 2 * s + lk));
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16(fa[i], fb[j], acc[i][j]);
+    }
+  }
+  __syncthreads();  // all waves done reading the pipeline buffers
+
+  // ---- epilogue: bias/activation in registers, fp16 tile staged in LDS ----
+  half_t* Cs = smem;  // [BM][BN]
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int cl = wn * WN + j * 32 + lr;
+    const float b = (EPI != GD_EPI_NONE) ? (float)bias[tile_n * BN + cl] : 0.f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int r0 = wm * WM + i * 32 + 4 * lk;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) Cs[(r0 + 8 * (e >> 2) + (e & 3)) * BN + cl] = epilogue<EPI>(acc[i][j][e], b);
+    }
+  }
+  __syncthreads();
+  constexpr int CHUNKS_PER_ROW = BN / 8;
+  constexpr int ROWS_PER_PASS = kThreads8 / CHUNKS_PER_ROW;
+  const int cc = t % CHUNKS_PER_ROW;
+#pragma unroll 4
+  for (int r = t / CHUNKS_PER_ROW; r < BM; r += ROWS_PER_PASS) {
+    const int row = tile_m * BM + r;
+    if (row < M)
+      *reinterpret_cast<half8_t*>(C + (int64_t)row * ldc + tile_n * BN + cc * 8) =
+          *reinterpret_cast<const half8_t*>(Cs + r * BN + cc * 8);
+  }
+}
+
+template <int BM, int BN, int WAVES_M, int NSTAGE>
+int launch_lds_tile(const half_t* A, const half_t* W, const half_t* bias, half_t* C, int M, int N, int K, int64_t lda,
+                    int64_t ldc, int epi, hipStream_t stream) {
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = N / BN;
+  const dim3 grid(tiles_m * tiles_n), block(kThreads8);
+  switch (epi) {
+    case GD_EPI_NONE:
+      hipLaunchKernelGGL((gemm_nt_lds_kernel<BM, BN, WAVES_M, NSTAGE, GD_EPI_NONE>), grid, block, 0, stream, A, W, bias, C, M,
+                         N, K, lda, ldc, tiles_m, tiles_n);
+      break;
+    case GD_EPI_BIAS:
+      hipLaunchKernelGGL((gemm_nt_lds_kernel<BM, BN, WAVES_M, NSTAGE, GD_EPI_BIAS>), grid, block, 0, stream, A, W, bias, C, M,
+                         N, K, lda, ldc, tiles_m, tiles_n);
+      break;
+    case GD_EPI_BIAS_GELU:
+      hipLaunchKernelGGL((gemm_nt_lds_kernel<BM, BN, WAVES_M, NSTAGE, GD_EPI_BIAS_GELU>), grid, block, 0, stream, A, W, bias,
+                         C, M, N, K, lda, ldc, tiles_m, tiles_n);
+      break;
+    default:
+      hipLaunchKernelGGL((gemm_nt_lds_kernel<BM, BN, WAVES_M, NSTAGE, GD_EPI_BIAS_RELU>), grid, block, 0, stream, A, W, bias,
+                         C, M, N, K, lda, ldc, tiles_m, tiles_n);
+      break;
+  }
+  GD_LAUNCH_CHECK();
+  return GD_OK;
+}
+
 template <int BM, int BN, bool GATHER>
 int launch_tile(const half_t* A, const half_t* W, const half_t* bias, half_t* C, int M, int N, int K, int64_t lda,
                 int64_t ldc, const int32_t* a_rows, int a_row_count, int epi, hipStream_t stream) {
@@ -187,6 +375,16 @@ int launch_tile(const half_t* A, const half_t* W, const half_t* bias, half_t* C,
   return GD_OK;
 }
 
+// GD_GEMM_VARIANT=1 selects the register-staged kernel for every shape (A/B
+// comparisons); the default 0 uses the direct-to-LDS kernel for M >= 2048.
+int gemm_variant() {
+  static const int v = [] {
+    const char* e = std::getenv("GD_GEMM_VARIANT");
+    return e ? std::atoi(e) : 0;
+  }();
+  return v;
+}
+
 }  // namespace
 
 int launch_linear(const void* a, const void* w, const void* bias, void* c, int64_t m, int64_t n, int64_t k, int64_t lda,
@@ -202,6 +400,13 @@ int launch_linear(const void* a, const void* w, const void* bias, void* c, int64
   if (a_rows) {
     if (M >= 1024) return launch_tile<128, 128, true>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
     return launch_tile<64, 128, true>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
+  }
+  if (M >= 2048 && gemm_variant() == 0) {
+    // 256 x 256 tiles when they fill whole waves of the 256 CUs, else 256 x 128.
+    const int t256 = ((M + 255) / 256) * (N / 256);
+    if (N % 256 == 0 && (t256 % 256 == 0 || t256 >= 512))
+      return launch_lds_tile<256, 256, 2, 2>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
+    return launch_lds_tile<256, 128, 4, 3>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
   }
   if (M >= 4096) return launch_tile<256, 128, false>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
   if (M >= 1024) return launch_tile<128, 128, false>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
