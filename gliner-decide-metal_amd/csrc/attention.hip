@@ -35,6 +35,7 @@
 // context output V is streamed again, transposed into LDS.
 // ---------------------------------------------------------------------------
 #include <cmath>
+#include <cstdlib>
 
 #include "gd_common.hpp"
 #include "gd_kernels.hpp"
@@ -486,6 +487,13 @@ int max_c2p_window(int L, int bucket_size, int max_position) {
 }  // namespace
 
 int launch_deberta_attention(const AttentionArgs& a, hipStream_t stream) {
+  // GD_ATTN_VARIANT=1 selects the first (per-wave streaming) kernel for A/B
+  // comparisons; the staged kernel is the default.
+  static const int variant = [] {
+    const char* e = std::getenv("GD_ATTN_VARIANT");
+    return e ? std::atoi(e) : 0;
+  }();
+  if (variant == 0) return launch_deberta_attention2(a, stream);
   const int window = max_c2p_window((int)a.L, a.bucket_size, (int)a.P);
   if (a.L <= 64) {
     if (window > c2p_cap_for(4)) return fail(GD_ERR_UNSUPPORTED, "c2p window exceeds LDS capacity");

@@ -1,0 +1,439 @@
+// Disentangled attention, staged design (the encoder's attention kernel).
+//
+// Reference: DeBERTa.swift:322-395 (relative bias from the fp16 c2pRaw/p2cRaw
+// gathers, additive key mask, SDPA) with the index math of :498-551.
+//
+// One workgroup = (batch b, head h, 128 queries): 8 waves, wave w owns queries
+// q0 + 16w .. q0 + 16w + 15.  Keys stream through LDS in chunks of 64.  For
+// a chunk, every relative index the workgroup can need, idx(q - k) for its
+// 128 queries and the chunk's 64 keys, lies in one window of at most 191
+// consecutive rows of the relative tables (idx is monotone in q - k), so the
+// stage of a chunk is
+//     K rows        64 x 128 B
+//     posK window  192 x 128 B   (relative keys, for c2p)
+//     posQ window  192 x 128 B   (relative queries, for p2c)
+// fetched with global_load_lds_dwordx4 (16 B per lane straight into LDS; the
+// XOR swizzle of the 128-byte rows is applied on the global side) into one of
+// two buffers while the other chunk is computed.  Inside a chunk nothing
+// touches global memory:
+//   c2p  per wave: C2P^T = posK[window] . Q^T over <= 80 positions (5 MFMA
+//        column tiles, v_mfma_f32_16x16x32_f16), rounded to fp16 (the
+//        reference's c2pRaw) into a per-wave LDS tile;
+//   per 16-key tile: S^T = K Q^T (2 MFMAs) and P2C = K . posQ[window]^T over
+//        <= 31 positions (4 MFMAs), fp16 into a per-wave LDS tile; each score
+//        gathers its two terms by idx and applies the reference rounding
+//        chain fp16(fp16(c2p + p2c) / fp16(sqrt(3D))).
+// Scores stay in registers (a lane owns one query column and 4 keys per
+// tile), the softmax reduces in registers plus two cross-lane steps, and the
+// outputs leave through LDS as 16-byte row segments: P rows (probabilities),
+// the SDPA additive mask (bias), or the context P.V (V^T chunks in LDS, P as
+// the MFMA A operand split into fp16 hi + lo parts).
+#include <cmath>
+
+#include "gd_common.hpp"
+#include "gd_kernels.hpp"
+
+namespace gd {
+namespace {
+
+constexpr int kThreads = 512;
+constexpr int kWaves = 8;
+constexpr int kQT = 128;           // queries per workgroup
+constexpr int kKC = 64;            // keys per chunk
+constexpr int kD = 64;             // head dim
+constexpr int kWin = 192;          // relative-table rows per chunk window (>= 191)
+constexpr int kC2PCols = 80;       // per-wave c2p window (<= 79 positions)
+constexpr int kC2PStride = kC2PCols + 4;  // 168-byte rows keep the 8-byte stores aligned
+constexpr int kP2CStride = 34;     // per-wave p2c tile: 16 keys x 32 positions (+pad)
+constexpr int kVtStride = 68;      // V^T chunk row (64 keys + pad)
+
+// LDS map (halfs).  The stage buffers are reused for the V^T chunks and the
+// output staging once the score loop is done.
+constexpr int kStageK = kKC * kD;                 // 4096
+constexpr int kStageWin = kWin * kD;              // 12288
+constexpr int kStage = kStageK + 2 * kStageWin;   // 28672 halfs = 56 KiB
+constexpr int kScratchWave = 16 * kC2PStride + 16 * kP2CStride;
+constexpr int kSmemHalfs = 2 * kStage + kWaves * kScratchWave;
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ void load_lds16(const half_t* g, half_t* lds_block) {
+  __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g), (lds_void_t*)(lds_block), 16, 0, 0);
+}
+
+// 128-byte rows; the 16-byte chunk index is XORed with bits 1..3 of the row.
+// gfx950's LDS serves a ds_read_b128 16 lanes at a time over 64 banks
+// (256 B): 16 consecutive rows at the same logical chunk then land on 16
+// distinct (row parity, chunk) bank groups -- conflict-free.
+__device__ __forceinline__ int swz(int row, int chunk) { return row * kD + ((chunk ^ ((row >> 1) & 7)) << 3); }
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (((N >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <int MAXT, int OUT>
+__global__ __launch_bounds__(kThreads) void deberta_attention2_kernel(
+    const half_t* __restrict__ Q, const half_t* __restrict__ K, const half_t* __restrict__ V, int64_t qsb, int64_t qsh,
+    int64_t qsl, int64_t ksb, int64_t ksh, int64_t ksl, int64_t vsb, int64_t vsh, int64_t vsl,
+    const half_t* __restrict__ PK, const half_t* __restrict__ PQ, int64_t pksh, int64_t pksp, int64_t pqsh,
+    int64_t pqsp, const half_t* __restrict__ mask, int mask_kind, int B, int H, int L, int P, int bucket_size,
+    float scale_qk, float scale16, half_t* __restrict__ out, int64_t ldo) {
+  __shared__ __attribute__((aligned(1024))) half_t smem[kSmemHalfs];
+  __shared__ int16_t idx_tab[2 * 16 * MAXT];
+  __shared__ __attribute__((aligned(16))) float mask_add[16 * MAXT];
+
+  const int ntq = (L + kQT - 1) / kQT;
+  const int nblk = B * H * ntq;
+  int bid = blockIdx.x;
+  if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);  // a (b, h)'s query tiles share an XCD
+  const int qt = bid % ntq;
+  const int bh = bid / ntq;
+  const int h = bh % H;
+  const int b = bh / H;
+
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  // Wave-uniform values live in scalar registers: branches on them are scalar
+  // and their address arithmetic runs once per wave, not per lane.
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int lc = lane & 15;  // MFMA output column: the lane's query
+  const int g = lane >> 4;   // lane group
+  const int q0 = qt * kQT;
+  const int qw = q0 + 16 * wave;
+  const bool active = qw < L;
+  const int nt = L >> 4;
+  const int nchunks = (L + kKC - 1) / kKC;
+  const float inv_scale16 = 1.0f / scale16;  // correctly rounded fp32 reciprocal
+
+  for (int i = t; i < 2 * L - 1; i += kThreads) idx_tab[i] = (int16_t)relative_index(i - (L - 1), bucket_size, P);
+  // The key mask of batch row b as an additive term: 0 for a valid key, -inf
+  // (probabilities) or -65504 (the SDPA mask output) for a masked one.
+  for (int i = t; i < L; i += kThreads) {
+    const float m = (float)mask[(int64_t)b * L + i];
+    const bool valid = mask_kind == GD_MASK_ATTENTION ? (m > 0.f) : !(m < -60000.f);
+    mask_add[i] = valid ? 0.f : (OUT == GD_ATTN_OUT_BIAS ? -65504.f : -INFINITY);
+  }
+  __syncthreads();  // the stage windows below are located through the table
+
+  const half_t* Kb = K + (int64_t)b * ksb + (int64_t)h * ksh;
+  const half_t* PKh = PK + (int64_t)h * pksh;
+  const half_t* PQh = PQ + (int64_t)h * pqsh;
+  half_t* c2p_w = smem + 2 * kStage + wave * kScratchWave;
+  half_t* p2c_w = c2p_w + 16 * kC2PStride;
+
+  // Relative index of a wave-uniform r, clipped to the span of this length.
+  auto idx_clip = [&](int r) -> int {
+    r = r < -(L - 1) ? -(L - 1) : (r > L - 1 ? L - 1 : r);
+    return __builtin_amdgcn_readfirstlane((int)idx_tab[r + L - 1]);
+  };
+
+  // ---- stage loads: lane l of 1 KiB block `blk` writes physical chunk l%8 of
+  // row 8*blk + l/8, so it fetches the logical chunk that swz() puts there.
+  // Every block this wave loads has the parity of the wave index. ----
+  const int blk_row = lane >> 3;
+  const int blk_chunk = (lane & 7) ^ (((wave & 1) << 2) | (lane >> 4));
+  auto win_lo_of = [&](int kc) { return idx_clip(q0 - kc - (kKC - 1)); };
+  auto issue_stage = [&](int c, int buf) {
+    half_t* st = smem + buf * kStage;
+    const int kc = c * kKC;
+    {  // K rows: 8 blocks of 8 rows, one per wave
+      int key = kc + wave * 8 + blk_row;
+      key = key < L ? key : L - 1;
+      load_lds16(Kb + (int64_t)key * ksl + blk_chunk * 8, st + wave * 512);
+    }
+    const int wlo = win_lo_of(kc);
+#pragma unroll
+    for (int j = 0; j < kWin / 8 / kWaves; ++j) {  // 3 blocks per wave per table
+      const int blk = wave + kWaves * j;
+      int p = wlo + blk * 8 + blk_row;
+      p = p < P ? p : P - 1;
+      load_lds16(PKh + (int64_t)p * pksp + blk_chunk * 8, st + kStageK + blk * 512);
+      load_lds16(PQh + (int64_t)p * pqsp + blk_chunk * 8, st + kStageK + kStageWin + blk * 512);
+    }
+  };
+
+  // ---- Q fragments (B operand of K Q^T): Q[qw + lc][8g..] and [32 + 8g..] ----
+  half8_t qf0 = {}, qf1 = {};
+  if (active) {
+    const half_t* qrow = Q + (int64_t)b * qsb + (int64_t)h * qsh + (int64_t)(qw + lc) * qsl;
+    qf0 = *reinterpret_cast<const half8_t*>(qrow + 8 * g);
+    qf1 = *reinterpret_cast<const half8_t*>(qrow + 32 + 8 * g);
+  }
+
+  float sc[MAXT][4];
+#pragma unroll
+  for (int T = 0; T < MAXT; ++T)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sc[T][i] = -INFINITY;
+
+  issue_stage(0, 0);
+#pragma unroll
+  for (int c = 0; c < MAXT / 4; ++c) {
+    if (c >= nchunks) break;  // uniform
+    wait_vmcnt<0>();
+    __syncthreads();  // stage c landed everywhere; every wave is done with stage c - 1
+    if (c + 1 < nchunks) issue_stage(c + 1, (c + 1) & 1);
+    const half_t* st = smem + (c & 1) * kStage;
+    const half_t* Ks = st;
+    const half_t* PKs = st + kStageK;
+    const half_t* PQs = st + kStageK + kStageWin;
+    const int kc = c * kKC;
+    const int wlo = win_lo_of(kc);
+    if (active) {
+      // c2p for this wave's 16 queries and the chunk's keys
+      const int cw_lo = idx_clip(qw - kc - (kKC - 1));
+      const int cw_hi = idx_clip(qw + 15 - kc);
+      const int ntw = (cw_hi - cw_lo + 16) >> 4;  // <= 5
+#pragma unroll
+      for (int tw = 0; tw < kC2PCols / 16; ++tw) {
+        if (tw < ntw) {
+          int row = cw_lo - wlo + 16 * tw + lc;
+          row = row < kWin - 1 ? row : kWin - 1;
+          const half8_t a0 = *reinterpret_cast<const half8_t*>(PKs + swz(row, g));
+          const half8_t a1 = *reinterpret_cast<const half8_t*>(PKs + swz(row, 4 + g));
+          float4_t r = {0.f, 0.f, 0.f, 0.f};
+          r = mfma16x16x32(a0, qf0, r);
+          r = mfma16x16x32(a1, qf1, r);
+          half4_t hv;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) hv[i] = (half_t)r[i];
+          *reinterpret_cast<half4_t*>(c2p_w + lc * kC2PStride + 16 * tw + 4 * g) = hv;
+        }
+      }
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const int T = 4 * c + tt;
+        if (T < nt) {
+          const int k0 = 16 * T;
+          const half8_t ka0 = *reinterpret_cast<const half8_t*>(Ks + swz(16 * tt + lc, g));
+          const half8_t ka1 = *reinterpret_cast<const half8_t*>(Ks + swz(16 * tt + lc, 4 + g));
+          float4_t s = {0.f, 0.f, 0.f, 0.f};
+          s = mfma16x16x32(ka0, qf0, s);
+          s = mfma16x16x32(ka1, qf1, s);
+          const int pp_lo = idx_clip(qw - k0 - 15);
+          const int pp_hi = idx_clip(qw - k0 + 15);
+          const int nj = (pp_hi - pp_lo + 16) >> 4;  // 1 or 2
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            if (j < nj) {
+              int row = pp_lo - wlo + 16 * j + lc;
+              row = row < kWin - 1 ? row : kWin - 1;
+              const half8_t b0 = *reinterpret_cast<const half8_t*>(PQs + swz(row, g));
+              const half8_t b1 = *reinterpret_cast<const half8_t*>(PQs + swz(row, 4 + g));
+              float4_t r = {0.f, 0.f, 0.f, 0.f};
+              r = mfma16x16x32(ka0, b0, r);
+              r = mfma16x16x32(ka1, b1, r);
+#pragma unroll
+              for (int i = 0; i < 4; ++i) p2c_w[(4 * g + i) * kP2CStride + 16 * j + lc] = (half_t)r[i];
+            }
+          }
+          wave_lds_sync();
+          // Gather the two terms of score (q = qw + lc, k = k0 + 4g + i) at
+          // idx(q - k).  In the linear zone (|q - k| <= 128 over the whole
+          // tile) idx = q - k + 256, so both addresses are a per-lane base plus
+          // a constant per i (folded into the LDS instruction's offset).
+          const float4_t madd = *reinterpret_cast<const float4_t*>(mask_add + k0 + 4 * g);
+          half_t c2p[4], p2c[4];
+          if ((qw - k0 <= 113) && (k0 - qw <= 113)) {
+            const int d0 = qw - k0 + bucket_size + lc - 4 * g;  // id at i = 0
+            const half_t* cp = c2p_w + lc * kC2PStride + (d0 - cw_lo);
+            const half_t* pp = p2c_w + 4 * g * kP2CStride + (d0 - pp_lo);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              c2p[i] = cp[-i];
+              p2c[i] = pp[i * (kP2CStride - 1)];
+            }
+          } else {
+            const int r0 = qw + lc - k0 - 4 * g + L - 1;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int id = idx_tab[r0 - i];
+              c2p[i] = c2p_w[lc * kC2PStride + (id - cw_lo)];
+              p2c[i] = p2c_w[(4 * g + i) * kP2CStride + (id - pp_lo)];
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            // fp16(c2p + p2c) is the fp16 add; the division by fp16(sqrt(3D)) is a
+            // multiply by its fp32 reciprocal, which rounds to the same fp16 value
+            // for every finite fp16 numerator (checked exhaustively).
+            const half_t sum16 = c2p[i] + p2c[i];
+            const float bias16 = round_f16((float)sum16 * inv_scale16);
+            if (OUT == GD_ATTN_OUT_BIAS)
+              sc[T][i] = round_f16(bias16 + madd[i]);
+            else
+              sc[T][i] = fmaf(s[i], scale_qk, bias16) + madd[i];
+          }
+          wave_lds_sync();
+        }
+      }
+    }
+  }
+  __syncthreads();  // the stage buffers are free from here on
+
+  if (OUT != GD_ATTN_OUT_BIAS) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int T = 0; T < MAXT; ++T)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[T][i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mref = mx == -INFINITY ? 0.f : mx;
+    constexpr float kLog2e = 1.4426950408889634f;
+    float sum = 0.f;
+#pragma unroll
+    for (int T = 0; T < MAXT; ++T)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = __builtin_amdgcn_exp2f((sc[T][i] - mref) * kLog2e);  // v_exp_f32; exp2(-inf) = 0
+        sc[T][i] = e;
+        sum += e;
+      }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    const float inv = sum > 0.f ? 1.0f / sum : 0.f;
+#pragma unroll
+    for (int T = 0; T < MAXT; ++T)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sc[T][i] *= inv;
+  }
+
+  if (OUT == GD_ATTN_OUT_PROBS || OUT == GD_ATTN_OUT_BIAS) {
+    // Stage this wave's 16 rows x L in LDS, then write 16-byte row segments.
+    half_t* rows = smem + wave * 16 * (16 * MAXT);
+    if (active) {
+#pragma unroll
+      for (int T = 0; T < MAXT; ++T)
+        if (T < nt) {
+          half4_t v;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] = (half_t)sc[T][i];
+          *reinterpret_cast<half4_t*>(rows + lc * L + 16 * T + 4 * g) = v;
+        }
+      wave_lds_sync();
+      const int per_row = L / 8;  // 16-byte pieces per row
+      for (int pce = lane; pce < 16 * per_row; pce += 64) {
+        const int r = pce / per_row, cpos = pce - r * per_row;
+        *reinterpret_cast<half8_t*>(out + (((int64_t)b * H + h) * L + qw + r) * L + cpos * 8) =
+            *reinterpret_cast<const half8_t*>(rows + r * L + cpos * 8);
+      }
+    }
+    return;
+  }
+
+  // ---- context: O = P V; V^T chunks in LDS, P (hi + lo) as the A operand ----
+  float4_t o[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) o[dt] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  const half_t* Vb = V + (int64_t)b * vsb + (int64_t)h * vsh;
+  const int vrow = t >> 3, vch = t & 7;  // one 16-byte piece of the 64 x 64 chunk per thread
+  half8_t vnext = {};
+  if (vrow < L) vnext = *reinterpret_cast<const half8_t*>(Vb + (int64_t)vrow * vsl + 8 * vch);
+#pragma unroll
+  for (int c = 0; c < MAXT / 4; ++c) {
+    if (c >= nchunks) break;
+    half_t* vt = smem + (c & 1) * (kD * kVtStride);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vt[(8 * vch + e) * kVtStride + vrow] = vnext[e];
+    if (c + 1 < nchunks) {
+      const int key = (c + 1) * kKC + vrow;
+      vnext = key < L ? *reinterpret_cast<const half8_t*>(Vb + (int64_t)key * vsl + 8 * vch) : half8_t{};
+    }
+    __syncthreads();
+    if (active) {
+#pragma unroll
+      for (int tt = 0; tt < 4; tt += 2) {
+        const int T = 4 * c + tt;
+        if (T < nt) {
+          half8_t pa, pl;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float p0 = sc[T][i];
+            const float p1 = (T + 1 < nt) ? sc[T + 1][i] : 0.f;
+            pa[i] = (half_t)p0;
+            pa[4 + i] = (half_t)p1;
+            pl[i] = (half_t)(p0 - (float)pa[i]);
+            pl[4 + i] = (half_t)(p1 - (float)pa[4 + i]);
+          }
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) {
+            const half_t* vr = vt + (16 * dt + lc) * kVtStride;
+            const half4_t v0 = *reinterpret_cast<const half4_t*>(vr + 16 * tt + 4 * g);
+            const half4_t v1 = *reinterpret_cast<const half4_t*>(vr + 16 * (tt + 1) + 4 * g);
+            half8_t vb;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              vb[i] = v0[i];
+              vb[4 + i] = v1[i];
+            }
+            o[dt] = mfma16x16x32(pa, vb, o[dt]);
+            o[dt] = mfma16x16x32(pl, vb, o[dt]);
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (!active) return;
+  // lane holds O[qw + 4g + i][16 dt + lc]: stage 16 x 64 in LDS, write 128-byte rows
+  half_t* ot = smem + 2 * (kD * kVtStride) + wave * 16 * 72;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) ot[(4 * g + i) * 72 + 16 * dt + lc] = (half_t)o[dt][i];
+  wave_lds_sync();
+  {
+    const int r = lane >> 3, cpos = lane & 7;  // 8 rows x 8 pieces per pass
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+      const int row = r + 8 * pass;
+      *reinterpret_cast<half8_t*>(out + ((int64_t)b * L + qw + row) * ldo + (int64_t)h * kD + cpos * 8) =
+          *reinterpret_cast<const half8_t*>(ot + row * 72 + cpos * 8);
+    }
+  }
+}
+
+template <int MAXT>
+int launch2(const AttentionArgs& a, hipStream_t stream) {
+  const int ntq = (int)((a.L + kQT - 1) / kQT);
+  const dim3 grid((unsigned)(a.B * a.H * ntq)), block(kThreads);
+  auto hq = static_cast<const half_t*>(a.q);
+  auto hk = static_cast<const half_t*>(a.k);
+  auto hv = static_cast<const half_t*>(a.v);
+  auto hpk = static_cast<const half_t*>(a.pk);
+  auto hpq = static_cast<const half_t*>(a.pq);
+  auto hm = static_cast<const half_t*>(a.mask);
+  auto ho = static_cast<half_t*>(a.out);
+#define GD_ATTN2(OUTK)                                                                                             \
+  hipLaunchKernelGGL((deberta_attention2_kernel<MAXT, OUTK>), grid, block, 0, stream, hq, hk, hv, a.qsb, a.qsh,      \
+                     a.qsl, a.ksb, a.ksh, a.ksl, a.vsb, a.vsh, a.vsl, hpk, hpq, a.pksh, a.pksp, a.pqsh, a.pqsp, hm,  \
+                     a.mask_kind, (int)a.B, (int)a.H, (int)a.L, (int)a.P, a.bucket_size, a.scale_qk, a.scale16, ho, \
+                     a.ldo)
+  switch (a.output) {
+    case GD_ATTN_OUT_PROBS:
+      GD_ATTN2(GD_ATTN_OUT_PROBS);
+      break;
+    case GD_ATTN_OUT_CONTEXT:
+      GD_ATTN2(GD_ATTN_OUT_CONTEXT);
+      break;
+    default:
+      GD_ATTN2(GD_ATTN_OUT_BIAS);
+      break;
+  }
+#undef GD_ATTN2
+  GD_LAUNCH_CHECK();
+  return GD_OK;
+}
+
+}  // namespace
+
+int launch_deberta_attention2(const AttentionArgs& a, hipStream_t stream) {
+  if (a.L <= 64) return launch2<4>(a, stream);
+  if (a.L <= 128) return launch2<8>(a, stream);
+  if (a.L <= 256) return launch2<16>(a, stream);
+  return launch2<32>(a, stream);
+}
+
+}  // namespace gd

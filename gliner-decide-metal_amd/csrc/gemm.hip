@@ -11,8 +11,8 @@
 //   * global -> registers -> LDS, double-buffered: the loads of step k+1 are
 //     in flight while the MFMAs of step k run;
 //   * LDS rows are 128 B (64 halfs) with the 16-byte chunk index XOR-swizzled
-//     by (row & 7), so the fragment reads of 8 consecutive rows hit 8
-//     different chunk positions (no bank conflicts on ds_read_b128);
+//     by bits 1..3 of the row, so a fragment read of 16 consecutive rows
+//     covers all 64 banks once (no conflicts on ds_read_b128);
 //   * each wave runs v_mfma_f32_32x32x16_f16 over a (BM/2) x (BN/2) sub-tile
 //     with fp32 accumulators;
 //   * the epilogue adds the bias, rounds to fp16 (the addMM output), applies
@@ -33,7 +33,19 @@ constexpr int kBK = 64;
 constexpr int kThreads = 256;
 constexpr int kGroupM = 4;  // tile rows per band of the tile order
 
-__device__ __forceinline__ int lds_swz(int row, int chunk) { return row * kBK + ((chunk ^ (row & 7)) << 3); }
+// 128-byte LDS rows; the 16-byte chunk index is XORed with bits 1..3 of the
+// row.  gfx950's LDS serves ds_read_b128 16 lanes at a time over 64 banks
+// (256 B), and a fragment read has 16 consecutive rows at one logical chunk:
+// their (row parity, physical chunk) pairs are all distinct -- no conflicts.
+__device__ __forceinline__ int lds_swz(int row, int chunk) {
+  return row * kBK + ((chunk ^ ((row >> 1) & 7)) << 3);
+}
+
+// Logical chunk fetched by lane `lane` of the 1 KiB direct-to-LDS block `blk`
+// (8 rows): it lands at physical chunk lane%8 of row 8*blk + lane/8.
+__device__ __forceinline__ int dma_chunk(int lane, int blk) {
+  return (lane & 7) ^ (((blk & 1) << 2) | (lane >> 4));
+}
 
 __device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f)); }
 
@@ -166,14 +178,19 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(const half_t* __restr
 //
 // Each K step of 64 is fetched with global_load_lds_dwordx4: one instruction
 // moves 1 KiB (64 lanes x 16 B) straight into LDS at M0 + 16*lane, so no
-// VGPRs stage the tiles and the loads of step k+1 run under the MFMAs of step
-// k.  The XOR swizzle is applied on the global side: lane l of a 1 KiB block
-// (8 rows of 128 B) fetches logical chunk (l%8) ^ (l/8) of row l/8, which
-// lands at physical chunk l%8 -- the same layout lds_swz() reads.  One
-// barrier per K step: wait for this thread's step-k loads, barrier (all
-// loads landed, all waves done with step k-1), issue step k+1 into the other
-// buffer, compute step k.  The epilogue stages the fp16 tile through LDS and
-// writes 16-byte coalesced row segments.
+// VGPRs stage the tiles.  The XOR swizzle is applied on the global side: lane
+// l of a 1 KiB block (8 rows of 128 B) fetches the logical chunk dma_chunk()
+// names for row l/8, which lands at physical chunk l%8 -- the layout
+// lds_swz() reads.  Two LDS buffers: step k+1 is in flight while step k is
+// computed.
+//
+// The MFMA operands are double-buffered in registers as well: the fragments
+// of K slice s+1 (16 deep) are read from LDS while the MFMAs of slice s run,
+// so a wave never waits on LDS latency in front of its MFMAs.  One barrier per
+// K step, placed before the last slice's MFMAs: by then every wave holds its
+// slice-3 fragments in registers, the buffer can be refilled (step k+2), and
+// slice 0 of step k+1 is read under the remaining MFMAs.  The epilogue stages
+// the fp16 tile through LDS and writes 16-byte coalesced row segments.
 // ---------------------------------------------------------------------------
 constexpr int kThreads8 = 512;
 
@@ -190,7 +207,7 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | (((N >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-template <int BM, int BN, int WAVES_M, int NSTAGE, int EPI>
+template <int BM, int BN, int WAVES_M, int EPI>
 __global__ __launch_bounds__(kThreads8) void gemm_nt_lds_kernel(const half_t* __restrict__ A,
                                                                 const half_t* __restrict__ W,
                                                                 const half_t* __restrict__ bias,
@@ -203,10 +220,8 @@ __global__ __launch_bounds__(kThreads8) void gemm_nt_lds_kernel(const half_t* __
   constexpr int A_BLK = BM / 8 / NW, B_BLK = BN / 8 / NW;  // 1 KiB blocks per wave per K step
   constexpr int STAGE = (BM + BN) * kBK;                   // halfs per buffer
   static_assert(TM >= 1 && TN >= 1 && A_BLK >= 1 && B_BLK >= 1, "tile shape");
-  constexpr int LPS = A_BLK + B_BLK;                       // loads per thread per K step
-  static_assert(NSTAGE >= 2 && NSTAGE <= 4, "pipeline depth");
-  static_assert(NSTAGE * STAGE >= BM * BN, "epilogue staging must fit in the pipeline buffers");
-  __shared__ __attribute__((aligned(1024))) half_t smem[NSTAGE * STAGE];
+  static_assert(2 * STAGE >= BM * BN, "epilogue staging must fit in the pipeline buffers");
+  __shared__ __attribute__((aligned(1024))) half_t smem[2 * STAGE];
 
   const int nwg = tiles_m * tiles_n;
   int bid = blockIdx.x;
@@ -220,25 +235,26 @@ __global__ __launch_bounds__(kThreads8) void gemm_nt_lds_kernel(const half_t* __
 
   const int t = threadIdx.x;
   const int lane = t & 63;
-  const int wave = t >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int lr = lane & 31, lk = lane >> 5;
 
   // Source pointers of this lane's 16-byte pieces (fixed across K).
-  const int blk_row = lane >> 3;                       // row within a 1 KiB block
-  const int blk_chunk = (lane & 7) ^ blk_row;          // logical chunk it fetches
+  const int blk_row = lane >> 3;  // row within a 1 KiB block
   const half_t* a_src[A_BLK];
   const half_t* b_src[B_BLK];
 #pragma unroll
   for (int j = 0; j < A_BLK; ++j) {
-    int m = tile_m * BM + (wave * A_BLK + j) * 8 + blk_row;
+    const int blk = wave * A_BLK + j;
+    int m = tile_m * BM + blk * 8 + blk_row;
     m = m < M ? m : M - 1;
-    a_src[j] = A + (int64_t)m * lda + blk_chunk * 8;
+    a_src[j] = A + (int64_t)m * lda + dma_chunk(lane, blk) * 8;
   }
 #pragma unroll
   for (int j = 0; j < B_BLK; ++j) {
-    const int n = tile_n * BN + (wave * B_BLK + j) * 8 + blk_row;
-    b_src[j] = W + (int64_t)n * K + blk_chunk * 8;
+    const int blk = wave * B_BLK + j;
+    const int n = tile_n * BN + blk * 8 + blk_row;
+    b_src[j] = W + (int64_t)n * K + dma_chunk(lane, blk) * 8;
   }
   auto issue = [&](int k0, int buf) {
     half_t* As = smem + buf * STAGE;
@@ -257,39 +273,66 @@ __global__ __launch_bounds__(kThreads8) void gemm_nt_lds_kernel(const half_t* __
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  const int nk = K / kBK;
-  // Prologue: NSTAGE - 1 K steps in flight.
-#pragma unroll
-  for (int s = 0; s < NSTAGE - 1; ++s)
-    if (s < nk) issue(s * kBK, s);
-  for (int kt = 0; kt < nk; ++kt) {
-    // Step kt has landed once at most `pending` later steps are outstanding.
-    const int pending = min(NSTAGE - 2, nk - 1 - kt);
-    if (pending <= 0) {
-      wait_vmcnt<0>();
-    } else if (NSTAGE == 3 || pending == 1) {
-      wait_vmcnt<LPS>();
-    } else if (pending == 2) {
-      wait_vmcnt<(NSTAGE >= 4 ? 2 * LPS : 0)>();
-    }
-    __syncthreads();  // all pieces of step kt landed; all waves finished step kt - 1
-    if (kt + NSTAGE - 1 < nk) issue((kt + NSTAGE - 1) * kBK, (kt + NSTAGE - 1) % NSTAGE);
-    const half_t* As = smem + (kt % NSTAGE) * STAGE;
+  // Fragment sets: fa[set][i] = A rows of MFMA tile i, fb[set][j] = W rows of tile j.
+  half8_t fa[2][TM], fb[2][TN];
+  auto read_frags = [&](int buf, int slice, int set) {
+    const half_t* As = smem + buf * STAGE;
     const half_t* Bs = As + BM * kBK;
 #pragma unroll
-    for (int s = 0; s < kBK / 16; ++s) {
-      half8_t fa[TM], fb[TN];
+    for (int i = 0; i < TM; ++i)
+      fa[set][i] = *reinterpret_cast<const half8_t*>(As + lds_swz(wm * WM + i * 32 + lr, 2 * slice + lk));
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-        fa[i] = *reinterpret_cast<const half8_t*>(As + lds_swz(wm * WM + i * 32 + lr, 2 * s + lk));
+    for (int j = 0; j < TN; ++j)
+      fb[set][j] = *reinterpret_cast<const half8_t*>(Bs + lds_swz(wn * WN + j * 32 + lr, 2 * slice + lk));
+  };
+  auto mma = [&](int set) {
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
-        fb[j] = *reinterpret_cast<const half8_t*>(Bs + lds_swz(wn * WN + j * 32 + lr, 2 * s + lk));
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+      for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16(fa[set][i], fb[set][j], acc[i][j]);
+  };
+  // Issue order of a [read slice s+1][MFMAs of slice s] block: MFMAs and
+  // fragment reads alternate from the block's start (an MFMA first, so the
+  // wait for slice s's operands covers only reads issued a block earlier),
+  // then the remaining MFMAs follow; a sched_barrier closes the block.
+  auto interleave = [&]() {
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16(fa[i], fb[j], acc[i][j]);
+    for (int r = 0; r < TM + TN; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
     }
+    if constexpr (TM * TN > TM + TN) __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - (TM + TN), 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  const int nk = K / kBK;
+  issue(0, 0);
+  wait_vmcnt<0>();
+  __syncthreads();
+  if (nk > 1) issue(kBK, 1);
+  read_frags(0, 0, 0);
+  // Without the explicit block order the scheduler folds the two fragment
+  // sets into one and puts an lgkmcnt(0) wait in front of every MFMA group.
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    read_frags(buf, 1, 1);
+    mma(0);
+    interleave();
+    read_frags(buf, 2, 0);
+    mma(1);
+    interleave();
+    read_frags(buf, 3, 1);
+    mma(0);
+    interleave();
+    if (kt + 1 < nk) {
+      // Step kt + 1 has landed (its loads were issued one step ago); after the
+      // barrier every wave holds its slice-3 fragments, so buffer `buf` is free.
+      wait_vmcnt<0>();
+      __syncthreads();
+      if (kt + 2 < nk) issue((kt + 2) * kBK, buf);
+      read_frags(buf ^ 1, 0, 0);
+    }
+    mma(1);
   }
   __syncthreads();  // all waves done reading the pipeline buffers
 
@@ -319,7 +362,7 @@ __global__ __launch_bounds__(kThreads8) void gemm_nt_lds_kernel(const half_t* __
   }
 }
 
-template <int BM, int BN, int WAVES_M, int NSTAGE>
+template <int BM, int BN, int WAVES_M>
 int launch_lds_tile(const half_t* A, const half_t* W, const half_t* bias, half_t* C, int M, int N, int K, int64_t lda,
                     int64_t ldc, int epi, hipStream_t stream) {
   const int tiles_m = (M + BM - 1) / BM;
@@ -327,20 +370,20 @@ int launch_lds_tile(const half_t* A, const half_t* W, const half_t* bias, half_t
   const dim3 grid(tiles_m * tiles_n), block(kThreads8);
   switch (epi) {
     case GD_EPI_NONE:
-      hipLaunchKernelGGL((gemm_nt_lds_kernel<BM, BN, WAVES_M, NSTAGE, GD_EPI_NONE>), grid, block, 0, stream, A, W, bias, C, M,
-                         N, K, lda, ldc, tiles_m, tiles_n);
+      hipLaunchKernelGGL((gemm_nt_lds_kernel<BM, BN, WAVES_M, GD_EPI_NONE>), grid, block, 0, stream, A, W, bias, C, M, N,
+                         K, lda, ldc, tiles_m, tiles_n);
       break;
     case GD_EPI_BIAS:
-      hipLaunchKernelGGL((gemm_nt_lds_kernel<BM, BN, WAVES_M, NSTAGE, GD_EPI_BIAS>), grid, block, 0, stream, A, W, bias, C, M,
-                         N, K, lda, ldc, tiles_m, tiles_n);
+      hipLaunchKernelGGL((gemm_nt_lds_kernel<BM, BN, WAVES_M, GD_EPI_BIAS>), grid, block, 0, stream, A, W, bias, C, M, N,
+                         K, lda, ldc, tiles_m, tiles_n);
       break;
     case GD_EPI_BIAS_GELU:
-      hipLaunchKernelGGL((gemm_nt_lds_kernel<BM, BN, WAVES_M, NSTAGE, GD_EPI_BIAS_GELU>), grid, block, 0, stream, A, W, bias,
-                         C, M, N, K, lda, ldc, tiles_m, tiles_n);
+      hipLaunchKernelGGL((gemm_nt_lds_kernel<BM, BN, WAVES_M, GD_EPI_BIAS_GELU>), grid, block, 0, stream, A, W, bias, C, M,
+                         N, K, lda, ldc, tiles_m, tiles_n);
       break;
     default:
-      hipLaunchKernelGGL((gemm_nt_lds_kernel<BM, BN, WAVES_M, NSTAGE, GD_EPI_BIAS_RELU>), grid, block, 0, stream, A, W, bias,
-                         C, M, N, K, lda, ldc, tiles_m, tiles_n);
+      hipLaunchKernelGGL((gemm_nt_lds_kernel<BM, BN, WAVES_M, GD_EPI_BIAS_RELU>), grid, block, 0, stream, A, W, bias, C, M,
+                         N, K, lda, ldc, tiles_m, tiles_n);
       break;
   }
   GD_LAUNCH_CHECK();
@@ -405,8 +448,8 @@ int launch_linear(const void* a, const void* w, const void* bias, void* c, int64
     // 256 x 256 tiles when they fill whole waves of the 256 CUs, else 256 x 128.
     const int t256 = ((M + 255) / 256) * (N / 256);
     if (N % 256 == 0 && (t256 % 256 == 0 || t256 >= 512))
-      return launch_lds_tile<256, 256, 2, 2>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
-    return launch_lds_tile<256, 128, 4, 3>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
+      return launch_lds_tile<256, 256, 2>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
+    return launch_lds_tile<256, 128, 4>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
   }
   if (M >= 4096) return launch_tile<256, 128, false>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
   if (M >= 1024) return launch_tile<128, 128, false>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);

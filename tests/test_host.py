@@ -48,6 +48,20 @@ def test_buckets_and_chunks():
     assert valid == 4 and chunk["x"].shape == (4, 2)
 
 
+def test_bias_division_by_reciprocal_is_exact():
+    """The attention kernel divides the fp16 bias sum by fp16(sqrt(192)) =
+    13.859375 as a multiply by the fp32 reciprocal.  For every finite fp16
+    numerator the fp16 result equals the correctly rounded quotient."""
+    s = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    s = s[np.isfinite(s)]
+    scale = np.float16(math.sqrt(192.0))
+    assert float(scale) == 13.859375
+    exact = (s.astype(np.float64) / float(scale)).astype(np.float16)
+    recip = np.float32(1.0) / np.float32(scale)
+    via_mul = (s.astype(np.float32) * recip).astype(np.float16)
+    np.testing.assert_array_equal(via_mul.view(np.uint16), exact.view(np.uint16))
+
+
 def test_synthetic_weights_are_subset_stable():
     cfg = DeBERTaV2Configuration(hidden_size=128, intermediate_size=256, num_hidden_layers=3, num_attention_heads=2,
                                  vocab_size=64, classifier_hidden=128)
