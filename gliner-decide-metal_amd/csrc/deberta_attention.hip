@@ -1,4 +1,4 @@
-// Disentangled attention, staged design (the encoder's attention kernel).
+// Disentangled attention of the DeBERTa-v3 encoder (the hot path).
 //
 // Reference: DeBERTa.swift:322-395 (relative bias from the fp16 c2pRaw/p2cRaw
 // gathers, additive key mask, SDPA) with the index math of :498-551.
@@ -73,7 +73,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 template <int MAXT, int OUT>
-__global__ __launch_bounds__(kThreads) void deberta_attention2_kernel(
+__global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K, const half_t* __restrict__ V, int64_t qsb, int64_t qsh,
     int64_t qsl, int64_t ksb, int64_t ksh, int64_t ksl, int64_t vsb, int64_t vsh, int64_t vsl,
     const half_t* __restrict__ PK, const half_t* __restrict__ PQ, int64_t pksh, int64_t pksp, int64_t pqsh,
@@ -407,7 +407,7 @@ int launch2(const AttentionArgs& a, hipStream_t stream) {
   auto hm = static_cast<const half_t*>(a.mask);
   auto ho = static_cast<half_t*>(a.out);
 #define GD_ATTN2(OUTK)                                                                                             \
-  hipLaunchKernelGGL((deberta_attention2_kernel<MAXT, OUTK>), grid, block, 0, stream, hq, hk, hv, a.qsb, a.qsh,      \
+  hipLaunchKernelGGL((deberta_attention_kernel<MAXT, OUTK>), grid, block, 0, stream, hq, hk, hv, a.qsb, a.qsh,      \
                      a.qsl, a.ksb, a.ksh, a.ksl, a.vsb, a.vsh, a.vsl, hpk, hpq, a.pksh, a.pksp, a.pqsh, a.pqsp, hm,  \
                      a.mask_kind, (int)a.B, (int)a.H, (int)a.L, (int)a.P, a.bucket_size, a.scale_qk, a.scale16, ho, \
                      a.ldo)
@@ -429,7 +429,7 @@ int launch2(const AttentionArgs& a, hipStream_t stream) {
 
 }  // namespace
 
-int launch_deberta_attention2(const AttentionArgs& a, hipStream_t stream) {
+int launch_deberta_attention(const AttentionArgs& a, hipStream_t stream) {
   if (a.L <= 64) return launch2<4>(a, stream);
   if (a.L <= 128) return launch2<8>(a, stream);
   if (a.L <= 256) return launch2<16>(a, stream);

@@ -38,7 +38,6 @@ struct AttentionArgs {
 };
 
 int launch_deberta_attention(const AttentionArgs& args, hipStream_t stream);
-int launch_deberta_attention2(const AttentionArgs& args, hipStream_t stream);
 
 int launch_relative_bias_general(const void* q, const void* k, const void* pos_key, const void* pos_query,
                                  const int32_t* c2p, const int32_t* p2c, const void* key_mask, float scale, int64_t B,

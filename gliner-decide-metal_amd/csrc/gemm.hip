@@ -21,7 +21,7 @@
 //   * workgroups are dispatched round-robin over the 8 XCDs; the tile order is
 //     remapped so each XCD works on a compact 4-tile-row band and its private
 //     L2 serves the A rows and W columns it shares.
-#include <cstdlib>
+#include <type_traits>
 
 #include "gd_common.hpp"
 #include "gd_kernels.hpp"
@@ -47,7 +47,31 @@ __device__ __forceinline__ int dma_chunk(int lane, int blk) {
   return (lane & 7) ^ (((blk & 1) << 2) | (lane >> 4));
 }
 
-__device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f)); }
+// GELU(y) = 0.5 y (1 + erf(y / sqrt 2)), evaluated through erfc so neither tail
+// cancels: with z = |y| / sqrt 2, GELU = y - 0.5 y erfc(z) for y >= 0 and
+// 0.5 y erfc(z) for y < 0.  erfc is the Chebyshev fit of Numerical Recipes in
+// C (2nd ed., section 6.2, "erfcc"): t = 1 / (1 + z / 2),
+// erfc(z) = t exp(-z^2 + P(t)), fractional error below 1.2e-7 for all z >= 0.
+// One reciprocal, one exp2 and ten FMAs, no branches.  Over every finite fp16
+// input the fp16 result matches the correctly rounded GELU except for a few
+// values within ~2e-6 of a rounding boundary (1 ulp).
+__device__ __forceinline__ float gelu_erf(float y) {
+  const float z = fabsf(y) * 0.70710678118654752f;
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, z, 1.0f));
+  float p = 0.17087277f;
+  p = fmaf(p, t, -0.82215223f);
+  p = fmaf(p, t, 1.48851587f);
+  p = fmaf(p, t, -1.13520398f);
+  p = fmaf(p, t, 0.27886807f);
+  p = fmaf(p, t, -0.18628806f);
+  p = fmaf(p, t, 0.09678418f);
+  p = fmaf(p, t, 0.37409196f);
+  p = fmaf(p, t, 1.00002368f);
+  p = fmaf(p, t, -1.26551223f);
+  const float e = t * __builtin_amdgcn_exp2f(fmaf(-z, z, p) * 1.4426950408889634f);  // erfc(z)
+  const float h = 0.5f * y * e;
+  return y >= 0.f ? (e > 0.f ? y - h : y) : h;  // e == 0: y = +inf or erfc underflowed
+}
 
 template <int EPI>
 __device__ __forceinline__ half_t epilogue(float acc, float b) {
@@ -174,23 +198,29 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(const half_t* __restr
 }
 
 // ---------------------------------------------------------------------------
-// Large-M kernel: 8 waves (two per SIMD), direct global -> LDS loads.
+// Large-M kernel: 8 waves (two per SIMD), direct global -> LDS loads through an
+// NSTAGE-deep pipeline of BK-wide K steps.
 //
-// Each K step of 64 is fetched with global_load_lds_dwordx4: one instruction
-// moves 1 KiB (64 lanes x 16 B) straight into LDS at M0 + 16*lane, so no
-// VGPRs stage the tiles.  The XOR swizzle is applied on the global side: lane
-// l of a 1 KiB block (8 rows of 128 B) fetches the logical chunk dma_chunk()
-// names for row l/8, which lands at physical chunk l%8 -- the layout
-// lds_swz() reads.  Two LDS buffers: step k+1 is in flight while step k is
-// computed.
+// Each 1 KiB piece of a stage is fetched with global_load_lds_dwordx4 (64
+// lanes x 16 B straight into LDS at M0 + 16*lane), so no VGPRs stage the
+// tiles.  The XOR swizzle is applied on the global side: lane l of a block
+// fetches the logical chunk that lands, at its physical position, where
+// StageLayout::offset() reads it.
 //
-// The MFMA operands are double-buffered in registers as well: the fragments
-// of K slice s+1 (16 deep) are read from LDS while the MFMAs of slice s run,
-// so a wave never waits on LDS latency in front of its MFMAs.  One barrier per
-// K step, placed before the last slice's MFMAs: by then every wave holds its
-// slice-3 fragments in registers, the buffer can be refilled (step k+2), and
-// slice 0 of step k+1 is read under the remaining MFMAs.  The epilogue stages
-// the fp16 tile through LDS and writes 16-byte coalesced row segments.
+// Every stage is its own __shared__ array and the K loop is unrolled by
+// NSTAGE, so each LDS access names its buffer at compile time.  That is what
+// lets the compiler wait only for the DMA into the buffer being read instead
+// of for every load in flight (vmcnt(0)); likewise the stage barrier is a bare
+// s_barrier behind explicit waits -- __syncthreads() would also drain all
+// loads in flight and collapse the pipeline to one stage.
+//
+// Per K step: the fragments of K slice s+1 are read while the MFMAs of slice
+// s run (register double buffering); before the last slice's MFMAs each wave
+// waits for its own loads of the next stage, the barrier makes every wave's
+// loads visible and frees this stage's buffer, the buffer is refilled with
+// the step NSTAGE ahead, and slice 0 of the next stage is read under the
+// remaining MFMAs.  The epilogue stages the fp16 tile through the stage
+// buffers and writes 16-byte coalesced row segments.
 // ---------------------------------------------------------------------------
 constexpr int kThreads8 = 512;
 
@@ -207,21 +237,76 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | (((N >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-template <int BM, int BN, int WAVES_M, int EPI>
+// Workgroup barrier for the pipeline: this wave's LDS reads are complete
+// (lgkmcnt(0)); global loads are waited for explicitly by the caller.  The
+// empty asm statements keep the compiler from moving memory accesses across.
+__device__ __forceinline__ void stage_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// LDS layout of one operand tile: rows of BK halfs; the 16-byte chunk index
+// is XORed with the row's position inside its 256-byte bank line group, so a
+// fragment read (16 consecutive rows, one logical chunk, per ds_read_b128
+// pass over gfx950's 64 banks) touches every bank once.
+template <int BK>
+struct StageLayout {
+  static constexpr int kChunks = BK / 8;             // 16-byte chunks per row
+  static constexpr int kRowsPer256 = 256 / (BK * 2);  // rows sharing one pass of the banks
+  static constexpr int kRowsPerBlock = 1024 / (BK * 2);
+  __device__ static __forceinline__ int offset(int row, int chunk) {
+    return row * BK + ((chunk ^ ((row / kRowsPer256) & (kChunks - 1))) << 3);
+  }
+  // Logical chunk that lane `lane` of 1 KiB block `blk` must fetch: the lane
+  // writes physical chunk lane % kChunks of row blk * kRowsPerBlock + lane / kChunks.
+  __device__ static __forceinline__ int dma_chunk(int lane, int blk) {
+    const int row = blk * kRowsPerBlock + lane / kChunks;
+    return (lane % kChunks) ^ ((row / kRowsPer256) & (kChunks - 1));
+  }
+};
+
+template <int V>
+using ic = std::integral_constant<int, V>;
+
+template <int BM, int BN, int WAVES_M, int BK, int NSTAGE, int EPI>
 __global__ __launch_bounds__(kThreads8) void gemm_nt_lds_kernel(const half_t* __restrict__ A,
                                                                 const half_t* __restrict__ W,
                                                                 const half_t* __restrict__ bias,
                                                                 half_t* __restrict__ C, int M, int N, int K,
                                                                 int64_t lda, int64_t ldc, int tiles_m, int tiles_n) {
+  using Lay = StageLayout<BK>;
   constexpr int NW = 8;
   constexpr int WAVES_N = NW / WAVES_M;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int A_BLK = BM / 8 / NW, B_BLK = BN / 8 / NW;  // 1 KiB blocks per wave per K step
-  constexpr int STAGE = (BM + BN) * kBK;                   // halfs per buffer
+  constexpr int A_BLK = BM / Lay::kRowsPerBlock / NW;  // 1 KiB blocks per wave per stage
+  constexpr int B_BLK = BN / Lay::kRowsPerBlock / NW;
+  constexpr int LPS = A_BLK + B_BLK;                    // loads per wave per stage
+  constexpr int STAGE = (BM + BN) * BK;                 // halfs per stage buffer
+  constexpr int S = BK / 16;                            // MFMA K slices per stage
+  constexpr int RPA = STAGE / BN;                       // epilogue rows per stage buffer
   static_assert(TM >= 1 && TN >= 1 && A_BLK >= 1 && B_BLK >= 1, "tile shape");
-  static_assert(2 * STAGE >= BM * BN, "epilogue staging must fit in the pipeline buffers");
-  __shared__ __attribute__((aligned(1024))) half_t smem[2 * STAGE];
+  static_assert(S % 2 == 0, "fragment sets alternate per slice");
+  static_assert(NSTAGE >= 2 && NSTAGE <= 5, "pipeline depth");
+  static_assert(NSTAGE * STAGE * 2 <= 160 * 1024, "LDS budget");
+  static_assert(RPA % 32 == 0 && NSTAGE * RPA >= BM, "epilogue staging must fit in the stage buffers");
+  static_assert((NSTAGE - 1) * LPS < 64, "vmcnt range");
+
+  __shared__ __attribute__((aligned(1024))) half_t st0[STAGE];
+  __shared__ __attribute__((aligned(1024))) half_t st1[STAGE];
+  __shared__ __attribute__((aligned(1024))) half_t st2[NSTAGE > 2 ? STAGE : 8];
+  __shared__ __attribute__((aligned(1024))) half_t st3[NSTAGE > 3 ? STAGE : 8];
+  __shared__ __attribute__((aligned(1024))) half_t st4[NSTAGE > 4 ? STAGE : 8];
+  auto stage = [&](auto b) -> half_t* {
+    constexpr int B = decltype(b)::value;
+    if constexpr (B == 0) return st0;
+    else if constexpr (B == 1) return st1;
+    else if constexpr (B == 2) return st2;
+    else if constexpr (B == 3) return st3;
+    else return st4;
+  };
 
   const int nwg = tiles_m * tiles_n;
   int bid = blockIdx.x;
@@ -240,29 +325,26 @@ __global__ __launch_bounds__(kThreads8) void gemm_nt_lds_kernel(const half_t* __
   const int lr = lane & 31, lk = lane >> 5;
 
   // Source pointers of this lane's 16-byte pieces (fixed across K).
-  const int blk_row = lane >> 3;  // row within a 1 KiB block
   const half_t* a_src[A_BLK];
   const half_t* b_src[B_BLK];
 #pragma unroll
   for (int j = 0; j < A_BLK; ++j) {
     const int blk = wave * A_BLK + j;
-    int m = tile_m * BM + blk * 8 + blk_row;
+    int m = tile_m * BM + blk * Lay::kRowsPerBlock + lane / Lay::kChunks;
     m = m < M ? m : M - 1;
-    a_src[j] = A + (int64_t)m * lda + dma_chunk(lane, blk) * 8;
+    a_src[j] = A + (int64_t)m * lda + Lay::dma_chunk(lane, blk) * 8;
   }
 #pragma unroll
   for (int j = 0; j < B_BLK; ++j) {
     const int blk = wave * B_BLK + j;
-    const int n = tile_n * BN + blk * 8 + blk_row;
-    b_src[j] = W + (int64_t)n * K + dma_chunk(lane, blk) * 8;
+    const int n = tile_n * BN + blk * Lay::kRowsPerBlock + lane / Lay::kChunks;
+    b_src[j] = W + (int64_t)n * K + Lay::dma_chunk(lane, blk) * 8;
   }
-  auto issue = [&](int k0, int buf) {
-    half_t* As = smem + buf * STAGE;
-    half_t* Bs = As + BM * kBK;
+  auto issue = [&](half_t* st, int k0) {
 #pragma unroll
-    for (int j = 0; j < A_BLK; ++j) load_lds16(a_src[j] + k0, As + (wave * A_BLK + j) * 512);
+    for (int j = 0; j < A_BLK; ++j) load_lds16(a_src[j] + k0, st + (wave * A_BLK + j) * 512);
 #pragma unroll
-    for (int j = 0; j < B_BLK; ++j) load_lds16(b_src[j] + k0, Bs + (wave * B_BLK + j) * 512);
+    for (int j = 0; j < B_BLK; ++j) load_lds16(b_src[j] + k0, st + BM * BK + (wave * B_BLK + j) * 512);
   };
 
   float16_t acc[TM][TN];
@@ -275,15 +357,13 @@ __global__ __launch_bounds__(kThreads8) void gemm_nt_lds_kernel(const half_t* __
 
   // Fragment sets: fa[set][i] = A rows of MFMA tile i, fb[set][j] = W rows of tile j.
   half8_t fa[2][TM], fb[2][TN];
-  auto read_frags = [&](int buf, int slice, int set) {
-    const half_t* As = smem + buf * STAGE;
-    const half_t* Bs = As + BM * kBK;
+  auto read_frags = [&](const half_t* st, int slice, int set) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
-      fa[set][i] = *reinterpret_cast<const half8_t*>(As + lds_swz(wm * WM + i * 32 + lr, 2 * slice + lk));
+      fa[set][i] = *reinterpret_cast<const half8_t*>(st + Lay::offset(wm * WM + i * 32 + lr, 2 * slice + lk));
 #pragma unroll
     for (int j = 0; j < TN; ++j)
-      fb[set][j] = *reinterpret_cast<const half8_t*>(Bs + lds_swz(wn * WN + j * 32 + lr, 2 * slice + lk));
+      fb[set][j] = *reinterpret_cast<const half8_t*>(st + BM * BK + Lay::offset(wn * WN + j * 32 + lr, 2 * slice + lk));
   };
   auto mma = [&](int set) {
 #pragma unroll
@@ -295,6 +375,8 @@ __global__ __launch_bounds__(kThreads8) void gemm_nt_lds_kernel(const half_t* __
   // fragment reads alternate from the block's start (an MFMA first, so the
   // wait for slice s's operands covers only reads issued a block earlier),
   // then the remaining MFMAs follow; a sched_barrier closes the block.
+  // Without it the scheduler folds the two fragment sets into one and puts
+  // an lgkmcnt(0) wait in front of every MFMA group.
   auto interleave = [&]() {
 #pragma unroll
     for (int r = 0; r < TM + TN; ++r) {
@@ -305,48 +387,80 @@ __global__ __launch_bounds__(kThreads8) void gemm_nt_lds_kernel(const half_t* __
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  const int nk = K / kBK;
-  issue(0, 0);
-  wait_vmcnt<0>();
-  __syncthreads();
-  if (nk > 1) issue(kBK, 1);
-  read_frags(0, 0, 0);
-  // Without the explicit block order the scheduler folds the two fragment
-  // sets into one and puts an lgkmcnt(0) wait in front of every MFMA group.
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    read_frags(buf, 1, 1);
-    mma(0);
-    interleave();
-    read_frags(buf, 2, 0);
-    mma(1);
-    interleave();
-    read_frags(buf, 3, 1);
-    mma(0);
-    interleave();
-    if (kt + 1 < nk) {
-      // Step kt + 1 has landed (its loads were issued one step ago); after the
-      // barrier every wave holds its slice-3 fragments, so buffer `buf` is free.
-      wait_vmcnt<0>();
-      __syncthreads();
-      if (kt + 2 < nk) issue((kt + 2) * kBK, buf);
-      read_frags(buf ^ 1, 0, 0);
+  // Every step issues exactly one stage (past the end of K the last K step is
+  // fetched again into a buffer nobody reads), so the number of loads in
+  // flight behind any stage is a constant and each wait is a plain vmcnt(N).
+  const int nk = K / BK;
+  const int last_k0 = (nk - 1) * BK;
+  auto prologue_issue = [&](auto b) {
+    constexpr int B = decltype(b)::value;
+    issue(stage(b), min(B * BK, last_k0));
+  };
+  prologue_issue(ic<0>{});
+  prologue_issue(ic<1>{});
+  if constexpr (NSTAGE > 2) prologue_issue(ic<2>{});
+  if constexpr (NSTAGE > 3) prologue_issue(ic<3>{});
+  if constexpr (NSTAGE > 4) prologue_issue(ic<4>{});
+  wait_vmcnt<(NSTAGE - 1) * LPS>();  // stage 0 landed
+  stage_barrier();
+  read_frags(stage(ic<0>{}), 0, 0);
+
+  // One K step on stage buffer B.
+  auto step = [&](auto b, int kt) {
+    constexpr int B = decltype(b)::value;
+#pragma unroll
+    for (int s = 0; s + 1 < S; ++s) {
+      read_frags(stage(b), s + 1, (s + 1) & 1);
+      mma(s & 1);
+      interleave();
     }
-    mma(1);
+    // Stage kt + 1 must have landed everywhere; the NSTAGE - 2 stages issued
+    // after it may stay in flight.
+    wait_vmcnt<(NSTAGE - 2) * LPS>();
+    stage_barrier();
+    issue(stage(b), min((kt + NSTAGE) * BK, last_k0));
+    read_frags(stage(ic<(B + 1) % NSTAGE>{}), 0, 0);  // unused after the last step
+    mma((S - 1) & 1);
+    interleave();
+  };
+  // Whole groups of NSTAGE steps run branch-free (a branch between steps
+  // would merge waitcnt states and cost a full vmcnt(0) drain); the
+  // remaining nk % NSTAGE steps follow the loop.
+  int kt = 0;
+  for (; kt + NSTAGE <= nk; kt += NSTAGE) {
+    step(ic<0>{}, kt);
+    step(ic<1>{}, kt + 1);
+    if constexpr (NSTAGE > 2) step(ic<2>{}, kt + 2);
+    if constexpr (NSTAGE > 3) step(ic<3>{}, kt + 3);
+    if constexpr (NSTAGE > 4) step(ic<4>{}, kt + 4);
   }
-  __syncthreads();  // all waves done reading the pipeline buffers
+  if (kt < nk) step(ic<0>{}, kt);
+  if constexpr (NSTAGE > 2) if (kt + 1 < nk) step(ic<1>{}, kt + 1);
+  if constexpr (NSTAGE > 3) if (kt + 2 < nk) step(ic<2>{}, kt + 2);
+  if constexpr (NSTAGE > 4) if (kt + 3 < nk) step(ic<3>{}, kt + 3);
+  __syncthreads();  // all waves done reading the stage buffers; every load landed
 
   // ---- epilogue: bias/activation in registers, fp16 tile staged in LDS ----
-  half_t* Cs = smem;  // [BM][BN]
+  // Rows [p * RPA, (p + 1) * RPA) of the tile go to stage buffer p.
+  auto rows_of = [&](int p) -> half_t* {
+    half_t* r = st0;
+    r = p == 1 ? st1 : r;
+    if constexpr (NSTAGE > 2) r = p == 2 ? st2 : r;
+    if constexpr (NSTAGE > 3) r = p == 3 ? st3 : r;
+    if constexpr (NSTAGE > 4) r = p == 4 ? st4 : r;
+    return r;
+  };
 #pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const int cl = wn * WN + j * 32 + lr;
-    const float b = (EPI != GD_EPI_NONE) ? (float)bias[tile_n * BN + cl] : 0.f;
+  for (int i = 0; i < TM; ++i) {
+    const int rb = wm * WM + i * 32;  // a 32-row group lies inside one buffer
+    half_t* Cs = rows_of(rb / RPA) + (rb % RPA) * BN;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int r0 = wm * WM + i * 32 + 4 * lk;
+    for (int j = 0; j < TN; ++j) {
+      const int cl = wn * WN + j * 32 + lr;
+      const float b = (EPI != GD_EPI_NONE) ? (float)bias[tile_n * BN + cl] : 0.f;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) Cs[(r0 + 8 * (e >> 2) + (e & 3)) * BN + cl] = epilogue<EPI>(acc[i][j][e], b);
+      for (int e = 0; e < 16; ++e)
+        Cs[(4 * lk + 8 * (e >> 2) + (e & 3)) * BN + cl] = epilogue<EPI>(acc[i][j][e], b);
     }
   }
   __syncthreads();
@@ -358,34 +472,26 @@ __global__ __launch_bounds__(kThreads8) void gemm_nt_lds_kernel(const half_t* __
     const int row = tile_m * BM + r;
     if (row < M)
       *reinterpret_cast<half8_t*>(C + (int64_t)row * ldc + tile_n * BN + cc * 8) =
-          *reinterpret_cast<const half8_t*>(Cs + r * BN + cc * 8);
+          *reinterpret_cast<const half8_t*>(rows_of(r / RPA) + (r % RPA) * BN + cc * 8);
   }
 }
 
-template <int BM, int BN, int WAVES_M>
+template <int BM, int BN, int WAVES_M, int BK, int NSTAGE>
 int launch_lds_tile(const half_t* A, const half_t* W, const half_t* bias, half_t* C, int M, int N, int K, int64_t lda,
                     int64_t ldc, int epi, hipStream_t stream) {
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = N / BN;
   const dim3 grid(tiles_m * tiles_n), block(kThreads8);
+#define GD_LDS_GEMM(E)                                                                                               \
+  hipLaunchKernelGGL((gemm_nt_lds_kernel<BM, BN, WAVES_M, BK, NSTAGE, E>), grid, block, 0, stream, A, W, bias, C, M, N, \
+                     K, lda, ldc, tiles_m, tiles_n)
   switch (epi) {
-    case GD_EPI_NONE:
-      hipLaunchKernelGGL((gemm_nt_lds_kernel<BM, BN, WAVES_M, GD_EPI_NONE>), grid, block, 0, stream, A, W, bias, C, M, N,
-                         K, lda, ldc, tiles_m, tiles_n);
-      break;
-    case GD_EPI_BIAS:
-      hipLaunchKernelGGL((gemm_nt_lds_kernel<BM, BN, WAVES_M, GD_EPI_BIAS>), grid, block, 0, stream, A, W, bias, C, M, N,
-                         K, lda, ldc, tiles_m, tiles_n);
-      break;
-    case GD_EPI_BIAS_GELU:
-      hipLaunchKernelGGL((gemm_nt_lds_kernel<BM, BN, WAVES_M, GD_EPI_BIAS_GELU>), grid, block, 0, stream, A, W, bias, C, M,
-                         N, K, lda, ldc, tiles_m, tiles_n);
-      break;
-    default:
-      hipLaunchKernelGGL((gemm_nt_lds_kernel<BM, BN, WAVES_M, GD_EPI_BIAS_RELU>), grid, block, 0, stream, A, W, bias, C, M,
-                         N, K, lda, ldc, tiles_m, tiles_n);
-      break;
+    case GD_EPI_NONE: GD_LDS_GEMM(GD_EPI_NONE); break;
+    case GD_EPI_BIAS: GD_LDS_GEMM(GD_EPI_BIAS); break;
+    case GD_EPI_BIAS_GELU: GD_LDS_GEMM(GD_EPI_BIAS_GELU); break;
+    default: GD_LDS_GEMM(GD_EPI_BIAS_RELU); break;
   }
+#undef GD_LDS_GEMM
   GD_LAUNCH_CHECK();
   return GD_OK;
 }
@@ -418,16 +524,6 @@ int launch_tile(const half_t* A, const half_t* W, const half_t* bias, half_t* C,
   return GD_OK;
 }
 
-// GD_GEMM_VARIANT=1 selects the register-staged kernel for every shape (A/B
-// comparisons); the default 0 uses the direct-to-LDS kernel for M >= 2048.
-int gemm_variant() {
-  static const int v = [] {
-    const char* e = std::getenv("GD_GEMM_VARIANT");
-    return e ? std::atoi(e) : 0;
-  }();
-  return v;
-}
-
 }  // namespace
 
 int launch_linear(const void* a, const void* w, const void* bias, void* c, int64_t m, int64_t n, int64_t k, int64_t lda,
@@ -444,14 +540,14 @@ int launch_linear(const void* a, const void* w, const void* bias, void* c, int64
     if (M >= 1024) return launch_tile<128, 128, true>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
     return launch_tile<64, 128, true>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
   }
-  if (M >= 2048 && gemm_variant() == 0) {
-    // 256 x 256 tiles when they fill whole waves of the 256 CUs, else 256 x 128.
+  if (M >= 2048) {
+    // 256 x 256 tiles (two 64-deep stages, 128 KiB of LDS) when they fill
+    // whole waves of the 256 CUs, else 256 x 128 (three stages, 144 KiB).
     const int t256 = ((M + 255) / 256) * (N / 256);
     if (N % 256 == 0 && (t256 % 256 == 0 || t256 >= 512))
-      return launch_lds_tile<256, 256, 2>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
-    return launch_lds_tile<256, 128, 4>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
+      return launch_lds_tile<256, 256, 2, 64, 2>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
+    return launch_lds_tile<256, 128, 4, 64, 3>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
   }
-  if (M >= 4096) return launch_tile<256, 128, false>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
   if (M >= 1024) return launch_tile<128, 128, false>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
   return launch_tile<64, 128, false>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
 }

@@ -9,7 +9,6 @@
 // exactly once, held in registers, reduced with wave64 butterflies (mean, then
 // the centred second moment) and written once: 3 x 2 KiB of HBM traffic per
 // row for residual LN, the algorithmic minimum.
-#include <cstdlib>
 
 #include "gd_common.hpp"
 #include "gd_kernels.hpp"
@@ -109,16 +108,6 @@ __global__ __launch_bounds__(256) void residual_ln_kernel(const half_t* x, const
 #pragma unroll
   for (int i = 0; i < RPW; ++i)
     if (row0 + i < rows) normalize_store<VPL>(r[i], sum[i], gamma, beta, out, row0 + i, lane, eps, 1.0f);
-}
-
-// Rows per wave for the 1024-wide kernel (GD_LN_ROWS_PER_WAVE = 1, 2 or 4).
-int ln_rows_per_wave() {
-  static const int v = [] {
-    const char* e = std::getenv("GD_LN_ROWS_PER_WAVE");
-    const int r = e ? std::atoi(e) : 1;
-    return (r == 2 || r == 4) ? r : 1;
-  }();
-  return v;
 }
 
 // Any width that is a multiple of 8: three passes like the reference kernel
@@ -237,14 +226,7 @@ int launch_residual_layer_norm(const void* x, const void* residual, const void* 
   const bool vec_ok = aligned16(x) && (!residual || aligned16(residual)) && aligned16(gamma) && aligned16(beta) &&
                       aligned16(out);
   if (vec_ok && cols == 1024) {
-    const int rpw = ln_rows_per_wave();
-    const dim3 g2((unsigned)((rows + kRowsPerBlock * rpw - 1) / (kRowsPerBlock * rpw)));
-    if (rpw == 4)
-      hipLaunchKernelGGL((residual_ln_kernel<2, 4>), g2, block, 0, stream, X, R, G, Bt, O, rows, eps, round_sum);
-    else if (rpw == 2)
-      hipLaunchKernelGGL((residual_ln_kernel<2, 2>), g2, block, 0, stream, X, R, G, Bt, O, rows, eps, round_sum);
-    else
-      hipLaunchKernelGGL((residual_ln_kernel<2, 1>), g2, block, 0, stream, X, R, G, Bt, O, rows, eps, round_sum);
+    hipLaunchKernelGGL((residual_ln_kernel<2, 1>), grid, block, 0, stream, X, R, G, Bt, O, rows, eps, round_sum);
   } else if (vec_ok && cols == 512) {
     hipLaunchKernelGGL((residual_ln_kernel<1, 1>), grid, block, 0, stream, X, R, G, Bt, O, rows, eps, round_sum);
   } else if (vec_ok && cols == 2048) {

@@ -186,6 +186,34 @@ def test_linear_row_gather():
     check_linear(out, x[rows], w, b, "relu")
 
 
+def _ordered16(a):
+    """fp16 bit patterns mapped to integers that are monotone in the value
+    (so a difference of 1 is one ulp, across zero as well)."""
+    i = np.asarray(a, np.float16).view(np.int16).astype(np.int64)
+    return np.where(i < 0, -(i & 0x7FFF), i)
+
+
+@pytest.mark.parametrize("m", [248, 2048])  # small-M kernel, large-M kernel
+def test_gelu_epilogue_every_fp16_input(m):
+    """x @ I^T + 0 reproduces x exactly, so the GELU epilogue sees every finite
+    fp16 value once (63488 = 248 x 256).  Against the correctly rounded GELU:
+    at most 1 ulp anywhere, and only for values next to a rounding boundary."""
+    vals = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    vals = vals[np.isfinite(vals)]
+    n = 256
+    x = np.zeros((m, n), np.float16)
+    x.flat[:vals.size] = vals
+    w = np.eye(n, dtype=np.float16)
+    b = np.zeros(n, np.float16)
+    out = fk().linear(dev(x), dev(w), dev(b), epilogue="gelu")
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().reshape(-1)[:vals.size]
+    want = O.gelu(vals.astype(np.float64))
+    d = np.abs(_ordered16(got) - _ordered16(want))
+    assert d.max() <= 1, f"{d.max()} ulp at x={vals[np.argmax(d)]}"
+    assert (d > 0).sum() <= 64
+
+
 # ---------------------------------------------------------------------------
 # fused relative bias + masked softmax (+ P.V) -- DeBERTa.swift:322-395
 # ---------------------------------------------------------------------------
