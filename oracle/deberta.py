@@ -259,8 +259,8 @@ def relative_bias_default(q, k, pos_key, pos_query, c2p_idx, p2c_idx, head_size:
     k = np.asarray(k, dtype)
     pk = np.asarray(pos_key, dtype)
     pq = np.asarray(pos_query, dtype)
-    c2p_raw = f16(np.einsum("bhld,hpd->bhlp", q, pk, optimize=True), round16, dtype)
-    p2c_raw = f16(np.einsum("bhld,hpd->bhlp", k, pq, optimize=True), round16, dtype)
+    c2p_raw = f16(np.matmul(q, np.swapaxes(pk, -1, -2)[None]), round16, dtype)
+    p2c_raw = f16(np.matmul(k, np.swapaxes(pq, -1, -2)[None]), round16, dtype)
     L = q.shape[2]
     rows = np.arange(L)[:, None]
     c2p = c2p_raw[:, :, rows, np.asarray(c2p_idx)]  # [B,H,L,L]: [q, c2p_idx[q,k]]
@@ -326,7 +326,7 @@ def attention_probs_default(q, k, bias, attention_mask, head_size: int, round16:
     q = np.asarray(q, dtype)
     k = np.asarray(k, dtype)
     mask = f16(np.asarray(bias, dtype) + additive_key_mask(attention_mask), round16, dtype)
-    scores = np.einsum("bhqd,bhkd->bhqk", q, k, optimize=True) * dtype(scale_f32(head_size)) + mask
+    scores = np.matmul(q, np.swapaxes(k, -1, -2)) * dtype(scale_f32(head_size)) + mask
     with np.errstate(over="ignore", invalid="ignore"):
         return _softmax(scores)
 
@@ -336,7 +336,7 @@ def attention_default(q, k, v, bias, attention_mask, head_size: int, round16: bo
     then transpose/reshape to [B, L, H*D] (DeBERTa.swift:382-395).  Key-only
     masking: padded query rows attend over the valid keys."""
     p = attention_probs_default(q, k, bias, attention_mask, head_size, round16, dtype)
-    ctx = np.einsum("bhqk,bhkd->bhqd", p, np.asarray(v, dtype), optimize=True)
+    ctx = np.matmul(p, np.asarray(v, dtype))
     B, H, L, D = ctx.shape
     return f16(np.transpose(ctx, (0, 2, 1, 3)).reshape(B, L, H * D), round16, dtype)
 
@@ -347,13 +347,13 @@ def attention_generic(q, k, v, bias, attention_mask, head_size: int, round16: bo
     masked keys := -65504; P = softmax -> fp16; ctx = fp16(P v)."""
     q = np.asarray(q, dtype)
     k = np.asarray(k, dtype)
-    content = f16(f16(np.einsum("bhqd,bhkd->bhqk", q, k, optimize=True), round16, dtype) / scale_f16(head_size), round16,
+    content = f16(f16(np.matmul(q, np.swapaxes(k, -1, -2)), round16, dtype) / scale_f16(head_size), round16,
                   dtype)
     scores = f16(content + np.asarray(bias, dtype), round16, dtype)
     valid = (np.asarray(attention_mask, np.float64) > 0)[:, None, None, :]
     masked = np.where(valid, scores, MASK_FILL)
     p = f16(_softmax(masked), round16, dtype)
-    ctx = f16(np.einsum("bhqk,bhkd->bhqd", p, np.asarray(v, dtype), optimize=True), round16, dtype)
+    ctx = f16(np.matmul(p, np.asarray(v, dtype)), round16, dtype)
     B, H, L, D = ctx.shape
     return np.transpose(ctx, (0, 2, 1, 3)).reshape(B, L, H * D)
 
@@ -379,13 +379,13 @@ def fused_attention_kernel(q, k, v, pos_key, pos_query, c2p_indices, p2c_indices
     hh = np.arange(H)[:, None, None]
     c2p = np.einsum("bhqd,hqkd->bhqk", q, pk[hh, c2pi], optimize=True)
     p2c = np.einsum("bhkd,hqkd->bhqk", k, pq[hh, np.swapaxes(p2ci, 1, 2)], optimize=True)
-    score = (np.einsum("bhqd,bhkd->bhqk", q, k, optimize=True) + c2p + p2c) * np.float64(np.float32(scale))
+    score = (np.matmul(q, np.swapaxes(k, -1, -2)) + c2p + p2c) * np.float64(np.float32(scale))
     masked = np.asarray(key_mask, np.float64).reshape(B, 1, 1, L) < -60000.0
     score = np.where(masked, MASK_FILL, score)
     m = np.maximum(score.max(axis=-1, keepdims=True), MASK_FILL)
     e = np.exp(score - m)
     w = e / e.sum(axis=-1, keepdims=True)
-    out = np.einsum("bhqk,bhkd->bqhd", w, v, optimize=True)
+    out = np.matmul(w, v).transpose(0, 2, 1, 3)
     return f16(out)
 
 

@@ -173,3 +173,51 @@ def test_full_model_classify_workload():
                       a["marker_mask"][rows])
     near = compare_decisions(got[rows], want, [batch.tasks[i] for i in rows])
     assert len(near) == 0 or len(near) < len(rows)
+
+
+def _oracle_rows(om, arrays, rows):
+    return om.forward(*(arrays[k][rows] for k in ("input_ids", "attention_mask", "marker_indices", "marker_mask")))
+
+
+def test_long_context_workload():
+    """B=64, L=512 (every row full), 3 task heads x 20 options (two multi-label
+    heads of 20 labels, one single-label head of 8): 24 layers + classifier.
+    Options past a head's label count read -10000; the oracle recomputes one
+    row."""
+    from gliner_decide import DecisionInput
+    from gliner_decide.synthetic import long_context_batch
+    gpu, w, pc, oc = _models(dict(vocab_size=128100), seed=6)
+    batch = long_context_batch(seed=6)
+    a = batch.arrays()
+    got = gpu.classify(DecisionInput(**a)).logits.float().cpu().numpy()
+    assert got.shape == (64, 3, 20) and np.all(np.isfinite(got))
+    assert np.all(got[a["marker_mask"] == 0] == -10000.0)
+    om = O.OracleModel(O.ModelWeights.from_store(w, oc), oc, dtype=np.float64)
+    rows = [63]
+    compare_decisions(got[rows], _oracle_rows(om, a, rows), [batch.tasks[i] for i in rows])
+
+
+def test_bucket_mix_workload():
+    """All 4096 rows of the mixed workload (buckets L = 32 ... 512, 1-2 tasks
+    x 2-10 labels, B=32 with the last batch of a bucket padded by copies of
+    its last valid row).  Padded rows must reproduce that row's logits
+    exactly; the oracle recomputes the last valid row of one batch per bucket."""
+    from gliner_decide import DecisionInput
+    from gliner_decide.synthetic import bucket_mix
+    gpu, w, pc, oc = _models(dict(vocab_size=128100), seed=5)
+    om = O.OracleModel(O.ModelWeights.from_store(w, oc), oc, dtype=np.float64)
+    checked, rows_run = set(), 0
+    for x in bucket_mix(seed=5):
+        a = x.arrays()
+        got = gpu.classify(DecisionInput(**a)).logits.float().cpu().numpy()
+        assert np.all(np.isfinite(got))
+        v = x.valid_rows
+        rows_run += v
+        if v < got.shape[0]:
+            np.testing.assert_array_equal(got[v:], np.broadcast_to(got[v - 1], got[v:].shape))
+        L = x.shape[1]
+        if L not in checked:
+            checked.add(L)
+            rows = [v - 1]
+            compare_decisions(got[rows], _oracle_rows(om, a, rows), [x.tasks[i] for i in rows])
+    assert rows_run == 4096 and checked == {32, 64, 96, 128, 256, 512}
