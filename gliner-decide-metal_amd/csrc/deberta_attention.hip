@@ -42,9 +42,16 @@ constexpr int kQT = 128;           // queries per workgroup
 constexpr int kKC = 64;            // keys per chunk
 constexpr int kD = 64;             // head dim
 constexpr int kWin = 192;          // relative-table rows per chunk window (>= 191)
+constexpr int kMid = 128;          // |q - k| <= kMid: idx(q - k) = q - k + 256 (bucket size 256)
 constexpr int kC2PCols = 80;       // per-wave c2p window (<= 79 positions)
 constexpr int kC2PStride = kC2PCols + 4;  // 168-byte rows keep the 8-byte stores aligned
-constexpr int kP2CStride = 34;     // per-wave p2c tile: 16 keys x 32 positions (+pad)
+// Per-wave p2c tile (16 keys x 32 window positions), stored skewed: value
+// (key row kr, position p) at (kr + p) * kP2CSkew + kr.  A score's four keys
+// 4g .. 4g+3 in the linear zone share kr + p = 15 + lc, so its four p2c terms
+// are one aligned 8-byte read; rows of 24 halfs make those reads
+// conflict-free across the wave.
+constexpr int kP2CSkew = 24;
+constexpr int kP2CRows = 47;       // kr + p <= 15 + 31
 constexpr int kVtStride = 68;      // V^T chunk row (64 keys + pad)
 
 // LDS map (halfs).  The stage buffers are reused for the V^T chunks and the
@@ -52,14 +59,25 @@ constexpr int kVtStride = 68;      // V^T chunk row (64 keys + pad)
 constexpr int kStageK = kKC * kD;                 // 4096
 constexpr int kStageWin = kWin * kD;              // 12288
 constexpr int kStage = kStageK + 2 * kStageWin;   // 28672 halfs = 56 KiB
-constexpr int kScratchWave = 16 * kC2PStride + 16 * kP2CStride;
-constexpr int kSmemHalfs = 2 * kStage + kWaves * kScratchWave;
+constexpr int kScratchWave = 16 * kC2PStride + kP2CRows * kP2CSkew;
+static_assert(16 * 72 <= kScratchWave, "context staging fits a wave's scratch");
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
+// 16-byte direct-to-LDS load (global_load_lds_dwordx4: lane l's 16 bytes land
+// at M0 + 16 l), issued as inline assembly.  The compiler cannot tell which
+// LDS buffer the builtin form writes once stage pointers are merged across
+// the unrolled chunks, so it would drain every load in flight (vmcnt(0))
+// before each later LDS read and serialise the stage pipeline; here the
+// pipeline orders these loads itself (vmcnt(0) + barrier before a stage is
+// read).  M0 is not used by anything else in this kernel.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void load_lds16(const half_t* g, half_t* lds_block) {
-  __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g), (lds_void_t*)(lds_block), 16, 0, 0);
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)lds_block);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 // 128-byte rows; the 16-byte chunk index is XORed with bits 1..3 of the row.
 // gfx950's LDS serves a ds_read_b128 16 lanes at a time over 64 banks
@@ -79,7 +97,13 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     const half_t* __restrict__ PK, const half_t* __restrict__ PQ, int64_t pksh, int64_t pksp, int64_t pqsh,
     int64_t pqsp, const half_t* __restrict__ mask, int mask_kind, int B, int H, int L, int P, int bucket_size,
     float scale_qk, float scale16, half_t* __restrict__ out, int64_t ldo) {
-  __shared__ __attribute__((aligned(1024))) half_t smem[kSmemHalfs];
+  // Two stage buffers and the per-wave scratch are separate LDS objects: with
+  // the chunk loop unrolled, every access names its buffer at compile time,
+  // so reads of one stage wait only for that stage's DMA, never for the next
+  // stage's loads in flight.
+  __shared__ __attribute__((aligned(1024))) half_t stage0[kStage];
+  __shared__ __attribute__((aligned(1024))) half_t stage1[kStage];
+  __shared__ __attribute__((aligned(1024))) half_t scratch_lds[kWaves * kScratchWave];
   __shared__ int16_t idx_tab[2 * 16 * MAXT];
   __shared__ __attribute__((aligned(16))) float mask_add[16 * MAXT];
 
@@ -119,7 +143,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   const half_t* Kb = K + (int64_t)b * ksb + (int64_t)h * ksh;
   const half_t* PKh = PK + (int64_t)h * pksh;
   const half_t* PQh = PQ + (int64_t)h * pqsh;
-  half_t* c2p_w = smem + 2 * kStage + wave * kScratchWave;
+  half_t* c2p_w = scratch_lds + wave * kScratchWave;
   half_t* p2c_w = c2p_w + 16 * kC2PStride;
 
   // Relative index of a wave-uniform r, clipped to the span of this length.
@@ -135,7 +159,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   const int blk_chunk = (lane & 7) ^ (((wave & 1) << 2) | (lane >> 4));
   auto win_lo_of = [&](int kc) { return idx_clip(q0 - kc - (kKC - 1)); };
   auto issue_stage = [&](int c, int buf) {
-    half_t* st = smem + buf * kStage;
+    half_t* st = buf ? stage1 : stage0;
     const int kc = c * kKC;
     {  // K rows: 8 blocks of 8 rows, one per wave
       int key = kc + wave * 8 + blk_row;
@@ -161,6 +185,12 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     qf1 = *reinterpret_cast<const half8_t*>(qrow + 32 + 8 * g);
   }
 
+  // Swizzled offsets of this lane's two 16-byte chunks (g and 4 + g) in row
+  // 16m + lc of a staged table: the XOR term depends on the row only through
+  // lc, so a 16-aligned tile row base is a plain (uniform) offset.
+  const int swz_lo = swz(lc, g);
+  const int swz_hi = swz(lc, 4 + g);
+
   float sc[MAXT][4];
 #pragma unroll
   for (int T = 0; T < MAXT; ++T)
@@ -174,24 +204,43 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     wait_vmcnt<0>();
     __syncthreads();  // stage c landed everywhere; every wave is done with stage c - 1
     if (c + 1 < nchunks) issue_stage(c + 1, (c + 1) & 1);
-    const half_t* st = smem + (c & 1) * kStage;
+    const half_t* st = (c & 1) ? stage1 : stage0;
     const half_t* Ks = st;
     const half_t* PKs = st + kStageK;
     const half_t* PQs = st + kStageK + kStageWin;
     const int kc = c * kKC;
     const int wlo = win_lo_of(kc);
     if (active) {
-      // c2p for this wave's 16 queries and the chunk's keys
-      const int cw_lo = idx_clip(qw - kc - (kKC - 1));
-      const int cw_hi = idx_clip(qw + 15 - kc);
-      const int ntw = (cw_hi - cw_lo + 16) >> 4;  // <= 5
+      // In a linear chunk every (query, key) pair of this wave, and the start
+      // of the workgroup's window, lies in the linear zone with no clipping to
+      // the sequence: every window offset below is closed-form and 16-aligned.
+      const bool lin = (kc + kKC <= L) && (q0 - kc - (kKC - 1) >= -kMid) && (qw + 15 - kc <= kMid) &&
+                       (kc + (kKC - 1) - qw <= kMid);
+      // c2p for this wave's 16 queries and the chunk's keys: positions
+      // [cw_lo, cw_lo + 16 ntw) = window rows [crow0, crow0 + 16 ntw)
+      int cw_lo, ntw;
+      if (lin) {
+        cw_lo = qw - kc - (kKC - 1) + bucket_size;
+        ntw = 5;
+      } else {
+        cw_lo = idx_clip(qw - kc - (kKC - 1));
+        const int cw_hi = idx_clip(qw + 15 - kc);
+        ntw = (cw_hi - cw_lo + 16) >> 4;  // <= 5
+      }
+      const int crow0 = cw_lo - wlo;
 #pragma unroll
       for (int tw = 0; tw < kC2PCols / 16; ++tw) {
         if (tw < ntw) {
-          int row = cw_lo - wlo + 16 * tw + lc;
-          row = row < kWin - 1 ? row : kWin - 1;
-          const half8_t a0 = *reinterpret_cast<const half8_t*>(PKs + swz(row, g));
-          const half8_t a1 = *reinterpret_cast<const half8_t*>(PKs + swz(row, 4 + g));
+          half8_t a0, a1;
+          if (lin) {
+            a0 = *reinterpret_cast<const half8_t*>(PKs + (crow0 + 16 * tw) * kD + swz_lo);
+            a1 = *reinterpret_cast<const half8_t*>(PKs + (crow0 + 16 * tw) * kD + swz_hi);
+          } else {
+            int row = crow0 + 16 * tw + lc;
+            row = row < kWin - 1 ? row : kWin - 1;
+            a0 = *reinterpret_cast<const half8_t*>(PKs + swz(row, g));
+            a1 = *reinterpret_cast<const half8_t*>(PKs + swz(row, 4 + g));
+          }
           float4_t r = {0.f, 0.f, 0.f, 0.f};
           r = mfma16x16x32(a0, qf0, r);
           r = mfma16x16x32(a1, qf1, r);
@@ -201,73 +250,109 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
           *reinterpret_cast<half4_t*>(c2p_w + lc * kC2PStride + 16 * tw + 4 * g) = hv;
         }
       }
+
+      // Per 16-key tile tt: S^T = K Q^T (scores) and P2C = K . posQ[window]^T
+      // over the <= 31 positions [pp_lo, pp_lo + 16 nj) the tile needs, stored
+      // skewed into p2c_w.  Tiles are software-pipelined: tile tt's gathers are
+      // issued before tile tt+1's MFMAs and p2c stores (the LDS executes a
+      // wave's accesses in order, so one p2c buffer suffices), and tile tt is
+      // combined while those are in flight.
+      int pp_lo[4], nj_t[4];
+      float4_t s_t[4];
+      half8_t fk[2][2], fq[2][4];  // per tile parity: K rows (chunks g, 4+g), posQ rows (j = 0, 1)
+      // Operand fragments of tile tt (LDS reads only; issued a tile ahead).
+      auto prep_load = [&](int tt) {
+        const int k0 = kc + 16 * tt;
+        const int par = tt & 1;
+        if (lin) {
+          pp_lo[tt] = qw - k0 - 15 + bucket_size;
+          nj_t[tt] = 2;
+        } else {
+          pp_lo[tt] = idx_clip(qw - k0 - 15);
+          nj_t[tt] = (idx_clip(qw - k0 + 15) - pp_lo[tt] + 16) >> 4;  // 1 or 2
+        }
+        const int prow0 = pp_lo[tt] - wlo;
+        fk[par][0] = *reinterpret_cast<const half8_t*>(Ks + 16 * tt * kD + swz_lo);
+        fk[par][1] = *reinterpret_cast<const half8_t*>(Ks + 16 * tt * kD + swz_hi);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          if (j < nj_t[tt]) {
+            if (lin) {  // prow0 = 16 (wave - tt) + 48
+              fq[par][2 * j] = *reinterpret_cast<const half8_t*>(PQs + (prow0 + 16 * j) * kD + swz_lo);
+              fq[par][2 * j + 1] = *reinterpret_cast<const half8_t*>(PQs + (prow0 + 16 * j) * kD + swz_hi);
+            } else {
+              int row = prow0 + 16 * j + lc;
+              row = row < kWin - 1 ? row : kWin - 1;
+              fq[par][2 * j] = *reinterpret_cast<const half8_t*>(PQs + swz(row, g));
+              fq[par][2 * j + 1] = *reinterpret_cast<const half8_t*>(PQs + swz(row, 4 + g));
+            }
+          }
+        }
+      };
+      // Scores and p2c of tile tt from its fragments; p2c stored skewed.
+      auto prep_compute = [&](int tt) {
+        const int par = tt & 1;
+        float4_t sv = {0.f, 0.f, 0.f, 0.f};
+        sv = mfma16x16x32(fk[par][0], qf0, sv);
+        s_t[tt] = mfma16x16x32(fk[par][1], qf1, sv);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          if (j < nj_t[tt]) {
+            float4_t r = {0.f, 0.f, 0.f, 0.f};
+            r = mfma16x16x32(fk[par][0], fq[par][2 * j], r);
+            r = mfma16x16x32(fk[par][1], fq[par][2 * j + 1], r);
+            // lane holds (kr = 4g + i, p = 16 j + lc)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) p2c_w[(4 * g + i + 16 * j + lc) * kP2CSkew + 4 * g + i] = (half_t)r[i];
+          }
+        }
+      };
+      prep_load(0);
+      prep_compute(0);
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
         const int T = 4 * c + tt;
-        if (T < nt) {
-          const int k0 = 16 * T;
-          const half8_t ka0 = *reinterpret_cast<const half8_t*>(Ks + swz(16 * tt + lc, g));
-          const half8_t ka1 = *reinterpret_cast<const half8_t*>(Ks + swz(16 * tt + lc, 4 + g));
-          float4_t s = {0.f, 0.f, 0.f, 0.f};
-          s = mfma16x16x32(ka0, qf0, s);
-          s = mfma16x16x32(ka1, qf1, s);
-          const int pp_lo = idx_clip(qw - k0 - 15);
-          const int pp_hi = idx_clip(qw - k0 + 15);
-          const int nj = (pp_hi - pp_lo + 16) >> 4;  // 1 or 2
+        if (T >= nt) break;  // uniform
+        const int k0 = 16 * T;
+        const bool next = tt + 1 < 4 && T + 1 < nt;
+        if (next) prep_load(tt + 1);  // fragment reads overlap this tile's gathers
+        wave_lds_sync();  // tile tt's p2c stores (and the chunk's c2p) precede its gathers
+        // Gather the two terms of score (q = qw + lc, k = k0 + 4g + i) at
+        // idx(q - k).  In the linear zone (|q - k| <= 128 over the whole tile)
+        // idx = q - k + 256: the four c2p terms are consecutive (descending)
+        // in the lane's c2p row and the four p2c terms are one 8-byte read.
+        const float4_t madd = *reinterpret_cast<const float4_t*>(mask_add + k0 + 4 * g);
+        half4_t c2p, p2c;
+        if ((qw - k0 <= kMid - 15) && (k0 - qw <= kMid - 15)) {
+          const half_t* cp = c2p_w + lc * kC2PStride + (qw - k0 + bucket_size - cw_lo) + lc - 4 * g;
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            if (j < nj) {
-              int row = pp_lo - wlo + 16 * j + lc;
-              row = row < kWin - 1 ? row : kWin - 1;
-              const half8_t b0 = *reinterpret_cast<const half8_t*>(PQs + swz(row, g));
-              const half8_t b1 = *reinterpret_cast<const half8_t*>(PQs + swz(row, 4 + g));
-              float4_t r = {0.f, 0.f, 0.f, 0.f};
-              r = mfma16x16x32(ka0, b0, r);
-              r = mfma16x16x32(ka1, b1, r);
-#pragma unroll
-              for (int i = 0; i < 4; ++i) p2c_w[(4 * g + i) * kP2CStride + 16 * j + lc] = (half_t)r[i];
-            }
-          }
-          wave_lds_sync();
-          // Gather the two terms of score (q = qw + lc, k = k0 + 4g + i) at
-          // idx(q - k).  In the linear zone (|q - k| <= 128 over the whole
-          // tile) idx = q - k + 256, so both addresses are a per-lane base plus
-          // a constant per i (folded into the LDS instruction's offset).
-          const float4_t madd = *reinterpret_cast<const float4_t*>(mask_add + k0 + 4 * g);
-          half_t c2p[4], p2c[4];
-          if ((qw - k0 <= 113) && (k0 - qw <= 113)) {
-            const int d0 = qw - k0 + bucket_size + lc - 4 * g;  // id at i = 0
-            const half_t* cp = c2p_w + lc * kC2PStride + (d0 - cw_lo);
-            const half_t* pp = p2c_w + 4 * g * kP2CStride + (d0 - pp_lo);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              c2p[i] = cp[-i];
-              p2c[i] = pp[i * (kP2CStride - 1)];
-            }
-          } else {
-            const int r0 = qw + lc - k0 - 4 * g + L - 1;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int id = idx_tab[r0 - i];
-              c2p[i] = c2p_w[lc * kC2PStride + (id - cw_lo)];
-              p2c[i] = p2c_w[(4 * g + i) * kP2CStride + (id - pp_lo)];
-            }
-          }
+          for (int i = 0; i < 4; ++i) c2p[i] = cp[-i];
+          p2c = *reinterpret_cast<const half4_t*>(p2c_w + (15 + lc) * kP2CSkew + 4 * g);
+        } else {
+          const int r0 = qw + lc - k0 - 4 * g + L - 1;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            // fp16(c2p + p2c) is the fp16 add; the division by fp16(sqrt(3D)) is a
-            // multiply by its fp32 reciprocal, which rounds to the same fp16 value
-            // for every finite fp16 numerator (checked exhaustively).
-            const half_t sum16 = c2p[i] + p2c[i];
-            const float bias16 = round_f16((float)sum16 * inv_scale16);
-            if (OUT == GD_ATTN_OUT_BIAS)
-              sc[T][i] = round_f16(bias16 + madd[i]);
-            else
-              sc[T][i] = fmaf(s[i], scale_qk, bias16) + madd[i];
+            const int id = idx_tab[r0 - i];
+            c2p[i] = c2p_w[lc * kC2PStride + (id - cw_lo)];
+            p2c[i] = p2c_w[(4 * g + i + id - pp_lo[tt]) * kP2CSkew + 4 * g + i];
           }
-          wave_lds_sync();
+        }
+        wave_lds_sync();  // these gathers precede the next tile's p2c stores
+        if (next) prep_compute(tt + 1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          // fp16(c2p + p2c) is the fp16 add; the division by fp16(sqrt(3D)) is a
+          // multiply by its fp32 reciprocal, which rounds to the same fp16 value
+          // for every finite fp16 numerator (checked exhaustively).
+          const half_t sum16 = c2p[i] + p2c[i];
+          const float bias16 = round_f16((float)sum16 * inv_scale16);
+          if (OUT == GD_ATTN_OUT_BIAS)
+            sc[T][i] = round_f16(bias16 + madd[i]);
+          else
+            sc[T][i] = fmaf(s_t[tt][i], scale_qk, bias16) + madd[i];
         }
       }
+      wave_lds_sync();  // the last gathers precede the next chunk's c2p / p2c stores
     }
   }
   __syncthreads();  // the stage buffers are free from here on
@@ -301,8 +386,14 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   }
 
   if (OUT == GD_ATTN_OUT_PROBS || OUT == GD_ATTN_OUT_BIAS) {
-    // Stage this wave's 16 rows x L in LDS, then write 16-byte row segments.
-    half_t* rows = smem + wave * 16 * (16 * MAXT);
+    // Stage this wave's 16 rows x L in LDS (rows padded by 16 bytes so the
+    // 8-byte column stores of a wave hit distinct banks), then write 16-byte
+    // row segments.
+    const int rs = L + 8;
+    // waves 0-2 stage in stage0, 3-5 in stage1, 6-7 in the scratch buffer
+    constexpr int kRowsWave = 16 * (16 * MAXT + 8);
+    static_assert(3 * kRowsWave <= kStage && 2 * kRowsWave <= kWaves * kScratchWave, "probability staging");
+    half_t* rows = (wave < 3 ? stage0 : (wave < 6 ? stage1 : scratch_lds)) + (wave % 3) * kRowsWave;
     if (active) {
 #pragma unroll
       for (int T = 0; T < MAXT; ++T)
@@ -310,14 +401,14 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
           half4_t v;
 #pragma unroll
           for (int i = 0; i < 4; ++i) v[i] = (half_t)sc[T][i];
-          *reinterpret_cast<half4_t*>(rows + lc * L + 16 * T + 4 * g) = v;
+          *reinterpret_cast<half4_t*>(rows + lc * rs + 16 * T + 4 * g) = v;
         }
       wave_lds_sync();
       const int per_row = L / 8;  // 16-byte pieces per row
       for (int pce = lane; pce < 16 * per_row; pce += 64) {
         const int r = pce / per_row, cpos = pce - r * per_row;
         *reinterpret_cast<half8_t*>(out + (((int64_t)b * H + h) * L + qw + r) * L + cpos * 8) =
-            *reinterpret_cast<const half8_t*>(rows + r * L + cpos * 8);
+            *reinterpret_cast<const half8_t*>(rows + r * rs + cpos * 8);
       }
     }
     return;
@@ -334,7 +425,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
 #pragma unroll
   for (int c = 0; c < MAXT / 4; ++c) {
     if (c >= nchunks) break;
-    half_t* vt = smem + (c & 1) * (kD * kVtStride);
+    half_t* vt = (c & 1) ? stage1 : stage0;
 #pragma unroll
     for (int e = 0; e < 8; ++e) vt[(8 * vch + e) * kVtStride + vrow] = vnext[e];
     if (c + 1 < nchunks) {
@@ -378,7 +469,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   __syncthreads();
   if (!active) return;
   // lane holds O[qw + 4g + i][16 dt + lc]: stage 16 x 64 in LDS, write 128-byte rows
-  half_t* ot = smem + 2 * (kD * kVtStride) + wave * 16 * 72;
+  half_t* ot = scratch_lds + wave * kScratchWave;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
