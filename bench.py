@@ -46,8 +46,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     p.add_argument("--kernel-iters", type=int, default=60)
     p.add_argument("--profile-kernel", default=None,
-                   choices=["residual_layernorm", "relbias_softmax", "attention_context", "qkv_proj", "out_proj",
-                            "ffn_up_gelu", "ffn_down"],
+                   choices=["residual_layernorm", "relbias_softmax", "relative_bias", "attention_context", "qkv_proj",
+                            "out_proj", "ffn_up_gelu", "ffn_down"],
                    help="only run this kernel (--kernel-iters launches on rotating buffers) followed by a 256 MiB "
                         "torch copy, for rocprofv3 counter runs; prints the kernel table, no JSON line")
     return p.parse_args()
@@ -129,6 +129,25 @@ def measure_kernels(model_cfg, iters, only=None):
                                       bytes=nbytes, gbs=nbytes / us / 1e3, bound="hbm", launches_per_step=0)
         del sets
 
+    # the relative-position bias alone (the reference's relativeBias kernel):
+    # fp16 bias with masked keys at -65504, [32,16,256,256]
+    if want("relative_bias"):
+        q0 = torch.from_numpy(d["q"]).to(dev)
+        k0 = torch.from_numpy(d["k"]).to(dev)
+        per_set = (2 * B * H * L * D + B * H * L * L) * 2
+        nsets = max(2, ROTATE_BYTES // per_set + 1)
+        sets = [(q0.roll(i, 0).contiguous(), k0.roll(i, 0).contiguous(),
+                 torch.empty((B, H, L, L), dtype=torch.float16, device=dev)) for i in range(nsets)]
+        nbytes = 2 * B * H * L * D * 2 + 2 * 512 * H * D * 2 + B * L * 2 + B * H * L * L * 2
+
+        def rbias(s):
+            fk.deberta_attention(s[0], s[1], None, pk, pq, mask, output="bias", out=s[2])
+
+        us = time_launches(rbias, sets, iters)
+        out["relative_bias"] = dict(kernel="deberta_attention_kernel<16,BIAS>", shape=[B, H, L, L], us=us,
+                                    bytes=nbytes, gbs=nbytes / us / 1e3, bound="hbm", launches_per_step=0)
+        del sets
+
     # attention as the encoder runs it: context output from the fused QKV layout
     T = B * L
     if want("attention_context"):
@@ -138,10 +157,14 @@ def measure_kernels(model_cfg, iters, only=None):
         qv, kv_, vv = (v5[:, :, i].permute(0, 2, 1, 3) for i in range(3))
         us = time_launches(lambda s: fk.deberta_attention(qv, kv_, vv, pk, pq, mask, output="context", out=ctx),
                            [0], iters)
-        flops = 4 * (2 * B * H * L * L * D)  # QK^T, c2p, p2c (direct dot products) and PV
+        # Roofline: 4 T H D fp16 (Q, K, V in, context out) = 67 MB takes 8.4 us at
+        # 8 TB/s, longer than the 17.2 GFLOP (QK^T, c2p, p2c, PV as direct dot
+        # products) take at 2.5 PFLOP/s (6.9 us): bounded by HBM.
+        flops = 4 * (2 * B * H * L * L * D)
+        nbytes = (4 * T * H * D) * 2
         out["attention_context"] = dict(kernel="deberta_attention_kernel<16,CONTEXT>", shape=[B, H, L, D], us=us,
-                                        flops=flops, bytes=(4 * T * H * D) * 2, bound="mfma", launches_per_step=24,
-                                        tflops=flops / us / 1e6)
+                                        flops=flops, bytes=nbytes, gbs=nbytes / us / 1e3, bound="hbm",
+                                        launches_per_step=24, tflops=flops / us / 1e6)
         del qkv, ctx
 
     # the four projections at T = 8192
@@ -161,7 +184,9 @@ def measure_kernels(model_cfg, iters, only=None):
 
         us = time_launches(lin, [0], iters)
         flops = 2 * T * n * k
-        out[name] = dict(kernel="gemm_nt_kernel<256,128>", shape=[T, n, k], us=us, flops=flops,
+        t256 = (T + 255) // 256 * (n // 256)  # the library's tile choice for T >= 2048
+        tile = "256,256" if n % 256 == 0 and (t256 % 256 == 0 or t256 >= 512) else "256,128"
+        out[name] = dict(kernel=f"gemm_nt_lds_kernel<{tile}>", shape=[T, n, k], us=us, flops=flops,
                          tflops=flops / us / 1e6, bound="mfma", launches_per_step=24,
                          bytes=(T * k + n * k + T * n) * 2)
         del a, w, c
@@ -193,7 +218,7 @@ def roofline_of(kernels):
     traffic, source = profiled_traffic(name)
     return dict(kernel=name, bound=best["bound"], achieved=round(ach, 2), peak=peak, unit=unit,
                 frac=round(ach / peak, 4), traffic=traffic, traffic_source=source, avg_us=round(best["us"], 2),
-                algorithmic_per_launch=best.get("flops", best.get("bytes")))
+                algorithmic_per_launch=best["bytes"] if best["bound"] == "hbm" else best["flops"])
 
 
 def profiled_traffic(kernel):
@@ -322,6 +347,8 @@ def main():
         "fused_ln_frac_hbm": round(kernels["residual_layernorm"]["gbs"] / HBM_PEAK_GBS, 4),
         "relbias_softmax_gbs": round(kernels["relbias_softmax"]["gbs"], 1),
         "relbias_softmax_frac_hbm": round(kernels["relbias_softmax"]["gbs"] / HBM_PEAK_GBS, 4),
+        "relative_bias_gbs": round(kernels["relative_bias"]["gbs"], 1),
+        "relative_bias_frac_hbm": round(kernels["relative_bias"]["gbs"] / HBM_PEAK_GBS, 4),
     }
     print(json.dumps(line), flush=True)
 
