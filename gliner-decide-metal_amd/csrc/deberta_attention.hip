@@ -29,6 +29,7 @@
 // the SDPA additive mask (bias), or the context P.V (V^T chunks in LDS, P as
 // the MFMA A operand split into fp16 hi + lo parts).
 #include <cmath>
+#include <type_traits>
 
 #include "gd_common.hpp"
 #include "gd_kernels.hpp"
@@ -210,16 +211,17 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     const half_t* PQs = st + kStageK + kStageWin;
     const int kc = c * kKC;
     const int wlo = win_lo_of(kc);
-    if (active) {
-      // In a linear chunk every (query, key) pair of this wave, and the start
-      // of the workgroup's window, lies in the linear zone with no clipping to
-      // the sequence: every window offset below is closed-form and 16-aligned.
-      const bool lin = (kc + kKC <= L) && (q0 - kc - (kKC - 1) >= -kMid) && (qw + 15 - kc <= kMid) &&
-                       (kc + (kKC - 1) - qw <= kMid);
+    // The chunk's work for this wave.  LIN (a linear chunk: every (query, key)
+    // pair of this wave, and the start of the workgroup's window, lies in the
+    // linear zone with no clipping to the sequence) is a compile-time variant:
+    // every window offset is closed-form and 16-aligned and the body has no
+    // branches, so the scheduler can overlap the tiles freely.
+    auto chunk = [&](auto lin_c) {
+      constexpr bool LIN = decltype(lin_c)::value;
       // c2p for this wave's 16 queries and the chunk's keys: positions
       // [cw_lo, cw_lo + 16 ntw) = window rows [crow0, crow0 + 16 ntw)
       int cw_lo, ntw;
-      if (lin) {
+      if constexpr (LIN) {
         cw_lo = qw - kc - (kKC - 1) + bucket_size;
         ntw = 5;
       } else {
@@ -230,9 +232,9 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       const int crow0 = cw_lo - wlo;
 #pragma unroll
       for (int tw = 0; tw < kC2PCols / 16; ++tw) {
-        if (tw < ntw) {
+        if (LIN || tw < ntw) {
           half8_t a0, a1;
-          if (lin) {
+          if constexpr (LIN) {  // crow0 = 16 wave
             a0 = *reinterpret_cast<const half8_t*>(PKs + (crow0 + 16 * tw) * kD + swz_lo);
             a1 = *reinterpret_cast<const half8_t*>(PKs + (crow0 + 16 * tw) * kD + swz_hi);
           } else {
@@ -264,7 +266,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       auto prep_load = [&](int tt) {
         const int k0 = kc + 16 * tt;
         const int par = tt & 1;
-        if (lin) {
+        if constexpr (LIN) {
           pp_lo[tt] = qw - k0 - 15 + bucket_size;
           nj_t[tt] = 2;
         } else {
@@ -276,8 +278,8 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
         fk[par][1] = *reinterpret_cast<const half8_t*>(Ks + 16 * tt * kD + swz_hi);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          if (j < nj_t[tt]) {
-            if (lin) {  // prow0 = 16 (wave - tt) + 48
+          if (LIN || j < nj_t[tt]) {
+            if constexpr (LIN) {  // prow0 = 16 (wave - tt) + 48
               fq[par][2 * j] = *reinterpret_cast<const half8_t*>(PQs + (prow0 + 16 * j) * kD + swz_lo);
               fq[par][2 * j + 1] = *reinterpret_cast<const half8_t*>(PQs + (prow0 + 16 * j) * kD + swz_hi);
             } else {
@@ -297,7 +299,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
         s_t[tt] = mfma16x16x32(fk[par][1], qf1, sv);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          if (j < nj_t[tt]) {
+          if (LIN || j < nj_t[tt]) {
             float4_t r = {0.f, 0.f, 0.f, 0.f};
             r = mfma16x16x32(fk[par][0], fq[par][2 * j], r);
             r = mfma16x16x32(fk[par][1], fq[par][2 * j + 1], r);
@@ -312,9 +314,11 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
         const int T = 4 * c + tt;
-        if (T >= nt) break;  // uniform
+        if constexpr (!LIN) {
+          if (T >= nt) break;  // uniform; a linear chunk is always full
+        }
         const int k0 = 16 * T;
-        const bool next = tt + 1 < 4 && T + 1 < nt;
+        const bool next = tt + 1 < 4 && (LIN || T + 1 < nt);
         if (next) prep_load(tt + 1);  // fragment reads overlap this tile's gathers
         wave_lds_sync();  // tile tt's p2c stores (and the chunk's c2p) precede its gathers
         // Gather the two terms of score (q = qw + lc, k = k0 + 4g + i) at
@@ -323,7 +327,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
         // in the lane's c2p row and the four p2c terms are one 8-byte read.
         const float4_t madd = *reinterpret_cast<const float4_t*>(mask_add + k0 + 4 * g);
         half4_t c2p, p2c;
-        if ((qw - k0 <= kMid - 15) && (k0 - qw <= kMid - 15)) {
+        if (LIN || ((qw - k0 <= kMid - 15) && (k0 - qw <= kMid - 15))) {
           const half_t* cp = c2p_w + lc * kC2PStride + (qw - k0 + bucket_size - cw_lo) + lc - 4 * g;
 #pragma unroll
           for (int i = 0; i < 4; ++i) c2p[i] = cp[-i];
@@ -353,6 +357,14 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
         }
       }
       wave_lds_sync();  // the last gathers precede the next chunk's c2p / p2c stores
+    };
+    if (active) {
+      const bool lin = (kc + kKC <= L) && (q0 - kc - (kKC - 1) >= -kMid) && (qw + 15 - kc <= kMid) &&
+                       (kc + (kKC - 1) - qw <= kMid);
+      if (lin)
+        chunk(std::true_type{});
+      else
+        chunk(std::false_type{});
     }
   }
   __syncthreads();  // the stage buffers are free from here on
