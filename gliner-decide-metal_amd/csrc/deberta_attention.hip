@@ -216,8 +216,9 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     // linear zone with no clipping to the sequence) is a compile-time variant:
     // every window offset is closed-form and 16-aligned and the body has no
     // branches, so the scheduler can overlap the tiles freely.
-    auto chunk = [&](auto lin_c) {
+    auto chunk = [&](auto lin_c, auto full_c) {
       constexpr bool LIN = decltype(lin_c)::value;
+      constexpr bool FULL = decltype(full_c)::value;  // all 64 keys of the chunk exist (LIN implies FULL)
       // c2p for this wave's 16 queries and the chunk's keys: positions
       // [cw_lo, cw_lo + 16 ntw) = window rows [crow0, crow0 + 16 ntw)
       int cw_lo, ntw;
@@ -314,11 +315,11 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
         const int T = 4 * c + tt;
-        if constexpr (!LIN) {
-          if (T >= nt) break;  // uniform; a linear chunk is always full
+        if constexpr (!FULL) {
+          if (T >= nt) break;  // uniform
         }
         const int k0 = 16 * T;
-        const bool next = tt + 1 < 4 && (LIN || T + 1 < nt);
+        const bool next = tt + 1 < 4 && (FULL || T + 1 < nt);
         if (next) prep_load(tt + 1);  // fragment reads overlap this tile's gathers
         wave_lds_sync();  // tile tt's p2c stores (and the chunk's c2p) precede its gathers
         // Gather the two terms of score (q = qw + lc, k = k0 + 4g + i) at
@@ -362,9 +363,11 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       const bool lin = (kc + kKC <= L) && (q0 - kc - (kKC - 1) >= -kMid) && (qw + 15 - kc <= kMid) &&
                        (kc + (kKC - 1) - qw <= kMid);
       if (lin)
-        chunk(std::true_type{});
+        chunk(std::true_type{}, std::true_type{});
+      else if (kc + kKC <= L)
+        chunk(std::false_type{}, std::true_type{});
       else
-        chunk(std::false_type{});
+        chunk(std::false_type{}, std::false_type{});
     }
   }
   __syncthreads();  // the stage buffers are free from here on
