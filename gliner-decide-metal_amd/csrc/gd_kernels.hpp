@@ -15,6 +15,10 @@ int launch_embedding_layer_norm(const int32_t* ids, const void* mask, const void
                                 const void* beta, void* out, int64_t tokens, int64_t cols, int64_t vocab, float eps,
                                 int32_t* error_flag, hipStream_t stream);
 
+// Fills the per-device GELU table used by the GELU epilogue (first call per
+// device; refuses while `stream` is capturing a graph).
+int ensure_gelu_table(hipStream_t stream);
+
 int launch_linear(const void* a, const void* w, const void* bias, void* c, int64_t m, int64_t n, int64_t k, int64_t lda,
                   int64_t ldc, const int32_t* a_rows, int64_t a_row_count, int epilogue_kind, hipStream_t stream);
 

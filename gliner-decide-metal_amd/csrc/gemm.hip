@@ -21,7 +21,11 @@
 //   * workgroups are dispatched round-robin over the 8 XCDs; the tile order is
 //     remapped so each XCD works on a compact 4-tile-row band and its private
 //     L2 serves the A rows and W columns it shares.
+#include <cmath>
+#include <cstring>
+#include <mutex>
 #include <type_traits>
+#include <vector>
 
 #include "gd_common.hpp"
 #include "gd_kernels.hpp"
@@ -81,6 +85,27 @@ __device__ __forceinline__ half_t epilogue(float acc, float b) {
   if (EPI == GD_EPI_BIAS_GELU) return (half_t)gelu_erf((float)y);
   // GD_EPI_BIAS_RELU
   return y > (half_t)0 ? y : (half_t)0;
+}
+
+// ---------------------------------------------------------------------------
+// GELU by table.  The GELU epilogue's input is the fp16 addMM output, so its
+// correctly rounded fp16 GELU can be looked up: one entry per fp16 value with
+// |y| < 8 (exponent field 0..17, both signs: 2 x 18432 entries, 72 KiB),
+// computed once per device on the host in double precision through erfc (no
+// cancellation in either tail).  |y| >= 8 needs no table: GELU(y) rounds to y
+// for y >= 8 and to -0 for y <= -8; y * 0 gives -0, and NaN for -inf / NaN.
+// ---------------------------------------------------------------------------
+constexpr int kGeluHalf = 18 * 1024;      // entries per sign
+constexpr int kGeluEntries = 2 * kGeluHalf;
+__device__ __attribute__((aligned(16))) half_t g_gelu_table[kGeluEntries];
+
+__device__ __forceinline__ half_t gelu_from_table(half_t y, const half_t* tab) {
+  const uint32_t u = __builtin_bit_cast(uint16_t, y);
+  const uint32_t mag = u & 0x7FFFu;
+  const uint32_t idx = (u >> 15) * kGeluHalf + (mag < (uint32_t)kGeluHalf ? mag : kGeluHalf - 1);
+  const half_t big = (u >> 15) ? (half_t)(y * (half_t)0) : y;
+  const half_t small = tab[idx];
+  return mag < (uint32_t)kGeluHalf ? small : big;
 }
 
 template <int BM, int BN, int EPI, bool GATHER>
@@ -294,8 +319,12 @@ __global__ __launch_bounds__(kThreads8) void gemm_nt_lds_kernel(const half_t* __
   static_assert(RPA % 32 == 0 && NSTAGE * RPA >= BM, "epilogue staging must fit in the stage buffers");
   static_assert((NSTAGE - 1) * LPS < 64, "vmcnt range");
 
+  // The GELU epilogue of a tile whose stage buffer holds 128 rows of C reads
+  // the GELU table from LDS: st1 is sized for it and C goes through st0 in
+  // two passes of RPA rows.
+  constexpr bool GELU_TABLE = EPI == GD_EPI_BIAS_GELU && NSTAGE == 2 && RPA == 128 && BM == 2 * RPA && WM == RPA;
   __shared__ __attribute__((aligned(1024))) half_t st0[STAGE];
-  __shared__ __attribute__((aligned(1024))) half_t st1[STAGE];
+  __shared__ __attribute__((aligned(1024))) half_t st1[GELU_TABLE && kGeluEntries > STAGE ? kGeluEntries : STAGE];
   __shared__ __attribute__((aligned(1024))) half_t st2[NSTAGE > 2 ? STAGE : 8];
   __shared__ __attribute__((aligned(1024))) half_t st3[NSTAGE > 3 ? STAGE : 8];
   __shared__ __attribute__((aligned(1024))) half_t st4[NSTAGE > 4 ? STAGE : 8];
@@ -440,6 +469,60 @@ __global__ __launch_bounds__(kThreads8) void gemm_nt_lds_kernel(const half_t* __
   if constexpr (NSTAGE > 4) if (kt + 3 < nk) step(ic<3>{}, kt + 3);
   __syncthreads();  // all waves done reading the stage buffers; every load landed
 
+  constexpr int CHUNKS_PER_ROW = BN / 8;
+  constexpr int ROWS_PER_PASS = kThreads8 / CHUNKS_PER_ROW;
+  const int cc = t % CHUNKS_PER_ROW;
+  if constexpr (GELU_TABLE) {
+    // ---- GELU epilogue: table into st1, C through st0 in two passes ----
+    // All of this thread's table pieces are loaded before any is stored, so
+    // the L2 latency is paid once.
+    constexpr int kPieces = kGeluEntries / 8;
+    constexpr int kPerThread = (kPieces + kThreads8 - 1) / kThreads8;
+    half8_t piece[kPerThread];
+#pragma unroll
+    for (int r = 0; r < kPerThread; ++r) {
+      const int i = t + r * kThreads8;
+      if (i < kPieces) piece[r] = *reinterpret_cast<const half8_t*>(g_gelu_table + 8 * i);
+    }
+#pragma unroll
+    for (int r = 0; r < kPerThread; ++r) {
+      const int i = t + r * kThreads8;
+      if (i < kPieces) *reinterpret_cast<half8_t*>(st1 + 8 * i) = piece[r];
+    }
+    __syncthreads();
+    half_t res[TM][TN][16];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const float b = (float)bias[tile_n * BN + wn * WN + j * 32 + lr];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) res[i][j][e] = gelu_from_table((half_t)(acc[i][j][e] + b), st1);
+    }
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+      if (wm == pass) {  // this wave's WM = RPA rows are rows [pass * RPA, (pass + 1) * RPA) of the tile
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+              st0[(i * 32 + 4 * lk + 8 * (e >> 2) + (e & 3)) * BN + wn * WN + j * 32 + lr] = res[i][j][e];
+      }
+      __syncthreads();
+#pragma unroll 4
+      for (int r = t / CHUNKS_PER_ROW; r < RPA; r += ROWS_PER_PASS) {
+        const int row = tile_m * BM + pass * RPA + r;
+        if (row < M)
+          *reinterpret_cast<half8_t*>(C + (int64_t)row * ldc + tile_n * BN + cc * 8) =
+              *reinterpret_cast<const half8_t*>(st0 + r * BN + cc * 8);
+      }
+      __syncthreads();
+    }
+    return;
+  }
+
   // ---- epilogue: bias/activation in registers, fp16 tile staged in LDS ----
   // Rows [p * RPA, (p + 1) * RPA) of the tile go to stage buffer p.
   auto rows_of = [&](int p) -> half_t* {
@@ -464,9 +547,6 @@ __global__ __launch_bounds__(kThreads8) void gemm_nt_lds_kernel(const half_t* __
     }
   }
   __syncthreads();
-  constexpr int CHUNKS_PER_ROW = BN / 8;
-  constexpr int ROWS_PER_PASS = kThreads8 / CHUNKS_PER_ROW;
-  const int cc = t % CHUNKS_PER_ROW;
 #pragma unroll 4
   for (int r = t / CHUNKS_PER_ROW; r < BM; r += ROWS_PER_PASS) {
     const int row = tile_m * BM + r;
@@ -524,11 +604,54 @@ int launch_tile(const half_t* A, const half_t* W, const half_t* bias, half_t* C,
   return GD_OK;
 }
 
+// Correctly rounded fp16 GELU of every table entry (host, double precision).
+const std::vector<uint16_t>& gelu_table_host() {
+  static const std::vector<uint16_t> tab = [] {
+    std::vector<uint16_t> v(kGeluEntries);
+    for (int sgn = 0; sgn < 2; ++sgn)
+      for (int mag = 0; mag < kGeluHalf; ++mag) {
+        const uint16_t bits = (uint16_t)((sgn << 15) | mag);
+        half_t yh;
+        std::memcpy(&yh, &bits, 2);
+        const double y = (double)(float)yh;
+        const double g = 0.5 * y * std::erfc(-y / std::sqrt(2.0));  // = 0.5 y (1 + erf(y / sqrt 2))
+        const half_t gh = (half_t)g;  // round to nearest even
+        std::memcpy(&v[sgn * kGeluHalf + mag], &gh, 2);
+      }
+    return v;
+  }();
+  return tab;
+}
+
 }  // namespace
+
+int ensure_gelu_table(hipStream_t stream) {
+  static std::mutex mu;
+  static bool ready[64] = {};
+  int dev = 0;
+  GD_HIP_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) {
+    set_error("device index %d out of range", dev);
+    return GD_ERR_UNSUPPORTED;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (ready[dev]) return GD_OK;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (stream && hipStreamIsCapturing(stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone) {
+    set_error("the GELU table of device %d is filled on first use, which cannot happen during graph capture: "
+              "run one GELU linear (or create the classifier) first", dev);
+    return GD_ERR_UNSUPPORTED;
+  }
+  const std::vector<uint16_t>& tab = gelu_table_host();
+  GD_HIP_CHECK(hipMemcpyToSymbol(HIP_SYMBOL(g_gelu_table), tab.data(), tab.size() * sizeof(uint16_t)));
+  ready[dev] = true;
+  return GD_OK;
+}
 
 int launch_linear(const void* a, const void* w, const void* bias, void* c, int64_t m, int64_t n, int64_t k, int64_t lda,
                   int64_t ldc, const int32_t* a_rows, int64_t a_row_count, int epilogue_kind, hipStream_t stream) {
   if (m == 0) return GD_OK;
+  if (epilogue_kind == GD_EPI_BIAS_GELU) GD_RETURN_IF_ERROR(ensure_gelu_table(stream));
   auto A = static_cast<const half_t*>(a);
   auto Wt = static_cast<const half_t*>(w);
   auto Bv = static_cast<const half_t*>(bias);

@@ -165,6 +165,7 @@ int Classifier::init(const WeightStore& store, const gd_config& cfg, uint32_t fl
     GD_RETURN_IF_ERROR(store.require(req.first, req.second, GD_F16, &t));
   }
   GD_HIP_CHECK(hipGetDevice(&device_));
+  GD_RETURN_IF_ERROR(ensure_gelu_table(stream));  // before any graph capture of the FFN
 
   // ---- weights (DeBERTa.swift:197-229) ----
   GD_RETURN_IF_ERROR(upload(store, "encoder.embeddings.word_embeddings.weight", {V, C}, &word_emb_, stream));
