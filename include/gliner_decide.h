@@ -131,6 +131,10 @@ typedef enum gd_epilogue {
  * n % 128 == 0, lda % 8 == 0, ldc % 8 == 0.  When a_rows is not NULL, row m
  * of A is A[a_rows[m], :] (row gather; used for the marker gather,
  * DeBERTa.swift:431-436); gathered indices are clamped into [0, a_row_count).
+ * The first GD_EPI_BIAS_GELU call on a device fills that device's GELU table
+ * (a synchronous 72 KiB upload); made on a stream that is capturing a graph it
+ * returns GD_ERR_UNSUPPORTED instead, so a caller that captures makes one
+ * GELU call (or creates a classifier) on the device beforehand.
  * Replaces LinearWeight / FusedProjectionWeight addMM (DeBERTa.swift:60-92). */
 int gd_linear(const void* a, const void* w, const void* bias, void* c, int64_t m, int64_t n,
               int64_t k, int64_t lda, int64_t ldc, const int32_t* a_rows, int64_t a_row_count,
