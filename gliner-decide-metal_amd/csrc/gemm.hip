@@ -311,7 +311,7 @@ __global__ __launch_bounds__(kThreads8) void gemm_nt_lds_kernel(const half_t* __
   constexpr int LPS = A_BLK + B_BLK;                    // loads per wave per stage
   constexpr int STAGE = (BM + BN) * BK;                 // halfs per stage buffer
   constexpr int S = BK / 16;                            // MFMA K slices per stage
-  constexpr int RPA = STAGE / BN;                       // epilogue rows per stage buffer
+  constexpr int RPA = STAGE / BN / 32 * 32;             // epilogue rows per stage buffer (32-row groups)
   static_assert(TM >= 1 && TN >= 1 && A_BLK >= 1 && B_BLK >= 1, "tile shape");
   static_assert(S % 2 == 0, "fragment sets alternate per slice");
   static_assert(NSTAGE >= 2 && NSTAGE <= 5, "pipeline depth");
@@ -665,10 +665,15 @@ int launch_linear(const void* a, const void* w, const void* bias, void* c, int64
   }
   if (M >= 2048) {
     // 256 x 256 tiles (two 64-deep stages, 128 KiB of LDS) when they fill
-    // whole waves of the 256 CUs, else 256 x 128 (three stages, 144 KiB).
-    const int t256 = ((M + 255) / 256) * (N / 256);
+    // whole waves of the 256 CUs; else 256 x 192 (two stages, 112 KiB) when
+    // those do (the fused QKV projection, N = 3072); else 256 x 128 (three
+    // stages, 144 KiB).
+    const int tiles_m = (M + 255) / 256;
+    const int t256 = tiles_m * (N / 256);
     if (N % 256 == 0 && (t256 % 256 == 0 || t256 >= 512))
       return launch_lds_tile<256, 256, 2, 64, 2>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
+    if (N % 192 == 0 && (tiles_m * (N / 192)) % 256 == 0)
+      return launch_lds_tile<256, 192, 4, 64, 2>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
     return launch_lds_tile<256, 128, 4, 64, 3>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
   }
   if (M >= 1024) return launch_tile<128, 128, false>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
