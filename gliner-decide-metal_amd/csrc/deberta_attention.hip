@@ -131,16 +131,6 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   const int nchunks = (L + kKC - 1) / kKC;
   const float inv_scale16 = 1.0f / scale16;  // correctly rounded fp32 reciprocal
 
-  for (int i = t; i < 2 * L - 1; i += kThreads) idx_tab[i] = (int16_t)relative_index(i - (L - 1), bucket_size, P);
-  // The key mask of batch row b as an additive term: 0 for a valid key, -inf
-  // (probabilities) or -65504 (the SDPA mask output) for a masked one.
-  for (int i = t; i < L; i += kThreads) {
-    const float m = (float)mask[(int64_t)b * L + i];
-    const bool valid = mask_kind == GD_MASK_ATTENTION ? (m > 0.f) : !(m < -60000.f);
-    mask_add[i] = valid ? 0.f : (OUT == GD_ATTN_OUT_BIAS ? -65504.f : -INFINITY);
-  }
-  __syncthreads();  // the stage windows below are located through the table
-
   const half_t* Kb = K + (int64_t)b * ksb + (int64_t)h * ksh;
   const half_t* PKh = PK + (int64_t)h * pksh;
   const half_t* PQh = PQ + (int64_t)h * pqsh;
@@ -155,11 +145,12 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
 
   // ---- stage loads: lane l of 1 KiB block `blk` writes physical chunk l%8 of
   // row 8*blk + l/8, so it fetches the logical chunk that swz() puts there.
-  // Every block this wave loads has the parity of the wave index. ----
+  // Every block this wave loads has the parity of the wave index.  `wlo` is
+  // the first relative-table row of the chunk's window, idx(q0 - kc - 63). ----
   const int blk_row = lane >> 3;
   const int blk_chunk = (lane & 7) ^ (((wave & 1) << 2) | (lane >> 4));
   auto win_lo_of = [&](int kc) { return idx_clip(q0 - kc - (kKC - 1)); };
-  auto issue_stage = [&](int c, int buf) {
+  auto issue_stage = [&](int c, int buf, int wlo) {
     half_t* st = buf ? stage1 : stage0;
     const int kc = c * kKC;
     {  // K rows: 8 blocks of 8 rows, one per wave
@@ -167,7 +158,6 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       key = key < L ? key : L - 1;
       load_lds16(Kb + (int64_t)key * ksl + blk_chunk * 8, st + wave * 512);
     }
-    const int wlo = win_lo_of(kc);
 #pragma unroll
     for (int j = 0; j < kWin / 8 / kWaves; ++j) {  // 3 blocks per wave per table
       const int blk = wave + kWaves * j;
@@ -177,6 +167,22 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       load_lds16(PQh + (int64_t)p * pqsp + blk_chunk * 8, st + kStageK + kStageWin + blk * 512);
     }
   };
+  // Chunk 0's stage is in flight while the index table and the mask are
+  // built (its window start is computed directly, not through the table).
+  {
+    const int r = q0 - (kKC - 1) < -(L - 1) ? -(L - 1) : q0 - (kKC - 1);
+    issue_stage(0, 0, __builtin_amdgcn_readfirstlane(relative_index(r, bucket_size, P)));
+  }
+
+  for (int i = t; i < 2 * L - 1; i += kThreads) idx_tab[i] = (int16_t)relative_index(i - (L - 1), bucket_size, P);
+  // The key mask of batch row b as an additive term: 0 for a valid key, -inf
+  // (probabilities) or -65504 (the SDPA mask output) for a masked one.
+  for (int i = t; i < L; i += kThreads) {
+    const float m = (float)mask[(int64_t)b * L + i];
+    const bool valid = mask_kind == GD_MASK_ATTENTION ? (m > 0.f) : !(m < -60000.f);
+    mask_add[i] = valid ? 0.f : (OUT == GD_ATTN_OUT_BIAS ? -65504.f : -INFINITY);
+  }
+  __syncthreads();  // the later stage windows are located through the table
 
   // ---- Q fragments (B operand of K Q^T): Q[qw + lc][8g..] and [32 + 8g..] ----
   half8_t qf0 = {}, qf1 = {};
@@ -198,13 +204,12 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) sc[T][i] = -INFINITY;
 
-  issue_stage(0, 0);
 #pragma unroll
   for (int c = 0; c < MAXT / 4; ++c) {
     if (c >= nchunks) break;  // uniform
     wait_vmcnt<0>();
     __syncthreads();  // stage c landed everywhere; every wave is done with stage c - 1
-    if (c + 1 < nchunks) issue_stage(c + 1, (c + 1) & 1);
+    if (c + 1 < nchunks) issue_stage(c + 1, (c + 1) & 1, win_lo_of((c + 1) * kKC));
     const half_t* st = (c & 1) ? stage1 : stage0;
     const half_t* Ks = st;
     const half_t* PKs = st + kStageK;
