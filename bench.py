@@ -346,16 +346,18 @@ def main():
     assert torch.isfinite(logits.float()).all()
     log(f"e2e: {ms:.3f} ms/step, {rows_s:.1f} rows/s")
 
-    mix = None
-    if args.workload == "classify" and not args.no_bucket_mix:
-        mix = bucket_mix_rate(model)
-        log(f"bucket mix: {mix}")
-
     kernels = measure_kernels(cfg, args.kernel_iters)
     for k, v in kernels.items():
         extra = f"{v['gbs']:.0f} GB/s" if "gbs" in v and v["bound"] == "hbm" else f"{v.get('tflops', 0):.0f} TFLOP/s"
         log(f"  {k:20s} {v['us']:9.2f} us  {extra}")
     roof = roofline_of(kernels)
+
+    # after the kernel table: seconds of sustained load change the clocks the
+    # short kernels above would be timed at
+    mix = None
+    if args.workload == "classify" and not args.no_bucket_mix:
+        mix = bucket_mix_rate(model)
+        log(f"bucket mix: {mix}")
 
     cpu = None
     if not args.no_cpu_baseline and args.workload == "classify":
