@@ -192,6 +192,23 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     qf1 = *reinterpret_cast<const half8_t*>(qrow + 32 + 8 * g);
   }
 
+  // ---- V pieces for the P.V pass, fetched now so that the score loop hides
+  // their HBM latency: thread t holds the 16-byte piece (row t / 8, chunk
+  // t % 8) of the 64 x 64 V block of each of the first kVPre key chunks. ----
+  // (one chunk ahead at L > 256, where the scores already hold 128 VGPRs)
+  constexpr int kVPre = OUT == GD_ATTN_OUT_CONTEXT ? (MAXT / 4 < 4 ? MAXT / 4 : (MAXT > 16 ? 1 : 4)) : 1;
+  const half_t* Vb = V + (int64_t)b * vsb + (int64_t)h * vsh;
+  const int vrow = t >> 3, vch = t & 7;
+  auto load_v = [&](int c) -> half8_t {
+    const int key = c * kKC + vrow;
+    return key < L ? *reinterpret_cast<const half8_t*>(Vb + (int64_t)key * vsl + 8 * vch) : half8_t{};
+  };
+  half8_t vbuf[kVPre];
+  if constexpr (OUT == GD_ATTN_OUT_CONTEXT) {
+#pragma unroll
+    for (int c = 0; c < kVPre; ++c) vbuf[c] = load_v(c);
+  }
+
   // Swizzled offsets of this lane's two 16-byte chunks (g and 4 + g) in row
   // 16m + lc of a staged table: the XOR term depends on the row only through
   // lc, so a 16-aligned tile row base is a plain (uniform) offset.
@@ -438,26 +455,40 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   float4_t o[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) o[dt] = (float4_t){0.f, 0.f, 0.f, 0.f};
-  const half_t* Vb = V + (int64_t)b * vsb + (int64_t)h * vsh;
-  const int vrow = t >> 3, vch = t & 7;  // one 16-byte piece of the 64 x 64 chunk per thread
-  half8_t vnext = {};
-  if (vrow < L) vnext = *reinterpret_cast<const half8_t*>(Vb + (int64_t)vrow * vsl + 8 * vch);
 #pragma unroll
   for (int c = 0; c < MAXT / 4; ++c) {
     if (c >= nchunks) break;
     half_t* vt = (c & 1) ? stage1 : stage0;
+    const half8_t vcur = vbuf[c % kVPre];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) vt[(8 * vch + e) * kVtStride + vrow] = vnext[e];
-    if (c + 1 < nchunks) {
-      const int key = (c + 1) * kKC + vrow;
-      vnext = key < L ? *reinterpret_cast<const half8_t*>(Vb + (int64_t)key * vsl + 8 * vch) : half8_t{};
-    }
+    for (int e = 0; e < 8; ++e) vt[(8 * vch + e) * kVtStride + vrow] = vcur[e];
+    if (c + kVPre < nchunks) vbuf[c % kVPre] = load_v(c + kVPre);  // refill the ring
     __syncthreads();
     if (active) {
+      // All of the chunk's V^T fragments first (8 reads in flight), then the
+      // MFMAs in an order where consecutive ones update different
+      // accumulators, so neither LDS latency nor the MFMA dependency of an
+      // accumulator on its previous value is exposed per step.
+      // vb[pr][dt]: keys 32 pr + 4g .. +3 and 32 pr + 16 + 4g .. +3, d = 16 dt + lc
+      half8_t vb[2][4];
 #pragma unroll
-      for (int tt = 0; tt < 4; tt += 2) {
-        const int T = 4 * c + tt;
+      for (int pr = 0; pr < 2; ++pr)
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          const half_t* vr = vt + (16 * dt + lc) * kVtStride + 32 * pr + 4 * g;
+          const half4_t v0 = *reinterpret_cast<const half4_t*>(vr);
+          const half4_t v1 = *reinterpret_cast<const half4_t*>(vr + 16);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            vb[pr][dt][i] = v0[i];
+            vb[pr][dt][4 + i] = v1[i];
+          }
+        }
+#pragma unroll
+      for (int pr = 0; pr < 2; ++pr) {
+        const int T = 4 * c + 2 * pr;
         if (T < nt) {
+          // P of key tiles T, T + 1 as the A operand, split into fp16 hi + lo
           half8_t pa, pl;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
@@ -469,19 +500,9 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
             pl[4 + i] = (half_t)(p1 - (float)pa[4 + i]);
           }
 #pragma unroll
-          for (int dt = 0; dt < 4; ++dt) {
-            const half_t* vr = vt + (16 * dt + lc) * kVtStride;
-            const half4_t v0 = *reinterpret_cast<const half4_t*>(vr + 16 * tt + 4 * g);
-            const half4_t v1 = *reinterpret_cast<const half4_t*>(vr + 16 * (tt + 1) + 4 * g);
-            half8_t vb;
+          for (int dt = 0; dt < 4; ++dt) o[dt] = mfma16x16x32(pa, vb[pr][dt], o[dt]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              vb[i] = v0[i];
-              vb[4 + i] = v1[i];
-            }
-            o[dt] = mfma16x16x32(pa, vb, o[dt]);
-            o[dt] = mfma16x16x32(pl, vb, o[dt]);
-          }
+          for (int dt = 0; dt < 4; ++dt) o[dt] = mfma16x16x32(pl, vb[pr][dt], o[dt]);
         }
       }
     }
