@@ -53,7 +53,7 @@ constexpr int kC2PStride = kC2PCols + 4;  // 168-byte rows keep the 8-byte store
 // conflict-free across the wave.
 constexpr int kP2CSkew = 24;
 constexpr int kP2CRows = 47;       // kr + p <= 15 + 31
-constexpr int kVtStride = 68;      // V^T chunk row (64 keys + pad)
+constexpr int kVRowsA = 448;       // V rows held by one stage buffer (448 x 128 B = 56 KiB)
 
 // LDS map (halfs).  The stage buffers are reused for the V^T chunks and the
 // output staging once the score loop is done.
@@ -64,6 +64,7 @@ constexpr int kScratchWave = 16 * kC2PStride + kP2CRows * kP2CSkew;
 static_assert(16 * 72 <= kScratchWave, "context staging fits a wave's scratch");
 
 typedef __attribute__((address_space(3))) void lds_void_t;
+typedef short short4_t __attribute__((ext_vector_type(4)));
 
 // 16-byte direct-to-LDS load (global_load_lds_dwordx4: lane l's 16 bytes land
 // at M0 + 16 l), issued as inline assembly.  The compiler cannot tell which
@@ -85,11 +86,6 @@ __device__ __forceinline__ void load_lds16(const half_t* g, half_t* lds_block) {
 // (256 B): 16 consecutive rows at the same logical chunk then land on 16
 // distinct (row parity, chunk) bank groups -- conflict-free.
 __device__ __forceinline__ int swz(int row, int chunk) { return row * kD + ((chunk ^ ((row >> 1) & 7)) << 3); }
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | (((N >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8));
-}
 
 template <int MAXT, int OUT>
 __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
@@ -192,22 +188,21 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     qf1 = *reinterpret_cast<const half8_t*>(qrow + 32 + 8 * g);
   }
 
-  // ---- V pieces for the P.V pass, fetched now so that the score loop hides
-  // their HBM latency: thread t holds the 16-byte piece (row t / 8, chunk
-  // t % 8) of the 64 x 64 V block of each of the first kVPre key chunks. ----
-  // (one chunk ahead at L > 256, where the scores already hold 128 VGPRs)
-  constexpr int kVPre = OUT == GD_ATTN_OUT_CONTEXT ? (MAXT / 4 < 4 ? MAXT / 4 : (MAXT > 16 ? 1 : 4)) : 1;
+  // ---- V for the P.V pass: rows [row_lo, row_hi) of the (b, h) slice land
+  // row-major and swizzled like K at rows 0.. of an LDS buffer, by DMA.  Rows
+  // past the sequence repeat row L - 1; their probabilities are exactly 0.
+  // Rows [0, kVRowsA) go to the stage buffer the last chunk leaves free (while
+  // that chunk is computed), rows from kVRowsA on (L > 448) to the other one
+  // after the score loop. ----
   const half_t* Vb = V + (int64_t)b * vsb + (int64_t)h * vsh;
-  const int vrow = t >> 3, vch = t & 7;
-  auto load_v = [&](int c) -> half8_t {
-    const int key = c * kKC + vrow;
-    return key < L ? *reinterpret_cast<const half8_t*>(Vb + (int64_t)key * vsl + 8 * vch) : half8_t{};
+  const int v_rows = ((L + 31) >> 5) << 5;  // the P.V tile pairs reach this far
+  auto issue_v = [&](half_t* dst, int row_lo, int row_hi) {
+    for (int blk = wave; 8 * blk < row_hi - row_lo; blk += kWaves) {  // uniform
+      int key = row_lo + 8 * blk + blk_row;
+      key = key < L ? key : L - 1;
+      load_lds16(Vb + (int64_t)key * vsl + blk_chunk * 8, dst + blk * 512);
+    }
   };
-  half8_t vbuf[kVPre];
-  if constexpr (OUT == GD_ATTN_OUT_CONTEXT) {
-#pragma unroll
-    for (int c = 0; c < kVPre; ++c) vbuf[c] = load_v(c);
-  }
 
   // Swizzled offsets of this lane's two 16-byte chunks (g and 4 + g) in row
   // 16m + lc of a staged table: the XOR term depends on the row only through
@@ -226,7 +221,10 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     if (c >= nchunks) break;  // uniform
     wait_vmcnt<0>();
     __syncthreads();  // stage c landed everywhere; every wave is done with stage c - 1
-    if (c + 1 < nchunks) issue_stage(c + 1, (c + 1) & 1, win_lo_of((c + 1) * kKC));
+    if (c + 1 < nchunks)
+      issue_stage(c + 1, (c + 1) & 1, win_lo_of((c + 1) * kKC));
+    else if constexpr (OUT == GD_ATTN_OUT_CONTEXT)
+      issue_v((c + 1) & 1 ? stage1 : stage0, 0, v_rows < kVRowsA ? v_rows : kVRowsA);
     const half_t* st = (c & 1) ? stage1 : stage0;
     const half_t* Ks = st;
     const half_t* PKs = st + kStageK;
@@ -392,8 +390,16 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
         chunk(std::false_type{}, std::false_type{});
     }
   }
-  __syncthreads();  // the stage buffers are free from here on
+  // The stage buffers are free from here on, except for the V rows in flight
+  // (context only; waited for before the P.V pass).
+  stage_barrier();
+  half_t* const v_lo = (nchunks & 1) ? stage1 : stage0;        // V rows [0, kVRowsA)
+  half_t* const v_hi = (nchunks & 1) ? stage0 : stage1;        // V rows [kVRowsA, v_rows)
+  if constexpr (OUT == GD_ATTN_OUT_CONTEXT && MAXT * 16 > kVRowsA) {
+    if (v_rows > kVRowsA) issue_v(v_hi, kVRowsA, v_rows);
+  }
 
+  float inv_sum = 0.f;
   if (OUT != GD_ATTN_OUT_BIAS) {
     float mx = -INFINITY;
 #pragma unroll
@@ -415,11 +421,14 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       }
     sum += __shfl_xor(sum, 16, 64);
     sum += __shfl_xor(sum, 32, 64);
-    const float inv = sum > 0.f ? 1.0f / sum : 0.f;
+    inv_sum = sum > 0.f ? 1.0f / sum : 0.f;
+    // The context path scales O once at the end instead of every probability.
+    if (OUT == GD_ATTN_OUT_PROBS) {
 #pragma unroll
-    for (int T = 0; T < MAXT; ++T)
+      for (int T = 0; T < MAXT; ++T)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sc[T][i] *= inv;
+        for (int i = 0; i < 4; ++i) sc[T][i] *= inv_sum;
+    }
   }
 
   if (OUT == GD_ATTN_OUT_PROBS || OUT == GD_ATTN_OUT_BIAS) {
@@ -451,70 +460,78 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     return;
   }
 
-  // ---- context: O = P V; V^T chunks in LDS, P (hi + lo) as the A operand ----
+  // ---- context: O = P V with V row-major in LDS, P (hi + lo) as the A operand ----
+  // The B operand (keys x d) is read with ds_read_b64_tr_b16: in each 16-lane
+  // group, source lane s names 4 consecutive halfs and output lane j receives
+  // element j % 4 of source lanes j / 4, 4 + j / 4, 8 + j / 4, 12 + j / 4.
+  // Source lane lc of group g names V[r0 + lc / 4][16 dt + 4 (lc % 4) ..] with
+  // r0 = 16 T + 4 g, so lane (g, lc) receives V[16 T + 4 g + i][16 dt + lc],
+  // i = 0..3: the B fragment of the keys that pa holds for tile T (and, from
+  // r0 + 16, for tile T + 1).  The swizzle term (row >> 1) & 7 of those rows
+  // is (2 g + lc / 8) & 7 for every 16-aligned tile base.
+  wait_vmcnt<0>();
+  stage_barrier();  // every wave's V rows have landed
+  if (!active) return;
   float4_t o[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) o[dt] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  typedef __attribute__((address_space(3))) short4_t lds_short4_t;
+  const int tr_sw = (2 * g + (lc >> 3)) & 7;
+  const int tr_lane = (4 * g + (lc >> 2)) * kD + 4 * (lc & 1);  // row and half offset of this source lane
+  const int tr_c = (lc >> 1) & 1;                                // 16-byte chunk within the 32-byte d slice
 #pragma unroll
   for (int c = 0; c < MAXT / 4; ++c) {
     if (c >= nchunks) break;
-    half_t* vt = (c & 1) ? stage1 : stage0;
-    const half8_t vcur = vbuf[c % kVPre];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) vt[(8 * vch + e) * kVtStride + vrow] = vcur[e];
-    if (c + kVPre < nchunks) vbuf[c % kVPre] = load_v(c + kVPre);  // refill the ring
-    __syncthreads();
-    if (active) {
-      // All of the chunk's V^T fragments first (8 reads in flight), then the
-      // MFMAs in an order where consecutive ones update different
-      // accumulators, so neither LDS latency nor the MFMA dependency of an
-      // accumulator on its previous value is exposed per step.
-      // vb[pr][dt]: keys 32 pr + 4g .. +3 and 32 pr + 16 + 4g .. +3, d = 16 dt + lc
-      half8_t vb[2][4];
+    for (int pr = 0; pr < 2; ++pr) {
+      const int T = 4 * c + 2 * pr;
+      if (T >= nt) break;  // uniform; nt is at most one past the last pair's first tile
+      const int row0 = 16 * T;
+      const half_t* vsrc = row0 < kVRowsA ? v_lo + row0 * kD : v_hi + (row0 - kVRowsA) * kD;
+      // Unnormalised P of key tiles T, T + 1 as the A operand, split into
+      // fp16 hi (truncated) + lo (the exact fp32 remainder, rounded).  Tiles
+      // at or past nt hold exp(-inf) = 0.
+      half8_t pa, pl;
 #pragma unroll
-      for (int pr = 0; pr < 2; ++pr)
+      for (int i = 0; i < 4; i += 2) {
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-          const half_t* vr = vt + (16 * dt + lc) * kVtStride + 32 * pr + 4 * g;
-          const half4_t v0 = *reinterpret_cast<const half4_t*>(vr);
-          const half4_t v1 = *reinterpret_cast<const half4_t*>(vr + 16);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            vb[pr][dt][i] = v0[i];
-            vb[pr][dt][4 + i] = v1[i];
-          }
-        }
-#pragma unroll
-      for (int pr = 0; pr < 2; ++pr) {
-        const int T = 4 * c + 2 * pr;
-        if (T < nt) {
-          // P of key tiles T, T + 1 as the A operand, split into fp16 hi + lo
-          half8_t pa, pl;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float p0 = sc[T][i];
-            const float p1 = (T + 1 < nt) ? sc[T + 1][i] : 0.f;
-            pa[i] = (half_t)p0;
-            pa[4 + i] = (half_t)p1;
-            pl[i] = (half_t)(p0 - (float)pa[i]);
-            pl[4 + i] = (half_t)(p1 - (float)pa[4 + i]);
-          }
-#pragma unroll
-          for (int dt = 0; dt < 4; ++dt) o[dt] = mfma16x16x32(pa, vb[pr][dt], o[dt]);
-#pragma unroll
-          for (int dt = 0; dt < 4; ++dt) o[dt] = mfma16x16x32(pl, vb[pr][dt], o[dt]);
+        for (int u = 0; u < 2; ++u) {
+          const float x0 = sc[T + u][i], x1 = sc[T + u][i + 1];
+          const half2_t hi = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(x0, x1));
+          pa[4 * u + i] = hi[0];
+          pa[4 * u + i + 1] = hi[1];
+          pl[4 * u + i] = (half_t)(x0 - (float)hi[0]);
+          pl[4 * u + i + 1] = (half_t)(x1 - (float)hi[1]);
         }
       }
+      half8_t vb[4];
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const half_t* a = vsrc + tr_lane + (((2 * dt + tr_c) ^ tr_sw) << 3);
+        const short4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(lds_void_t*)a);
+        const short4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(lds_void_t*)(a + 16 * kD));
+        const half4_t h0 = __builtin_bit_cast(half4_t, v0), h1 = __builtin_bit_cast(half4_t, v1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          vb[dt][i] = h0[i];
+          vb[dt][4 + i] = h1[i];
+        }
+      }
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) o[dt] = mfma16x16x32(pa, vb[dt], o[dt]);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) o[dt] = mfma16x16x32(pl, vb[dt], o[dt]);
     }
   }
-  __syncthreads();
-  if (!active) return;
   // lane holds O[qw + 4g + i][16 dt + lc]: stage 16 x 64 in LDS, write 128-byte rows
+  // (the softmax sum of query row r sits in lanes with lc = r)
   half_t* ot = scratch_lds + wave * kScratchWave;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 4; ++i) {
+    const float inv_row = __shfl(inv_sum, 4 * g + i, 64);
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) ot[(4 * g + i) * 72 + 16 * dt + lc] = (half_t)o[dt][i];
+    for (int dt = 0; dt < 4; ++dt) ot[(4 * g + i) * 72 + 16 * dt + lc] = (half_t)(o[dt][i] * inv_row);
+  }
   wave_lds_sync();
   {
     const int r = lane >> 3, cpos = lane & 7;  // 8 rows x 8 pieces per pass

@@ -105,6 +105,25 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// vmcnt(N) with lgkmcnt / expcnt left unconstrained (gfx9 s_waitcnt encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (((N >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Workgroup barrier for pipelines that load LDS by DMA: this wave's LDS
+// accesses are complete (lgkmcnt(0)); global loads, including DMA into LDS
+// still in flight, are waited for explicitly by the caller (__syncthreads
+// would drain them).  The empty asm statements keep the compiler from moving
+// memory accesses across.
+__device__ __forceinline__ void stage_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // MFMA wrappers (gfx950 double-rate fp16 forms).
 //  16x16x32: A lane l -> row l%16, k = 8*(l/16)+[0,8); B lane l -> col l%16,
 //            same k; C lane l -> col l%16, rows 4*(l/16)+[0,4).

@@ -255,22 +255,6 @@ __device__ __forceinline__ void load_lds16(const half_t* g, half_t* lds_block) {
   __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g), (lds_void_t*)(lds_block), 16, 0, 0);
 }
 
-// vmcnt(N) with lgkmcnt / expcnt left unconstrained (gfx9 s_waitcnt encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | (((N >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
-// Workgroup barrier for the pipeline: this wave's LDS reads are complete
-// (lgkmcnt(0)); global loads are waited for explicitly by the caller.  The
-// empty asm statements keep the compiler from moving memory accesses across.
-__device__ __forceinline__ void stage_barrier() {
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
 
 // LDS layout of one operand tile: rows of BK halfs; the 16-byte chunk index
 // is XORed with the row's position inside its 256-byte bank line group, so a
