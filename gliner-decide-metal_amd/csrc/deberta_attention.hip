@@ -133,19 +133,23 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   half_t* c2p_w = scratch_lds + wave * kScratchWave;
   half_t* p2c_w = c2p_w + 16 * kC2PStride;
 
-  // Relative index of a wave-uniform r, clipped to the span of this length.
-  auto idx_clip = [&](int r) -> int {
-    r = r < -(L - 1) ? -(L - 1) : (r > L - 1 ? L - 1 : r);
-    return __builtin_amdgcn_readfirstlane((int)idx_tab[r + L - 1]);
-  };
-
   // ---- stage loads: lane l of 1 KiB block `blk` writes physical chunk l%8 of
   // row 8*blk + l/8, so it fetches the logical chunk that swz() puts there.
   // Every block this wave loads has the parity of the wave index.  `wlo` is
-  // the first relative-table row of the chunk's window, idx(q0 - kc - 63). ----
+  // the relative-table row at window row 0.  The chunk's pairs have
+  // q - k in [bot, top = bot + 190], bot = q0 - kc - 63.  When bot or top lies
+  // in the linear zone [-128, 128], wlo is the linear extrapolation bot + 256:
+  // every index the chunk needs lies in [wlo, wlo + 190] (log buckets keep
+  // |bucket(r)| <= |r| and stay beyond the linear zone's ends), and every
+  // wave whose own pairs are all linear finds its rows at closed-form,
+  // 16-aligned offsets.  Otherwise wlo = idx(bot). ----
   const int blk_row = lane >> 3;
   const int blk_chunk = (lane & 7) ^ (((wave & 1) << 2) | (lane >> 4));
-  auto win_lo_of = [&](int kc) { return idx_clip(q0 - kc - (kKC - 1)); };
+  auto window_lo = [&](int kc, auto&& idx_of) -> int {
+    const int bot = q0 - kc - (kKC - 1), top = bot + kQT + kKC - 2;
+    const bool lin = (bot >= -kMid && bot <= kMid) || (top >= -kMid && top <= kMid);
+    return lin ? bot + bucket_size : idx_of(bot);
+  };
   auto issue_stage = [&](int c, int buf, int wlo) {
     half_t* st = buf ? stage1 : stage0;
     const int kc = c * kKC;
@@ -157,18 +161,17 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
 #pragma unroll
     for (int j = 0; j < kWin / 8 / kWaves; ++j) {  // 3 blocks per wave per table
       const int blk = wave + kWaves * j;
-      int p = wlo + blk * 8 + blk_row;
-      p = p < P ? p : P - 1;
+      int p = wlo + blk * 8 + blk_row;  // rows below 0 or past P - 1 are never read
+      p = p < 0 ? 0 : (p < P ? p : P - 1);
       load_lds16(PKh + (int64_t)p * pksp + blk_chunk * 8, st + kStageK + blk * 512);
       load_lds16(PQh + (int64_t)p * pqsp + blk_chunk * 8, st + kStageK + kStageWin + blk * 512);
     }
   };
   // Chunk 0's stage is in flight while the index table and the mask are
   // built (its window start is computed directly, not through the table).
-  {
-    const int r = q0 - (kKC - 1) < -(L - 1) ? -(L - 1) : q0 - (kKC - 1);
-    issue_stage(0, 0, __builtin_amdgcn_readfirstlane(relative_index(r, bucket_size, P)));
-  }
+  issue_stage(0, 0, window_lo(0, [&](int r) {
+                return __builtin_amdgcn_readfirstlane(relative_index(r < -(L - 1) ? -(L - 1) : r, bucket_size, P));
+              }));
 
   for (int i = t; i < 2 * L - 1; i += kThreads) idx_tab[i] = (int16_t)relative_index(i - (L - 1), bucket_size, P);
   // The key mask of batch row b as an additive term: 0 for a valid key, -inf
@@ -179,6 +182,25 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     mask_add[i] = valid ? 0.f : (OUT == GD_ATTN_OUT_BIAS ? -65504.f : -INFINITY);
   }
   __syncthreads();  // the later stage windows are located through the table
+
+  // Window starts of this wave, one per lane (fetched with readlane): lane
+  // T < MAXT holds idx(qw - 16 T - 15), the first p2c position of key tile T;
+  // lane 32 + c holds idx(qw - 64 c - 63), the first c2p position of chunk c;
+  // lane 48 + c holds wlo of chunk c.
+  int win_tab;
+  {
+    auto idx_lane = [&](int r) -> int {
+      r = r < -(L - 1) ? -(L - 1) : (r > L - 1 ? L - 1 : r);
+      return idx_tab[r + L - 1];
+    };
+    if (lane < 32)
+      win_tab = idx_lane(qw - 16 * lane - 15);
+    else if (lane < 48)
+      win_tab = idx_lane(qw - kKC * (lane - 32) - (kKC - 1));
+    else
+      win_tab = window_lo(kKC * (lane - 48), idx_lane);
+  }
+  auto win = [&](int j) -> int { return __builtin_amdgcn_readlane(win_tab, j); };
 
   // ---- Q fragments (B operand of K Q^T): Q[qw + lc][8g..] and [32 + 8g..] ----
   half8_t qf0 = {}, qf1 = {};
@@ -222,7 +244,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     wait_vmcnt<0>();
     __syncthreads();  // stage c landed everywhere; every wave is done with stage c - 1
     if (c + 1 < nchunks)
-      issue_stage(c + 1, (c + 1) & 1, win_lo_of((c + 1) * kKC));
+      issue_stage(c + 1, (c + 1) & 1, win(48 + c + 1));
     else if constexpr (OUT == GD_ATTN_OUT_CONTEXT)
       issue_v((c + 1) & 1 ? stage1 : stage0, 0, v_rows < kVRowsA ? v_rows : kVRowsA);
     const half_t* st = (c & 1) ? stage1 : stage0;
@@ -230,39 +252,40 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     const half_t* PKs = st + kStageK;
     const half_t* PQs = st + kStageK + kStageWin;
     const int kc = c * kKC;
-    const int wlo = win_lo_of(kc);
-    // The chunk's work for this wave.  LIN (a linear chunk: every (query, key)
-    // pair of this wave, and the start of the workgroup's window, lies in the
-    // linear zone with no clipping to the sequence) is a compile-time variant:
-    // every window offset is closed-form and 16-aligned and the body has no
-    // branches, so the scheduler can overlap the tiles freely.
+    const int wlo = win(48 + c);
+    // The chunk's work for this wave, in compile-time variants whose bodies
+    // have no branches, so the scheduler can overlap the tiles freely.  LIN
+    // (every (query, key) pair of this wave lies in the linear zone): every
+    // window offset is closed-form and 16-aligned and the gathers are
+    // contiguous.  Otherwise the window starts come from the lane table, the
+    // fixed 80 c2p and 32 p2c positions are computed (rows clamped to the
+    // window; the extra ones are never gathered) and every score gathers
+    // through the index table.  FULL: all 64 keys of the chunk exist.
     auto chunk = [&](auto lin_c, auto full_c) {
       constexpr bool LIN = decltype(lin_c)::value;
-      constexpr bool FULL = decltype(full_c)::value;  // all 64 keys of the chunk exist (LIN implies FULL)
+      constexpr bool FULL = decltype(full_c)::value;  // LIN implies FULL
       // c2p for this wave's 16 queries and the chunk's keys: positions
-      // [cw_lo, cw_lo + 16 ntw) = window rows [crow0, crow0 + 16 ntw)
-      int cw_lo, ntw;
-      if constexpr (LIN) {
-        cw_lo = qw - kc - (kKC - 1) + bucket_size;
-        ntw = 5;
-      } else {
-        cw_lo = idx_clip(qw - kc - (kKC - 1));
-        const int cw_hi = idx_clip(qw + 15 - kc);
-        ntw = (cw_hi - cw_lo + 16) >> 4;  // <= 5
-      }
+      // [cw_lo, cw_lo + 80) = window rows [crow0, crow0 + 80)
+      const int cw_lo = LIN ? qw - kc - (kKC - 1) + bucket_size : win(32 + c);
       const int crow0 = cw_lo - wlo;
+      // Off the linear zone a lane's window row r = crow0 + 16 tw + lc may run
+      // past the window; such rows hold positions this wave never gathers and
+      // are clamped to a row with the same r mod 16, so the swizzle term of
+      // the lane is the same for every tile.
+      const int crow_l = crow0 + lc;
+      const int crow_lim = kWin - 16 + (crow_l & 15);
+      const int csw_lo = (g ^ ((crow_l >> 1) & 7)) << 3, csw_hi = ((4 + g) ^ ((crow_l >> 1) & 7)) << 3;
 #pragma unroll
       for (int tw = 0; tw < kC2PCols / 16; ++tw) {
-        if (LIN || tw < ntw) {
+        {
           half8_t a0, a1;
           if constexpr (LIN) {  // crow0 = 16 wave
             a0 = *reinterpret_cast<const half8_t*>(PKs + (crow0 + 16 * tw) * kD + swz_lo);
             a1 = *reinterpret_cast<const half8_t*>(PKs + (crow0 + 16 * tw) * kD + swz_hi);
           } else {
-            int row = crow0 + 16 * tw + lc;
-            row = row < kWin - 1 ? row : kWin - 1;
-            a0 = *reinterpret_cast<const half8_t*>(PKs + swz(row, g));
-            a1 = *reinterpret_cast<const half8_t*>(PKs + swz(row, 4 + g));
+            const int row = crow_l + 16 * tw < crow_lim ? crow_l + 16 * tw : crow_lim;
+            a0 = *reinterpret_cast<const half8_t*>(PKs + row * kD + csw_lo);
+            a1 = *reinterpret_cast<const half8_t*>(PKs + row * kD + csw_hi);
           }
           float4_t r = {0.f, 0.f, 0.f, 0.f};
           r = mfma16x16x32(a0, qf0, r);
@@ -280,34 +303,30 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       // issued before tile tt+1's MFMAs and p2c stores (the LDS executes a
       // wave's accesses in order, so one p2c buffer suffices), and tile tt is
       // combined while those are in flight.
-      int pp_lo[4], nj_t[4];
+      int pp_lo[4];
       float4_t s_t[4];
       half8_t fk[2][2], fq[2][4];  // per tile parity: K rows (chunks g, 4+g), posQ rows (j = 0, 1)
       // Operand fragments of tile tt (LDS reads only; issued a tile ahead).
       auto prep_load = [&](int tt) {
         const int k0 = kc + 16 * tt;
         const int par = tt & 1;
-        if constexpr (LIN) {
-          pp_lo[tt] = qw - k0 - 15 + bucket_size;
-          nj_t[tt] = 2;
-        } else {
-          pp_lo[tt] = idx_clip(qw - k0 - 15);
-          nj_t[tt] = (idx_clip(qw - k0 + 15) - pp_lo[tt] + 16) >> 4;  // 1 or 2
-        }
+        pp_lo[tt] = LIN ? qw - k0 - 15 + bucket_size : win(4 * c + tt);
         const int prow0 = pp_lo[tt] - wlo;
+        const int prow_l = prow0 + lc;  // clamped as the c2p rows
+        const int prow_lim = kWin - 16 + (prow_l & 15);
+        const int psw_lo = (g ^ ((prow_l >> 1) & 7)) << 3, psw_hi = ((4 + g) ^ ((prow_l >> 1) & 7)) << 3;
         fk[par][0] = *reinterpret_cast<const half8_t*>(Ks + 16 * tt * kD + swz_lo);
         fk[par][1] = *reinterpret_cast<const half8_t*>(Ks + 16 * tt * kD + swz_hi);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          if (LIN || j < nj_t[tt]) {
+          {
             if constexpr (LIN) {  // prow0 = 16 (wave - tt) + 48
               fq[par][2 * j] = *reinterpret_cast<const half8_t*>(PQs + (prow0 + 16 * j) * kD + swz_lo);
               fq[par][2 * j + 1] = *reinterpret_cast<const half8_t*>(PQs + (prow0 + 16 * j) * kD + swz_hi);
             } else {
-              int row = prow0 + 16 * j + lc;
-              row = row < kWin - 1 ? row : kWin - 1;
-              fq[par][2 * j] = *reinterpret_cast<const half8_t*>(PQs + swz(row, g));
-              fq[par][2 * j + 1] = *reinterpret_cast<const half8_t*>(PQs + swz(row, 4 + g));
+              const int row = prow_l + 16 * j < prow_lim ? prow_l + 16 * j : prow_lim;
+              fq[par][2 * j] = *reinterpret_cast<const half8_t*>(PQs + row * kD + psw_lo);
+              fq[par][2 * j + 1] = *reinterpret_cast<const half8_t*>(PQs + row * kD + psw_hi);
             }
           }
         }
@@ -320,7 +339,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
         s_t[tt] = mfma16x16x32(fk[par][1], qf1, sv);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          if (LIN || j < nj_t[tt]) {
+          {
             float4_t r = {0.f, 0.f, 0.f, 0.f};
             r = mfma16x16x32(fk[par][0], fq[par][2 * j], r);
             r = mfma16x16x32(fk[par][1], fq[par][2 * j + 1], r);
@@ -343,23 +362,25 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
         if (next) prep_load(tt + 1);  // fragment reads overlap this tile's gathers
         wave_lds_sync();  // tile tt's p2c stores (and the chunk's c2p) precede its gathers
         // Gather the two terms of score (q = qw + lc, k = k0 + 4g + i) at
-        // idx(q - k).  In the linear zone (|q - k| <= 128 over the whole tile)
-        // idx = q - k + 256: the four c2p terms are consecutive (descending)
-        // in the lane's c2p row and the four p2c terms are one 8-byte read.
+        // idx(q - k).  In the linear zone idx = q - k + 256: the four c2p
+        // terms are consecutive (descending) in the lane's c2p row and the
+        // four p2c terms are one 8-byte read.
         const float4_t madd = *reinterpret_cast<const float4_t*>(mask_add + k0 + 4 * g);
         half4_t c2p, p2c;
-        if (LIN || ((qw - k0 <= kMid - 15) && (k0 - qw <= kMid - 15))) {
+        if constexpr (LIN) {
           const half_t* cp = c2p_w + lc * kC2PStride + (qw - k0 + bucket_size - cw_lo) + lc - 4 * g;
 #pragma unroll
           for (int i = 0; i < 4; ++i) c2p[i] = cp[-i];
           p2c = *reinterpret_cast<const half4_t*>(p2c_w + (15 + lc) * kP2CSkew + 4 * g);
         } else {
           const int r0 = qw + lc - k0 - 4 * g + L - 1;
+          const half_t* cb = c2p_w + lc * kC2PStride - cw_lo;
+          const half_t* pb = p2c_w + (4 * g - pp_lo[tt]) * kP2CSkew + 4 * g;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int id = idx_tab[r0 - i];
-            c2p[i] = c2p_w[lc * kC2PStride + (id - cw_lo)];
-            p2c[i] = p2c_w[(4 * g + i + id - pp_lo[tt]) * kP2CSkew + 4 * g + i];
+            const int id = idx_tab[r0 - i];  // 0 <= id < 512
+            c2p[i] = cb[id];
+            p2c[i] = pb[__mul24(id, kP2CSkew) + i * (kP2CSkew + 1)];
           }
         }
         wave_lds_sync();  // these gathers precede the next tile's p2c stores
@@ -380,8 +401,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       wave_lds_sync();  // the last gathers precede the next chunk's c2p / p2c stores
     };
     if (active) {
-      const bool lin = (kc + kKC <= L) && (q0 - kc - (kKC - 1) >= -kMid) && (qw + 15 - kc <= kMid) &&
-                       (kc + (kKC - 1) - qw <= kMid);
+      const bool lin = (kc + kKC <= L) && (qw - kc - (kKC - 1) >= -kMid) && (qw + 15 - kc <= kMid);
       if (lin)
         chunk(std::true_type{}, std::true_type{});
       else if (kc + kKC <= L)
