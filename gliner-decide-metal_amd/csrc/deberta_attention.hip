@@ -29,6 +29,7 @@
 // the SDPA additive mask (bias), or the context P.V (V^T chunks in LDS, P as
 // the MFMA A operand split into fp16 hi + lo parts).
 #include <cmath>
+#include <mutex>
 #include <type_traits>
 
 #include "gd_common.hpp"
@@ -65,6 +66,16 @@ static_assert(16 * 72 <= kScratchWave, "context staging fits a wave's scratch");
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef short short4_t __attribute__((ext_vector_type(4)));
+
+// idx(r) for every r in [-511, 511] at bucket size 256 and 512 positions,
+// filled once per device (ensure_relative_index_table) by relative_index().
+constexpr int kRelSpan = 511;
+__device__ __attribute__((aligned(16))) int16_t g_rel_idx[2 * kRelSpan + 1];
+
+__global__ void fill_relative_index_kernel() {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < 2 * kRelSpan + 1) g_rel_idx[i] = (int16_t)relative_index(i - kRelSpan, 256, 512);
+}
 
 // 16-byte direct-to-LDS load (global_load_lds_dwordx4: lane l's 16 bytes land
 // at M0 + 16 l), issued as inline assembly.  The compiler cannot tell which
@@ -169,11 +180,11 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   };
   // Chunk 0's stage is in flight while the index table and the mask are
   // built (its window start is computed directly, not through the table).
-  issue_stage(0, 0, window_lo(0, [&](int r) {
-                return __builtin_amdgcn_readfirstlane(relative_index(r < -(L - 1) ? -(L - 1) : r, bucket_size, P));
+  issue_stage(0, 0, window_lo(0, [&](int r) -> int {  // arithmetic: a table load would delay the DMA
+                return __builtin_amdgcn_readfirstlane(relative_index(r < -(L - 1) ? -(L - 1) : r, 256, 512));
               }));
 
-  for (int i = t; i < 2 * L - 1; i += kThreads) idx_tab[i] = (int16_t)relative_index(i - (L - 1), bucket_size, P);
+  for (int i = t; i < 2 * L - 1; i += kThreads) idx_tab[i] = g_rel_idx[i - (L - 1) + kRelSpan];
   // The key mask of batch row b as an additive term: 0 for a valid key, -inf
   // (probabilities) or -65504 (the SDPA mask output) for a masked one.
   for (int i = t; i < L; i += kThreads) {
@@ -232,11 +243,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   const int swz_lo = swz(lc, g);
   const int swz_hi = swz(lc, 4 + g);
 
-  float sc[MAXT][4];
-#pragma unroll
-  for (int T = 0; T < MAXT; ++T)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) sc[T][i] = -INFINITY;
+  float sc[MAXT][4];  // tiles at or past nt are set to -inf after the chunk loop
 
 #pragma unroll
   for (int c = 0; c < MAXT / 4; ++c) {
@@ -343,9 +350,10 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
             float4_t r = {0.f, 0.f, 0.f, 0.f};
             r = mfma16x16x32(fk[par][0], fq[par][2 * j], r);
             r = mfma16x16x32(fk[par][1], fq[par][2 * j + 1], r);
-            // lane holds (kr = 4g + i, p = 16 j + lc)
+            // lane holds (kr = 4g + i, p = 16 j + lc); converted in pairs
+            const half4_t rh = __builtin_convertvector(r, half4_t);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) p2c_w[(4 * g + i + 16 * j + lc) * kP2CSkew + 4 * g + i] = (half_t)r[i];
+            for (int i = 0; i < 4; ++i) p2c_w[(4 * g + i + 16 * j + lc) * kP2CSkew + 4 * g + i] = rh[i];
           }
         }
       };
@@ -385,13 +393,14 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
         }
         wave_lds_sync();  // these gathers precede the next tile's p2c stores
         if (next) prep_compute(tt + 1);
+        // fp16(c2p + p2c) is the fp16 add (two packed adds); the division by
+        // fp16(sqrt(3D)) is a multiply by its fp32 reciprocal, which rounds to
+        // the same fp16 value for every finite fp16 numerator (checked
+        // exhaustively).
+        const half4_t sum16 = c2p + p2c;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          // fp16(c2p + p2c) is the fp16 add; the division by fp16(sqrt(3D)) is a
-          // multiply by its fp32 reciprocal, which rounds to the same fp16 value
-          // for every finite fp16 numerator (checked exhaustively).
-          const half_t sum16 = c2p[i] + p2c[i];
-          const float bias16 = round_f16((float)sum16 * inv_scale16);
+          const float bias16 = round_f16((float)sum16[i] * inv_scale16);
           if (OUT == GD_ATTN_OUT_BIAS)
             sc[T][i] = round_f16(bias16 + madd[i]);
           else
@@ -409,6 +418,13 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       else
         chunk(std::false_type{}, std::false_type{});
     }
+  }
+  if (nt < MAXT) {  // key tiles past the sequence take no part in the softmax
+#pragma unroll
+    for (int T = 0; T < MAXT; ++T)
+      if (T >= nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc[T][i] = -INFINITY;
   }
   // The stage buffers are free from here on, except for the V rows in flight
   // (context only; waited for before the P.V pass).
@@ -430,12 +446,15 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float mref = mx == -INFINITY ? 0.f : mx;
     constexpr float kLog2e = 1.4426950408889634f;
+    // exp(s - m) = 2^(s log2e - m log2e) as one fma per score; the rounding
+    // of m log2e scales the whole row alike and cancels in the normalisation.
+    const float mref_l2 = mref * kLog2e;
     float sum = 0.f;
 #pragma unroll
     for (int T = 0; T < MAXT; ++T)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float e = __builtin_amdgcn_exp2f((sc[T][i] - mref) * kLog2e);  // v_exp_f32; exp2(-inf) = 0
+        const float e = __builtin_amdgcn_exp2f(fmaf(sc[T][i], kLog2e, -mref_l2));  // v_exp_f32; exp2(-inf) = 0
         sc[T][i] = e;
         sum += e;
       }
@@ -598,7 +617,33 @@ int launch2(const AttentionArgs& a, hipStream_t stream) {
 
 }  // namespace
 
+int ensure_relative_index_table(hipStream_t stream) {
+  static std::mutex mu;
+  static bool ready[64] = {};
+  int dev = 0;
+  GD_HIP_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) {
+    set_error("device index %d out of range", dev);
+    return GD_ERR_UNSUPPORTED;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (ready[dev]) return GD_OK;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (stream && hipStreamIsCapturing(stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone) {
+    set_error("the relative index table of device %d is filled on first use, which cannot happen during graph "
+              "capture: run one attention call (or create the classifier) first", dev);
+    return GD_ERR_UNSUPPORTED;
+  }
+  hipLaunchKernelGGL(fill_relative_index_kernel, dim3((2 * kRelSpan + 1 + 255) / 256), dim3(256), 0, stream);
+  GD_LAUNCH_CHECK();
+  GD_HIP_CHECK(hipStreamSynchronize(stream));  // visible to every stream from here on
+  ready[dev] = true;
+  return GD_OK;
+}
+
 int launch_deberta_attention(const AttentionArgs& a, hipStream_t stream) {
+  if (a.bucket_size != 256 || a.P != 512) return fail(GD_ERR_SHAPE, "attention: bucket size 256 and 512 positions");
+  GD_RETURN_IF_ERROR(ensure_relative_index_table(stream));
   if (a.L <= 64) return launch2<4>(a, stream);
   if (a.L <= 128) return launch2<8>(a, stream);
   if (a.L <= 256) return launch2<16>(a, stream);

@@ -18,6 +18,9 @@ int launch_embedding_layer_norm(const int32_t* ids, const void* mask, const void
 // Fills the per-device GELU table used by the GELU epilogue (first call per
 // device; refuses while `stream` is capturing a graph).
 int ensure_gelu_table(hipStream_t stream);
+// Fills the device's relative index table used by launch_deberta_attention
+// (first call per device; not allowed during graph capture).
+int ensure_relative_index_table(hipStream_t stream);
 
 int launch_linear(const void* a, const void* w, const void* bias, void* c, int64_t m, int64_t n, int64_t k, int64_t lda,
                   int64_t ldc, const int32_t* a_rows, int64_t a_row_count, int epilogue_kind, hipStream_t stream);

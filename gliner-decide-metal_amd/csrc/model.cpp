@@ -166,6 +166,7 @@ int Classifier::init(const WeightStore& store, const gd_config& cfg, uint32_t fl
   }
   GD_HIP_CHECK(hipGetDevice(&device_));
   GD_RETURN_IF_ERROR(ensure_gelu_table(stream));  // before any graph capture of the FFN
+  GD_RETURN_IF_ERROR(ensure_relative_index_table(stream));  // and of the attention
 
   // ---- weights (DeBERTa.swift:197-229) ----
   GD_RETURN_IF_ERROR(upload(store, "encoder.embeddings.word_embeddings.weight", {V, C}, &word_emb_, stream));
