@@ -90,6 +90,12 @@ __device__ __forceinline__ void load_lds16(const half_t* g, half_t* lds_block) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)lds_block);
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
 }
+// The same with a wave-uniform base address and a 32-bit byte offset per lane.
+__device__ __forceinline__ void load_lds16(const half_t* sbase, uint32_t voff, half_t* lds_block) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)lds_block);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(m0)
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // 128-byte rows; the 16-byte chunk index is XORed with bits 1..3 of the row.
@@ -153,13 +159,20 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   // every index the chunk needs lies in [wlo, wlo + 190] (log buckets keep
   // |bucket(r)| <= |r| and stay beyond the linear zone's ends), and every
   // wave whose own pairs are all linear finds its rows at closed-form,
-  // 16-aligned offsets.  Otherwise wlo = idx(bot). ----
+  // 16-aligned offsets.  Otherwise wlo = idx(bot).  wlo is then clamped to
+  // [0, 512 - 192] so that every window row exists (the indices lie in
+  // [0, 511]); the clamp moves only windows with no all-linear wave (their
+  // bot lies in (64, 128] or below -256). ----
   const int blk_row = lane >> 3;
   const int blk_chunk = (lane & 7) ^ (((wave & 1) << 2) | (lane >> 4));
+  // byte offsets of this lane's 16-byte piece from a block's first table row
+  const uint32_t pk_lane = (uint32_t)((blk_row * pksp + blk_chunk * 8) * 2);
+  const uint32_t pq_lane = (uint32_t)((blk_row * pqsp + blk_chunk * 8) * 2);
   auto window_lo = [&](int kc, auto&& idx_of) -> int {
     const int bot = q0 - kc - (kKC - 1), top = bot + kQT + kKC - 2;
     const bool lin = (bot >= -kMid && bot <= kMid) || (top >= -kMid && top <= kMid);
-    return lin ? bot + bucket_size : idx_of(bot);
+    const int w = lin ? bot + bucket_size : idx_of(bot);
+    return w < 0 ? 0 : (w > 512 - kWin ? 512 - kWin : w);
   };
   auto issue_stage = [&](int c, int buf, int wlo) {
     half_t* st = buf ? stage1 : stage0;
@@ -170,12 +183,11 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       load_lds16(Kb + (int64_t)key * ksl + blk_chunk * 8, st + wave * 512);
     }
 #pragma unroll
-    for (int j = 0; j < kWin / 8 / kWaves; ++j) {  // 3 blocks per wave per table
+    for (int j = 0; j < kWin / 8 / kWaves; ++j) {  // 3 blocks per wave per table; rows wlo .. wlo + 191 exist
       const int blk = wave + kWaves * j;
-      int p = wlo + blk * 8 + blk_row;  // rows below 0 or past P - 1 are never read
-      p = p < 0 ? 0 : (p < P ? p : P - 1);
-      load_lds16(PKh + (int64_t)p * pksp + blk_chunk * 8, st + kStageK + blk * 512);
-      load_lds16(PQh + (int64_t)p * pqsp + blk_chunk * 8, st + kStageK + kStageWin + blk * 512);
+      const int p0 = wlo + blk * 8;  // uniform
+      load_lds16(PKh + (int64_t)p0 * pksp, pk_lane, st + kStageK + blk * 512);
+      load_lds16(PQh + (int64_t)p0 * pqsp, pq_lane, st + kStageK + kStageWin + blk * 512);
     }
   };
   // Chunk 0's stage is in flight while the index table and the mask are
