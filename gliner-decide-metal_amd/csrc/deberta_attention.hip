@@ -196,35 +196,30 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
                 return __builtin_amdgcn_readfirstlane(relative_index(r < -(L - 1) ? -(L - 1) : r, 256, 512));
               }));
 
-  for (int i = t; i < 2 * L - 1; i += kThreads) idx_tab[i] = g_rel_idx[i - (L - 1) + kRelSpan];
-  // The key mask of batch row b as an additive term: 0 for a valid key, -inf
-  // (probabilities) or -65504 (the SDPA mask output) for a masked one.
-  for (int i = t; i < L; i += kThreads) {
-    const float m = (float)mask[(int64_t)b * L + i];
-    const bool valid = mask_kind == GD_MASK_ATTENTION ? (m > 0.f) : !(m < -60000.f);
-    mask_add[i] = valid ? 0.f : (OUT == GD_ATTN_OUT_BIAS ? -65504.f : -INFINITY);
-  }
-  __syncthreads();  // the later stage windows are located through the table
-
+  // Every global read of the set-up is issued before any of them is used, so
+  // the set-up waits for memory once: this thread's (at most two) entries of
+  // the index table, its key-mask entry, its lane of the window table below
+  // and the Q fragments.
+  static_assert(2 * kThreads >= 2 * 16 * MAXT - 1 && kThreads >= 16 * MAXT, "one pass of set-up reads");
+  auto rel = [&](int r) -> int {
+    r = r < -(L - 1) ? -(L - 1) : (r > L - 1 ? L - 1 : r);
+    return g_rel_idx[r + kRelSpan];
+  };
+  const int n_idx = 2 * L - 1;
+  const int16_t id0 = t < n_idx ? g_rel_idx[t - (L - 1) + kRelSpan] : (int16_t)0;
+  const int16_t id1 = t + kThreads < n_idx ? g_rel_idx[t + kThreads - (L - 1) + kRelSpan] : (int16_t)0;
+  const half_t mval = t < L ? mask[(int64_t)b * L + t] : (half_t)0;
   // Window starts of this wave, one per lane (fetched with readlane): lane
   // T < MAXT holds idx(qw - 16 T - 15), the first p2c position of key tile T;
   // lane 32 + c holds idx(qw - 64 c - 63), the first c2p position of chunk c;
   // lane 48 + c holds wlo of chunk c.
   int win_tab;
-  {
-    auto idx_lane = [&](int r) -> int {
-      r = r < -(L - 1) ? -(L - 1) : (r > L - 1 ? L - 1 : r);
-      return idx_tab[r + L - 1];
-    };
-    if (lane < 32)
-      win_tab = idx_lane(qw - 16 * lane - 15);
-    else if (lane < 48)
-      win_tab = idx_lane(qw - kKC * (lane - 32) - (kKC - 1));
-    else
-      win_tab = window_lo(kKC * (lane - 48), idx_lane);
-  }
-  auto win = [&](int j) -> int { return __builtin_amdgcn_readlane(win_tab, j); };
-
+  if (lane < 32)
+    win_tab = rel(qw - 16 * lane - 15);
+  else if (lane < 48)
+    win_tab = rel(qw - kKC * (lane - 32) - (kKC - 1));
+  else
+    win_tab = window_lo(kKC * (lane - 48), rel);
   // ---- Q fragments (B operand of K Q^T): Q[qw + lc][8g..] and [32 + 8g..] ----
   half8_t qf0 = {}, qf1 = {};
   if (active) {
@@ -232,6 +227,17 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     qf0 = *reinterpret_cast<const half8_t*>(qrow + 8 * g);
     qf1 = *reinterpret_cast<const half8_t*>(qrow + 32 + 8 * g);
   }
+  if (t < n_idx) idx_tab[t] = id0;
+  if (t + kThreads < n_idx) idx_tab[t + kThreads] = id1;
+  // The key mask of batch row b as an additive term: 0 for a valid key, -inf
+  // (probabilities) or -65504 (the SDPA mask output) for a masked one.
+  if (t < L) {
+    const float m = (float)mval;
+    const bool valid = mask_kind == GD_MASK_ATTENTION ? (m > 0.f) : !(m < -60000.f);
+    mask_add[t] = valid ? 0.f : (OUT == GD_ATTN_OUT_BIAS ? -65504.f : -INFINITY);
+  }
+  __syncthreads();  // the index table and the mask are complete
+  auto win = [&](int j) -> int { return __builtin_amdgcn_readlane(win_tab, j); };
 
   // ---- V for the P.V pass: rows [row_lo, row_hi) of the (b, h) slice land
   // row-major and swizzled like K at rows 0.. of an LDS buffer, by DMA.  Rows
