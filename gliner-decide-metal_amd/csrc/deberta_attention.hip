@@ -3,8 +3,11 @@
 // Reference: DeBERTa.swift:322-395 (relative bias from the fp16 c2pRaw/p2cRaw
 // gathers, additive key mask, SDPA) with the index math of :498-551.
 //
-// One workgroup = (batch b, head h, 128 queries): 8 waves, wave w owns queries
-// q0 + 16w .. q0 + 16w + 15.  Keys stream through LDS in chunks of 64.  For
+// One work item = (batch b, head h, 128 queries), run by a workgroup of 8
+// waves, wave w owning queries q0 + 16w .. q0 + 16w + 15.  The LDS holds one
+// workgroup per CU; up to L = 256 the grid has one workgroup per CU, each
+// looping over items and fetching the next item's first stage while it
+// finishes the current one.  Keys stream through LDS in chunks of 64.  For
 // a chunk, every relative index the workgroup can need, idx(q - k) for its
 // 128 queries and the chunk's 64 keys, lies in one window of at most 191
 // consecutive rows of the relative tables (idx is monotone in q - k), so the
@@ -28,6 +31,8 @@
 // outputs leave through LDS as 16-byte row segments: P rows (probabilities),
 // the SDPA additive mask (bias), or the context P.V (V^T chunks in LDS, P as
 // the MFMA A operand split into fp16 hi + lo parts).
+#include <atomic>
+#include <climits>
 #include <cmath>
 #include <mutex>
 #include <type_traits>
@@ -65,6 +70,7 @@ constexpr int kScratchWave = 16 * kC2PStride + kP2CRows * kP2CSkew;
 static_assert(16 * 72 <= kScratchWave, "context staging fits a wave's scratch");
 
 typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) half_t lds_half_t;
 typedef short short4_t __attribute__((ext_vector_type(4)));
 
 // idx(r) for every r in [-511, 511] at bucket size 256 and 512 positions,
@@ -86,13 +92,19 @@ __global__ void fill_relative_index_kernel() {
 // read).  M0 is not used by anything else in this kernel.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void load_lds16(const half_t* g, half_t* lds_block) {
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)lds_block);
+__device__ __forceinline__ void load_lds16(const half_t* g, lds_half_t* lds_block) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_block);
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
 }
 // The same with a wave-uniform base address and a 32-bit byte offset per lane.
-__device__ __forceinline__ void load_lds16(const half_t* sbase, uint32_t voff, half_t* lds_block) {
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)lds_block);
+__device__ __forceinline__ void load_lds16(const half_t* sbase, uint32_t voff, lds_half_t* lds_block) {
+  // (readfirstlane returns int: each half goes through uint32_t so that the
+  // low half is not sign-extended into the high one)
+  const uint64_t a = (uint64_t)(uintptr_t)sbase;
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
+  sbase = (const half_t*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_block);
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(m0)
                : "memory", "m0");
 }
@@ -104,32 +116,34 @@ __device__ __forceinline__ void load_lds16(const half_t* sbase, uint32_t voff, h
 // distinct (row parity, chunk) bank groups -- conflict-free.
 __device__ __forceinline__ int swz(int row, int chunk) { return row * kD + ((chunk ^ ((row >> 1) & 7)) << 3); }
 
+// Workgroups loop over items up to L = 256 (16 key tiles).
+template <int MAXT>
+constexpr bool attention_persistent() {
+  return MAXT <= 16;
+}
+
 template <int MAXT, int OUT>
 __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
-    const half_t* __restrict__ Q, const half_t* __restrict__ K, const half_t* __restrict__ V, int64_t qsb, int64_t qsh,
-    int64_t qsl, int64_t ksb, int64_t ksh, int64_t ksl, int64_t vsb, int64_t vsh, int64_t vsl,
-    const half_t* __restrict__ PK, const half_t* __restrict__ PQ, int64_t pksh, int64_t pksp, int64_t pqsh,
-    int64_t pqsp, const half_t* __restrict__ mask, int mask_kind, int B, int H, int L, int P, int bucket_size,
-    float scale_qk, float scale16, half_t* __restrict__ out, int64_t ldo) {
-  // Two stage buffers and the per-wave scratch are separate LDS objects: with
-  // the chunk loop unrolled, every access names its buffer at compile time,
-  // so reads of one stage wait only for that stage's DMA, never for the next
-  // stage's loads in flight.
-  __shared__ __attribute__((aligned(1024))) half_t stage0[kStage];
-  __shared__ __attribute__((aligned(1024))) half_t stage1[kStage];
+    const half_t* __restrict__ Q, const half_t* __restrict__ K, const half_t* __restrict__ V, int qsb, int qsh,
+    int qsl, int ksb, int ksh, int ksl, int vsb, int vsh, int vsl, const half_t* __restrict__ PK,
+    const half_t* __restrict__ PQ, int pksh, int pksp, int pqsh, int pqsp, const half_t* __restrict__ mask,
+    int mask_kind, int B, int H, int L, int P, int bucket_size, float scale_qk, float scale16,
+    half_t* __restrict__ out, int ldo) {
+  // Two stage buffers and the per-wave scratch.  The stage DMA is inline
+  // assembly the compiler does not track, so its reads of a stage never wait
+  // for the next stage's loads in flight; the kernel orders them itself
+  // (vmcnt + barrier before a stage is read).
+  __shared__ __attribute__((aligned(1024))) half_t stages[2 * kStage];  // stage buffers 0 and 1
   __shared__ __attribute__((aligned(1024))) half_t scratch_lds[kWaves * kScratchWave];
   __shared__ int16_t idx_tab[2 * 16 * MAXT];
   __shared__ __attribute__((aligned(16))) float mask_add[16 * MAXT];
 
+  // The stage buffers as LDS pointers: the DMA and the transposing reads
+  // address them through these (no generic-to-LDS casts of computed pointers).
+  lds_half_t* const stages3 = (lds_half_t*)(lds_void_t*)stages;
+  constexpr bool kPersistent = attention_persistent<MAXT>();
   const int ntq = (L + kQT - 1) / kQT;
   const int nblk = B * H * ntq;
-  int bid = blockIdx.x;
-  if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);  // a (b, h)'s query tiles share an XCD
-  const int qt = bid % ntq;
-  const int bh = bid / ntq;
-  const int h = bh % H;
-  const int b = bh / H;
-
   const int t = threadIdx.x;
   const int lane = t & 63;
   // Wave-uniform values live in scalar registers: branches on them are scalar
@@ -137,16 +151,9 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int lc = lane & 15;  // MFMA output column: the lane's query
   const int g = lane >> 4;   // lane group
-  const int q0 = qt * kQT;
-  const int qw = q0 + 16 * wave;
-  const bool active = qw < L;
   const int nt = L >> 4;
   const int nchunks = (L + kKC - 1) / kKC;
   const float inv_scale16 = 1.0f / scale16;  // correctly rounded fp32 reciprocal
-
-  const half_t* Kb = K + (int64_t)b * ksb + (int64_t)h * ksh;
-  const half_t* PKh = PK + (int64_t)h * pksh;
-  const half_t* PQh = PQ + (int64_t)h * pqsh;
   half_t* c2p_w = scratch_lds + wave * kScratchWave;
   half_t* p2c_w = c2p_w + 16 * kC2PStride;
 
@@ -168,15 +175,14 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   // byte offsets of this lane's 16-byte piece from a block's first table row
   const uint32_t pk_lane = (uint32_t)((blk_row * pksp + blk_chunk * 8) * 2);
   const uint32_t pq_lane = (uint32_t)((blk_row * pqsp + blk_chunk * 8) * 2);
-  auto window_lo = [&](int kc, auto&& idx_of) -> int {
+  auto window_lo = [&](int q0, int kc, auto&& idx_of) -> int {
     const int bot = q0 - kc - (kKC - 1), top = bot + kQT + kKC - 2;
     const bool lin = (bot >= -kMid && bot <= kMid) || (top >= -kMid && top <= kMid);
     const int w = lin ? bot + bucket_size : idx_of(bot);
     return w < 0 ? 0 : (w > 512 - kWin ? 512 - kWin : w);
   };
-  auto issue_stage = [&](int c, int buf, int wlo) {
-    half_t* st = buf ? stage1 : stage0;
-    const int kc = c * kKC;
+  // Stage of key chunk kc into buffer st: kStageOps DMA instructions per wave.
+  auto issue_stage = [&](lds_half_t* st, const half_t* Kb, const half_t* PKh, const half_t* PQh, int kc, int wlo) {
     {  // K rows: 8 blocks of 8 rows, one per wave
       int key = kc + wave * 8 + blk_row;
       key = key < L ? key : L - 1;
@@ -190,421 +196,540 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       load_lds16(PQh + (int64_t)p0 * pqsp, pq_lane, st + kStageK + kStageWin + blk * 512);
     }
   };
-  // Chunk 0's stage is in flight while the index table and the mask are
-  // built (its window start is computed directly, not through the table).
-  issue_stage(0, 0, window_lo(0, [&](int r) -> int {  // arithmetic: a table load would delay the DMA
-                return __builtin_amdgcn_readfirstlane(relative_index(r < -(L - 1) ? -(L - 1) : r, 256, 512));
-              }));
-
-  // Every global read of the set-up is issued before any of them is used, so
-  // the set-up waits for memory once: this thread's (at most two) entries of
-  // the index table, its key-mask entry, its lane of the window table below
-  // and the Q fragments.
-  static_assert(2 * kThreads >= 2 * 16 * MAXT - 1 && kThreads >= 16 * MAXT, "one pass of set-up reads");
-  auto rel = [&](int r) -> int {
+  constexpr int kStageOps = 1 + 2 * (kWin / 8 / kWaves);
+  auto rel = [&](int r) -> int {  // idx(r) from the device table
     r = r < -(L - 1) ? -(L - 1) : (r > L - 1 ? L - 1 : r);
     return g_rel_idx[r + kRelSpan];
   };
+  auto rel_arith = [&](int r) -> int {  // idx(r) computed: no memory wait in front of a DMA
+    return relative_index(r < -(L - 1) ? -(L - 1) : r, 256, 512);
+  };
+
+  // ---- work items: (b, h, 128-query tile).  Up to L = 256 the grid holds
+  // at most one workgroup per CU (the LDS allows no more) and workgroup w
+  // takes items w, w + gridDim.x, ...; beyond, the scores fill the registers
+  // and every workgroup takes one item.  Item ids map so that a (b, h)'s query tiles share an
+  // XCD.  Each item's first stage and per-thread set-up reads are issued
+  // while the previous item finishes (last chunk, softmax, P.V, stores), into
+  // the stage buffer that item no longer needs. ----
+  struct Item {
+    int b, h, qt;
+  };
+  auto decode = [&](int item) -> Item {
+    int bid = item;
+    if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+    const int bh = bid / ntq;
+    return Item{__builtin_amdgcn_readfirstlane(bh / H), __builtin_amdgcn_readfirstlane(bh % H),
+                __builtin_amdgcn_readfirstlane(bid % ntq)};
+  };
+  // Window start of chunk 0 per query tile (at most 4), lane qt of w0_tab.
+  const int w0_tab = window_lo(kQT * (lane & 3), 0, rel_arith);
+  auto stage0_of = [&](const Item& it, lds_half_t* st) {
+    issue_stage(st, K + (int64_t)it.b * ksb + (int64_t)it.h * ksh, PK + (int64_t)it.h * pksh,
+                PQ + (int64_t)it.h * pqsh, 0, __builtin_amdgcn_readlane(w0_tab, it.qt));
+  };
+  // Per-thread set-up reads of an item: its key-mask entry, its lane of the
+  // window table and the Q fragments.  Window table (read with readlane):
+  // lane T < MAXT holds idx(qw - 16 T - 15), the first p2c position of key
+  // tile T; lane 32 + c holds idx(qw - 64 c - 63), the first c2p position of
+  // chunk c; lane 48 + c holds wlo of chunk c.
+  static_assert(2 * kThreads >= 2 * 16 * MAXT - 1 && kThreads >= 16 * MAXT, "one pass of set-up reads");
+  struct Setup {
+    half8_t qf0, qf1;  // Q[qw + lc][8g..] and [32 + 8g..] (B operand of K Q^T)
+    int win_tab;
+    half_t mval;
+  };
+  auto setup_of = [&](const Item& it) -> Setup {
+    Setup su;
+    const int q0 = it.qt * kQT, qw = q0 + 16 * wave;
+    su.mval = t < L ? mask[(int64_t)it.b * L + t] : (half_t)0;
+    if (lane < 32)
+      su.win_tab = rel(qw - 16 * lane - 15);
+    else if (lane < 48)
+      su.win_tab = rel(qw - kKC * (lane - 32) - (kKC - 1));
+    else
+      su.win_tab = window_lo(q0, kKC * (lane - 48), rel);
+    su.qf0 = half8_t{};
+    su.qf1 = half8_t{};
+    if (qw < L) {
+      const half_t* qrow = Q + (int64_t)it.b * qsb + (int64_t)it.h * qsh + (int64_t)(qw + lc) * qsl;
+      su.qf0 = *reinterpret_cast<const half8_t*>(qrow + 8 * g);
+      su.qf1 = *reinterpret_cast<const half8_t*>(qrow + 32 + 8 * g);
+    }
+    return su;
+  };
+
+  int item = blockIdx.x;
+  Item cur = decode(item);
+  stage0_of(cur, stages3);
+  // The index table, the same for every item, is built once.
   const int n_idx = 2 * L - 1;
   const int16_t id0 = t < n_idx ? g_rel_idx[t - (L - 1) + kRelSpan] : (int16_t)0;
   const int16_t id1 = t + kThreads < n_idx ? g_rel_idx[t + kThreads - (L - 1) + kRelSpan] : (int16_t)0;
-  const half_t mval = t < L ? mask[(int64_t)b * L + t] : (half_t)0;
-  // Window starts of this wave, one per lane (fetched with readlane): lane
-  // T < MAXT holds idx(qw - 16 T - 15), the first p2c position of key tile T;
-  // lane 32 + c holds idx(qw - 64 c - 63), the first c2p position of chunk c;
-  // lane 48 + c holds wlo of chunk c.
-  int win_tab;
-  if (lane < 32)
-    win_tab = rel(qw - 16 * lane - 15);
-  else if (lane < 48)
-    win_tab = rel(qw - kKC * (lane - 32) - (kKC - 1));
-  else
-    win_tab = window_lo(kKC * (lane - 48), rel);
-  // ---- Q fragments (B operand of K Q^T): Q[qw + lc][8g..] and [32 + 8g..] ----
-  half8_t qf0 = {}, qf1 = {};
-  if (active) {
-    const half_t* qrow = Q + (int64_t)b * qsb + (int64_t)h * qsh + (int64_t)(qw + lc) * qsl;
-    qf0 = *reinterpret_cast<const half8_t*>(qrow + 8 * g);
-    qf1 = *reinterpret_cast<const half8_t*>(qrow + 32 + 8 * g);
-  }
+  Setup cs = setup_of(cur);
   if (t < n_idx) idx_tab[t] = id0;
   if (t + kThreads < n_idx) idx_tab[t + kThreads] = id1;
-  // The key mask of batch row b as an additive term: 0 for a valid key, -inf
-  // (probabilities) or -65504 (the SDPA mask output) for a masked one.
-  if (t < L) {
-    const float m = (float)mval;
-    const bool valid = mask_kind == GD_MASK_ATTENTION ? (m > 0.f) : !(m < -60000.f);
-    mask_add[t] = valid ? 0.f : (OUT == GD_ATTN_OUT_BIAS ? -65504.f : -INFINITY);
-  }
-  __syncthreads();  // the index table and the mask are complete
-  auto win = [&](int j) -> int { return __builtin_amdgcn_readlane(win_tab, j); };
 
-  // ---- V for the P.V pass: rows [row_lo, row_hi) of the (b, h) slice land
-  // row-major and swizzled like K at rows 0.. of an LDS buffer, by DMA.  Rows
-  // past the sequence repeat row L - 1; their probabilities are exactly 0.
-  // Rows [0, kVRowsA) go to the stage buffer the last chunk leaves free (while
-  // that chunk is computed), rows from kVRowsA on (L > 448) to the other one
-  // after the score loop. ----
-  const half_t* Vb = V + (int64_t)b * vsb + (int64_t)h * vsh;
-  const int v_rows = ((L + 31) >> 5) << 5;  // the P.V tile pairs reach this far
-  auto issue_v = [&](half_t* dst, int row_lo, int row_hi) {
-    for (int blk = wave; 8 * blk < row_hi - row_lo; blk += kWaves) {  // uniform
-      int key = row_lo + 8 * blk + blk_row;
-      key = key < L ? key : L - 1;
-      load_lds16(Vb + (int64_t)key * vsl + blk_chunk * 8, dst + blk * 512);
-    }
-  };
+  for (;;) {
+    const int next = item + (int)gridDim.x;
+    const bool has_next = kPersistent && next < nblk;  // uniform
+    Item nit = cur;  // decoded once the chunk loop is done
+    bool next_staged = false, next_setup = false;
+    Setup ns;  // the next item's set-up reads, once issued
 
-  // Swizzled offsets of this lane's two 16-byte chunks (g and 4 + g) in row
-  // 16m + lc of a staged table: the XOR term depends on the row only through
-  // lc, so a 16-aligned tile row base is a plain (uniform) offset.
-  const int swz_lo = swz(lc, g);
-  const int swz_hi = swz(lc, 4 + g);
-
-  float sc[MAXT][4];  // tiles at or past nt are set to -inf after the chunk loop
-
-#pragma unroll
-  for (int c = 0; c < MAXT / 4; ++c) {
-    if (c >= nchunks) break;  // uniform
-    wait_vmcnt<0>();
-    __syncthreads();  // stage c landed everywhere; every wave is done with stage c - 1
-    if (c + 1 < nchunks)
-      issue_stage(c + 1, (c + 1) & 1, win(48 + c + 1));
-    else if constexpr (OUT == GD_ATTN_OUT_CONTEXT)
-      issue_v((c + 1) & 1 ? stage1 : stage0, 0, v_rows < kVRowsA ? v_rows : kVRowsA);
-    const half_t* st = (c & 1) ? stage1 : stage0;
-    const half_t* Ks = st;
-    const half_t* PKs = st + kStageK;
-    const half_t* PQs = st + kStageK + kStageWin;
-    const int kc = c * kKC;
-    const int wlo = win(48 + c);
-    // The chunk's work for this wave, in compile-time variants whose bodies
-    // have no branches, so the scheduler can overlap the tiles freely.  LIN
-    // (every (query, key) pair of this wave lies in the linear zone): every
-    // window offset is closed-form and 16-aligned and the gathers are
-    // contiguous.  Otherwise the window starts come from the lane table, the
-    // fixed 80 c2p and 32 p2c positions are computed (rows clamped to the
-    // window; the extra ones are never gathered) and every score gathers
-    // through the index table.  FULL: all 64 keys of the chunk exist.
-    auto chunk = [&](auto lin_c, auto full_c) {
-      constexpr bool LIN = decltype(lin_c)::value;
-      constexpr bool FULL = decltype(full_c)::value;  // LIN implies FULL
-      // c2p for this wave's 16 queries and the chunk's keys: positions
-      // [cw_lo, cw_lo + 80) = window rows [crow0, crow0 + 80)
-      const int cw_lo = LIN ? qw - kc - (kKC - 1) + bucket_size : win(32 + c);
-      const int crow0 = cw_lo - wlo;
-      // Off the linear zone a lane's window row r = crow0 + 16 tw + lc may run
-      // past the window; such rows hold positions this wave never gathers and
-      // are clamped to a row with the same r mod 16, so the swizzle term of
-      // the lane is the same for every tile.
-      const int crow_l = crow0 + lc;
-      const int crow_lim = kWin - 16 + (crow_l & 15);
-      const int csw_lo = (g ^ ((crow_l >> 1) & 7)) << 3, csw_hi = ((4 + g) ^ ((crow_l >> 1) & 7)) << 3;
-#pragma unroll
-      for (int tw = 0; tw < kC2PCols / 16; ++tw) {
-        {
-          half8_t a0, a1;
-          if constexpr (LIN) {  // crow0 = 16 wave
-            a0 = *reinterpret_cast<const half8_t*>(PKs + (crow0 + 16 * tw) * kD + swz_lo);
-            a1 = *reinterpret_cast<const half8_t*>(PKs + (crow0 + 16 * tw) * kD + swz_hi);
-          } else {
-            const int row = crow_l + 16 * tw < crow_lim ? crow_l + 16 * tw : crow_lim;
-            a0 = *reinterpret_cast<const half8_t*>(PKs + row * kD + csw_lo);
-            a1 = *reinterpret_cast<const half8_t*>(PKs + row * kD + csw_hi);
-          }
-          float4_t r = {0.f, 0.f, 0.f, 0.f};
-          r = mfma16x16x32(a0, qf0, r);
-          r = mfma16x16x32(a1, qf1, r);
-          half4_t hv;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) hv[i] = (half_t)r[i];
-          *reinterpret_cast<half4_t*>(c2p_w + lc * kC2PStride + 16 * tw + 4 * g) = hv;
-        }
+    [&]() {
+      // Lane-derived values of the item body are computed afresh per item
+      // (an opaque copy of the lane index), not hoisted out of the item loop
+      // where they would hold registers through every chunk.
+      int lane_item = lane;
+      asm volatile("" : "+v"(lane_item));
+      const int lane = lane_item;
+      const int lc = lane & 15;
+      const int g = lane >> 4;
+      // Swizzled offsets of this lane's two 16-byte chunks (g and 4 + g) in
+      // row 16m + lc of a staged table: the XOR term depends on the row only
+      // through lc, so a 16-aligned tile row base is a plain (uniform) offset.
+      const int swz_lo = swz(lc, g);
+      const int swz_hi = swz(lc, 4 + g);
+      const int b = cur.b, h = cur.h;
+      const int q0 = cur.qt * kQT;
+      const int qw = q0 + 16 * wave;
+      const bool active = qw < L;
+      const half_t* Kb = K + (int64_t)b * ksb + (int64_t)h * ksh;
+      const half_t* PKh = PK + (int64_t)h * pksh;
+      const half_t* PQh = PQ + (int64_t)h * pqsh;
+      const half_t* Vb = V + (int64_t)b * vsb + (int64_t)h * vsh;
+      const half8_t qf0 = cs.qf0, qf1 = cs.qf1;
+      const int win_tab = cs.win_tab;
+      auto win = [&](int j) -> int { return __builtin_amdgcn_readlane(win_tab, j); };
+      // The key mask of batch row b as an additive term: 0 for a valid key,
+      // -inf (probabilities) or -65504 (the SDPA mask output) for a masked
+      // one; made visible by chunk 0's barrier.
+      if (t < L) {
+        const float m = (float)cs.mval;
+        const bool valid = mask_kind == GD_MASK_ATTENTION ? (m > 0.f) : !(m < -60000.f);
+        mask_add[t] = valid ? 0.f : (OUT == GD_ATTN_OUT_BIAS ? -65504.f : -INFINITY);
       }
 
-      // Per 16-key tile tt: S^T = K Q^T (scores) and P2C = K . posQ[window]^T
-      // over the <= 31 positions [pp_lo, pp_lo + 16 nj) the tile needs, stored
-      // skewed into p2c_w.  Tiles are software-pipelined: tile tt's gathers are
-      // issued before tile tt+1's MFMAs and p2c stores (the LDS executes a
-      // wave's accesses in order, so one p2c buffer suffices), and tile tt is
-      // combined while those are in flight.
-      int pp_lo[4];
-      float4_t s_t[4];
-      half8_t fk[2][2], fq[2][4];  // per tile parity: K rows (chunks g, 4+g), posQ rows (j = 0, 1)
-      // Operand fragments of tile tt (LDS reads only; issued a tile ahead).
-      auto prep_load = [&](int tt) {
-        const int k0 = kc + 16 * tt;
-        const int par = tt & 1;
-        pp_lo[tt] = LIN ? qw - k0 - 15 + bucket_size : win(4 * c + tt);
-        const int prow0 = pp_lo[tt] - wlo;
-        const int prow_l = prow0 + lc;  // clamped as the c2p rows
-        const int prow_lim = kWin - 16 + (prow_l & 15);
-        const int psw_lo = (g ^ ((prow_l >> 1) & 7)) << 3, psw_hi = ((4 + g) ^ ((prow_l >> 1) & 7)) << 3;
-        fk[par][0] = *reinterpret_cast<const half8_t*>(Ks + 16 * tt * kD + swz_lo);
-        fk[par][1] = *reinterpret_cast<const half8_t*>(Ks + 16 * tt * kD + swz_hi);
+      // ---- V for the P.V pass: rows [row_lo, row_hi) of the (b, h) slice
+      // land row-major and swizzled like K at rows 0.. of an LDS buffer, by
+      // DMA (placement: after the chunk loop).  Rows past the sequence repeat
+      // row L - 1; their probabilities are exactly 0. ----
+      const int v_rows = ((L + 31) >> 5) << 5;  // the P.V tile pairs reach this far
+      auto issue_v = [&](lds_half_t* dst, int row_lo, int row_hi) {
+        for (int blk = wave; 8 * blk < row_hi - row_lo; blk += kWaves) {  // uniform
+          int key = row_lo + 8 * blk + blk_row;
+          key = key < L ? key : L - 1;
+          load_lds16(Vb + (int64_t)key * vsl + blk_chunk * 8, dst + blk * 512);
+        }
+      };
+
+      float sc[MAXT][4];  // tiles at or past nt are set to -inf after the chunk loop
+
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          {
-            if constexpr (LIN) {  // prow0 = 16 (wave - tt) + 48
-              fq[par][2 * j] = *reinterpret_cast<const half8_t*>(PQs + (prow0 + 16 * j) * kD + swz_lo);
-              fq[par][2 * j + 1] = *reinterpret_cast<const half8_t*>(PQs + (prow0 + 16 * j) * kD + swz_hi);
-            } else {
-              const int row = prow_l + 16 * j < prow_lim ? prow_l + 16 * j : prow_lim;
-              fq[par][2 * j] = *reinterpret_cast<const half8_t*>(PQs + row * kD + psw_lo);
-              fq[par][2 * j + 1] = *reinterpret_cast<const half8_t*>(PQs + row * kD + psw_hi);
+      for (int c = 0; c < MAXT / 4; ++c) {
+        if (c >= nchunks) break;  // uniform
+        wait_vmcnt<0>();
+        __syncthreads();  // stage c landed everywhere; every wave is done with stage c - 1
+        half_t* const st = stages + (c & 1) * kStage;
+        lds_half_t* const so = stages3 + ((c + 1) & 1) * kStage;  // free: every wave is done with stage c - 1
+        if (c + 1 < nchunks) {
+          issue_stage(so, Kb, PKh, PQh, (c + 1) * kKC, win(48 + c + 1));
+        } else if constexpr (OUT == GD_ATTN_OUT_CONTEXT) {  // V rows into the free buffer
+          if (!(c & 1) || !has_next) issue_v(so, 0, v_rows < kVRowsA ? v_rows : kVRowsA);
+        }
+        const half_t* Ks = st;
+        const half_t* PKs = st + kStageK;
+        const half_t* PQs = st + kStageK + kStageWin;
+        const int kc = c * kKC;
+        const int wlo = win(48 + c);
+        // The chunk's work for this wave, in compile-time variants whose bodies
+        // have no branches, so the scheduler can overlap the tiles freely.  LIN
+        // (every (query, key) pair of this wave lies in the linear zone): every
+        // window offset is closed-form and 16-aligned and the gathers are
+        // contiguous.  Otherwise the window starts come from the lane table, the
+        // fixed 80 c2p and 32 p2c positions are computed (rows clamped to the
+        // window; the extra ones are never gathered) and every score gathers
+        // through the index table.  FULL: all 64 keys of the chunk exist.
+        auto chunk = [&](auto lin_c, auto full_c) {
+          constexpr bool LIN = decltype(lin_c)::value;
+          constexpr bool FULL = decltype(full_c)::value;  // LIN implies FULL
+          // c2p for this wave's 16 queries and the chunk's keys: positions
+          // [cw_lo, cw_lo + 80) = window rows [crow0, crow0 + 80)
+          const int cw_lo = LIN ? qw - kc - (kKC - 1) + bucket_size : win(32 + c);
+          const int crow0 = cw_lo - wlo;
+          // Off the linear zone a lane's window row r = crow0 + 16 tw + lc may run
+          // past the window; such rows hold positions this wave never gathers and
+          // are clamped to a row with the same r mod 16, so the swizzle term of
+          // the lane is the same for every tile.
+          const int crow_l = crow0 + lc;
+          const int crow_lim = kWin - 16 + (crow_l & 15);
+          const int csw_lo = (g ^ ((crow_l >> 1) & 7)) << 3, csw_hi = ((4 + g) ^ ((crow_l >> 1) & 7)) << 3;
+#pragma unroll
+          for (int tw = 0; tw < kC2PCols / 16; ++tw) {
+            {
+              half8_t a0, a1;
+              if constexpr (LIN) {  // crow0 = 16 wave
+                a0 = *reinterpret_cast<const half8_t*>(PKs + (crow0 + 16 * tw) * kD + swz_lo);
+                a1 = *reinterpret_cast<const half8_t*>(PKs + (crow0 + 16 * tw) * kD + swz_hi);
+              } else {
+                const int row = crow_l + 16 * tw < crow_lim ? crow_l + 16 * tw : crow_lim;
+                a0 = *reinterpret_cast<const half8_t*>(PKs + row * kD + csw_lo);
+                a1 = *reinterpret_cast<const half8_t*>(PKs + row * kD + csw_hi);
+              }
+              float4_t r = {0.f, 0.f, 0.f, 0.f};
+              r = mfma16x16x32(a0, qf0, r);
+              r = mfma16x16x32(a1, qf1, r);
+              half4_t hv;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) hv[i] = (half_t)r[i];
+              *reinterpret_cast<half4_t*>(c2p_w + lc * kC2PStride + 16 * tw + 4 * g) = hv;
             }
           }
-        }
-      };
-      // Scores and p2c of tile tt from its fragments; p2c stored skewed.
-      auto prep_compute = [&](int tt) {
-        const int par = tt & 1;
-        float4_t sv = {0.f, 0.f, 0.f, 0.f};
-        sv = mfma16x16x32(fk[par][0], qf0, sv);
-        s_t[tt] = mfma16x16x32(fk[par][1], qf1, sv);
+
+          // Per 16-key tile tt: S^T = K Q^T (scores) and P2C = K . posQ[window]^T
+          // over the <= 31 positions [pp_lo, pp_lo + 16 nj) the tile needs, stored
+          // skewed into p2c_w.  Tiles are software-pipelined: tile tt's gathers are
+          // issued before tile tt+1's MFMAs and p2c stores (the LDS executes a
+          // wave's accesses in order, so one p2c buffer suffices), and tile tt is
+          // combined while those are in flight.
+          int pp_lo[4];
+          float4_t s_t[4];
+          half8_t fk[2][2], fq[2][4];  // per tile parity: K rows (chunks g, 4+g), posQ rows (j = 0, 1)
+          // Operand fragments of tile tt (LDS reads only; issued a tile ahead).
+          auto prep_load = [&](int tt) {
+            const int k0 = kc + 16 * tt;
+            const int par = tt & 1;
+            pp_lo[tt] = LIN ? qw - k0 - 15 + bucket_size : win(4 * c + tt);
+            const int prow0 = pp_lo[tt] - wlo;
+            const int prow_l = prow0 + lc;  // clamped as the c2p rows
+            const int prow_lim = kWin - 16 + (prow_l & 15);
+            const int psw_lo = (g ^ ((prow_l >> 1) & 7)) << 3, psw_hi = ((4 + g) ^ ((prow_l >> 1) & 7)) << 3;
+            fk[par][0] = *reinterpret_cast<const half8_t*>(Ks + 16 * tt * kD + swz_lo);
+            fk[par][1] = *reinterpret_cast<const half8_t*>(Ks + 16 * tt * kD + swz_hi);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          {
-            float4_t r = {0.f, 0.f, 0.f, 0.f};
-            r = mfma16x16x32(fk[par][0], fq[par][2 * j], r);
-            r = mfma16x16x32(fk[par][1], fq[par][2 * j + 1], r);
-            // lane holds (kr = 4g + i, p = 16 j + lc); converted in pairs
-            const half4_t rh = __builtin_convertvector(r, half4_t);
+            for (int j = 0; j < 2; ++j) {
+              {
+                if constexpr (LIN) {  // prow0 = 16 (wave - tt) + 48
+                  fq[par][2 * j] = *reinterpret_cast<const half8_t*>(PQs + (prow0 + 16 * j) * kD + swz_lo);
+                  fq[par][2 * j + 1] = *reinterpret_cast<const half8_t*>(PQs + (prow0 + 16 * j) * kD + swz_hi);
+                } else {
+                  const int row = prow_l + 16 * j < prow_lim ? prow_l + 16 * j : prow_lim;
+                  fq[par][2 * j] = *reinterpret_cast<const half8_t*>(PQs + row * kD + psw_lo);
+                  fq[par][2 * j + 1] = *reinterpret_cast<const half8_t*>(PQs + row * kD + psw_hi);
+                }
+              }
+            }
+          };
+          // Scores and p2c of tile tt from its fragments; p2c stored skewed.
+          auto prep_compute = [&](int tt) {
+            const int par = tt & 1;
+            float4_t sv = {0.f, 0.f, 0.f, 0.f};
+            sv = mfma16x16x32(fk[par][0], qf0, sv);
+            s_t[tt] = mfma16x16x32(fk[par][1], qf1, sv);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) p2c_w[(4 * g + i + 16 * j + lc) * kP2CSkew + 4 * g + i] = rh[i];
+            for (int j = 0; j < 2; ++j) {
+              {
+                float4_t r = {0.f, 0.f, 0.f, 0.f};
+                r = mfma16x16x32(fk[par][0], fq[par][2 * j], r);
+                r = mfma16x16x32(fk[par][1], fq[par][2 * j + 1], r);
+                // lane holds (kr = 4g + i, p = 16 j + lc); converted in pairs
+                const half4_t rh = __builtin_convertvector(r, half4_t);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) p2c_w[(4 * g + i + 16 * j + lc) * kP2CSkew + 4 * g + i] = rh[i];
+              }
+            }
+          };
+          prep_load(0);
+          prep_compute(0);
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt) {
+            const int T = 4 * c + tt;
+            if constexpr (!FULL) {
+              if (T >= nt) break;  // uniform
+            }
+            const int k0 = 16 * T;
+            const bool next = tt + 1 < 4 && (FULL || T + 1 < nt);
+            if (next) prep_load(tt + 1);  // fragment reads overlap this tile's gathers
+            wave_lds_sync();  // tile tt's p2c stores (and the chunk's c2p) precede its gathers
+            // Gather the two terms of score (q = qw + lc, k = k0 + 4g + i) at
+            // idx(q - k).  In the linear zone idx = q - k + 256: the four c2p
+            // terms are consecutive (descending) in the lane's c2p row and the
+            // four p2c terms are one 8-byte read.
+            const float4_t madd = *reinterpret_cast<const float4_t*>(mask_add + k0 + 4 * g);
+            half4_t c2p, p2c;
+            if constexpr (LIN) {
+              const half_t* cp = c2p_w + lc * kC2PStride + (qw - k0 + bucket_size - cw_lo) + lc - 4 * g;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) c2p[i] = cp[-i];
+              p2c = *reinterpret_cast<const half4_t*>(p2c_w + (15 + lc) * kP2CSkew + 4 * g);
+            } else {
+              const int r0 = qw + lc - k0 - 4 * g + L - 1;
+              const half_t* cb = c2p_w + lc * kC2PStride - cw_lo;
+              const half_t* pb = p2c_w + (4 * g - pp_lo[tt]) * kP2CSkew + 4 * g;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const int id = idx_tab[r0 - i];  // 0 <= id < 512
+                c2p[i] = cb[id];
+                p2c[i] = pb[__mul24(id, kP2CSkew) + i * (kP2CSkew + 1)];
+              }
+            }
+            wave_lds_sync();  // these gathers precede the next tile's p2c stores
+            if (next) prep_compute(tt + 1);
+            // fp16(c2p + p2c) is the fp16 add (two packed adds); the division by
+            // fp16(sqrt(3D)) is a multiply by its fp32 reciprocal, which rounds to
+            // the same fp16 value for every finite fp16 numerator (checked
+            // exhaustively).
+            const half4_t sum16 = c2p + p2c;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float bias16 = round_f16((float)sum16[i] * inv_scale16);
+              if (OUT == GD_ATTN_OUT_BIAS)
+                sc[T][i] = round_f16(bias16 + madd[i]);
+              else
+                sc[T][i] = fmaf(s_t[tt][i], scale_qk, bias16) + madd[i];
+            }
           }
+          wave_lds_sync();  // the last gathers precede the next chunk's c2p / p2c stores
+        };
+        if (active) {
+          const bool lin = (kc + kKC <= L) && (qw - kc - (kKC - 1) >= -kMid) && (qw + 15 - kc <= kMid);
+          if (lin)
+            chunk(std::true_type{}, std::true_type{});
+          else if (kc + kKC <= L)
+            chunk(std::false_type{}, std::true_type{});
+          else
+            chunk(std::false_type{}, std::false_type{});
         }
-      };
-      prep_load(0);
-      prep_compute(0);
+      }
+      if (nt < MAXT) {  // key tiles past the sequence take no part in the softmax
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        const int T = 4 * c + tt;
-        if constexpr (!FULL) {
-          if (T >= nt) break;  // uniform
+        for (int T = 0; T < MAXT; ++T)
+          if (T >= nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sc[T][i] = -INFINITY;
+      }
+      // The stage buffers are free from here on, except for V rows in flight
+      // (context; waited for before the P.V pass) and the next item's stage.
+      stage_barrier();
+      // Chunk c used buffer c & 1; the next item's first stage goes to buffer
+      // 0 now.  V rows [0, kVRowsA) are in buffer 1, loaded during the last
+      // chunk when that chunk was in buffer 0 and now otherwise, except
+      // without a next item when the last chunk was in buffer 1 (then in
+      // buffer 0, loaded during that chunk); rows from kVRowsA on (no next
+      // item) go to the other buffer now.
+      const bool last_in_1 = ((nchunks - 1) & 1) != 0;
+      const bool v_in_0 = last_in_1 && !has_next;
+      lds_half_t* const v_lo = stages3 + (v_in_0 ? 0 : kStage);  // V rows [0, kVRowsA)
+      lds_half_t* const v_hi = stages3 + (v_in_0 ? kStage : 0);  // V rows [kVRowsA, v_rows)
+      if constexpr (OUT == GD_ATTN_OUT_CONTEXT) {
+        if (last_in_1 && has_next) issue_v(v_lo, 0, v_rows < kVRowsA ? v_rows : kVRowsA);
+        if (MAXT * 16 > kVRowsA && v_rows > kVRowsA) issue_v(v_hi, kVRowsA, v_rows);  // no next item here
+      }
+      if (has_next) {  // after every V row
+        nit = decode(next);
+        stage0_of(nit, stages3);
+        next_staged = true;
+        if constexpr (OUT != GD_ATTN_OUT_CONTEXT) {
+          ns = setup_of(nit);
+          next_setup = true;
         }
-        const int k0 = 16 * T;
-        const bool next = tt + 1 < 4 && (FULL || T + 1 < nt);
-        if (next) prep_load(tt + 1);  // fragment reads overlap this tile's gathers
-        wave_lds_sync();  // tile tt's p2c stores (and the chunk's c2p) precede its gathers
-        // Gather the two terms of score (q = qw + lc, k = k0 + 4g + i) at
-        // idx(q - k).  In the linear zone idx = q - k + 256: the four c2p
-        // terms are consecutive (descending) in the lane's c2p row and the
-        // four p2c terms are one 8-byte read.
-        const float4_t madd = *reinterpret_cast<const float4_t*>(mask_add + k0 + 4 * g);
-        half4_t c2p, p2c;
-        if constexpr (LIN) {
-          const half_t* cp = c2p_w + lc * kC2PStride + (qw - k0 + bucket_size - cw_lo) + lc - 4 * g;
+      }
+
+      float inv_sum = 0.f;
+      if (OUT != GD_ATTN_OUT_BIAS) {
+        float mx = -INFINITY;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) c2p[i] = cp[-i];
-          p2c = *reinterpret_cast<const half4_t*>(p2c_w + (15 + lc) * kP2CSkew + 4 * g);
-        } else {
-          const int r0 = qw + lc - k0 - 4 * g + L - 1;
-          const half_t* cb = c2p_w + lc * kC2PStride - cw_lo;
-          const half_t* pb = p2c_w + (4 * g - pp_lo[tt]) * kP2CSkew + 4 * g;
+        for (int T = 0; T < MAXT; ++T)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[T][i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mref = mx == -INFINITY ? 0.f : mx;
+        constexpr float kLog2e = 1.4426950408889634f;
+        // exp(s - m) = 2^(s log2e - m log2e) as one fma per score; the rounding
+        // of m log2e scales the whole row alike and cancels in the normalisation.
+        const float mref_l2 = mref * kLog2e;
+        float sum = 0.f;
+#pragma unroll
+        for (int T = 0; T < MAXT; ++T)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int id = idx_tab[r0 - i];  // 0 <= id < 512
-            c2p[i] = cb[id];
-            p2c[i] = pb[__mul24(id, kP2CSkew) + i * (kP2CSkew + 1)];
+            const float e = __builtin_amdgcn_exp2f(fmaf(sc[T][i], kLog2e, -mref_l2));  // v_exp_f32; exp2(-inf) = 0
+            sc[T][i] = e;
+            sum += e;
+          }
+        sum += __shfl_xor(sum, 16, 64);
+        sum += __shfl_xor(sum, 32, 64);
+        inv_sum = sum > 0.f ? 1.0f / sum : 0.f;
+        // The context path scales O once at the end instead of every probability.
+        if (OUT == GD_ATTN_OUT_PROBS) {
+#pragma unroll
+          for (int T = 0; T < MAXT; ++T)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sc[T][i] *= inv_sum;
+        }
+      }
+      if (OUT == GD_ATTN_OUT_PROBS || OUT == GD_ATTN_OUT_BIAS) {
+        // Stage this wave's 16 rows x L in LDS (rows padded by 16 bytes so the
+        // 8-byte column stores of a wave hit distinct banks), then write
+        // 16-byte row segments.  At L <= 256 (where buffer 0 may hold the
+        // next item's stage) waves 0-3 stage in buffer 1, 4-7 in the scratch
+        // buffer; else waves 0-5 in the stage buffers, 6-7 in the scratch
+        // buffer.
+        const int rs = L + 8;
+        constexpr int kRowsWave = 16 * (16 * MAXT + 8);
+        static_assert(MAXT > 16 || (4 * kRowsWave <= kStage && 4 * kRowsWave <= kWaves * kScratchWave),
+                      "probability staging");
+        static_assert(3 * kRowsWave <= kStage && 2 * kRowsWave <= kWaves * kScratchWave, "probability staging");
+        half_t* rows;
+        if constexpr (MAXT <= 16)
+          rows = (wave < 4 ? stages + kStage : scratch_lds) + (wave & 3) * kRowsWave;
+        else
+          rows = wave < 6 ? stages + (wave / 3) * kStage + (wave % 3) * kRowsWave
+                          : scratch_lds + (wave - 6) * kRowsWave;
+        if (active) {
+#pragma unroll
+          for (int T = 0; T < MAXT; ++T)
+            if (T < nt) {
+              half4_t v;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) v[i] = (half_t)sc[T][i];
+              *reinterpret_cast<half4_t*>(rows + lc * rs + 16 * T + 4 * g) = v;
+            }
+          wave_lds_sync();
+          const int per_row = L / 8;  // 16-byte pieces per row
+          for (int pce = lane; pce < 16 * per_row; pce += 64) {
+            const int r = pce / per_row, cpos = pce - r * per_row;
+            *reinterpret_cast<half8_t*>(out + (((int64_t)b * H + h) * L + qw + r) * L + cpos * 8) =
+                *reinterpret_cast<const half8_t*>(rows + r * rs + cpos * 8);
           }
         }
-        wave_lds_sync();  // these gathers precede the next tile's p2c stores
-        if (next) prep_compute(tt + 1);
-        // fp16(c2p + p2c) is the fp16 add (two packed adds); the division by
-        // fp16(sqrt(3D)) is a multiply by its fp32 reciprocal, which rounds to
-        // the same fp16 value for every finite fp16 numerator (checked
-        // exhaustively).
-        const half4_t sum16 = c2p + p2c;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float bias16 = round_f16((float)sum16[i] * inv_scale16);
-          if (OUT == GD_ATTN_OUT_BIAS)
-            sc[T][i] = round_f16(bias16 + madd[i]);
-          else
-            sc[T][i] = fmaf(s_t[tt][i], scale_qk, bias16) + madd[i];
+        return;
+      }
+
+      // ---- context: O = P V with V row-major in LDS, P (hi + lo) as the A operand ----
+      // The B operand (keys x d) is read with ds_read_b64_tr_b16: in each
+      // 16-lane group, source lane s names 4 consecutive halfs and output lane
+      // j receives element j % 4 of source lanes j / 4, 4 + j / 4, 8 + j / 4,
+      // 12 + j / 4.  Source lane lc of group g names V[r0 + lc / 4][16 dt +
+      // 4 (lc % 4) ..] with r0 = 16 T + 4 g, so lane (g, lc) receives
+      // V[16 T + 4 g + i][16 dt + lc], i = 0..3: the B fragment of the keys
+      // that pa holds for tile T (and, from r0 + 16, for tile T + 1).  The
+      // swizzle term (row >> 1) & 7 of those rows is (2 g + lc / 8) & 7 for
+      // every 16-aligned tile base.  The next item's stage, issued after the
+      // V rows (kStageOps DMA instructions), may stay in flight.
+      if (next_staged)
+        wait_vmcnt<kStageOps>();
+      else
+        wait_vmcnt<0>();
+      stage_barrier();  // every wave's V rows have landed
+      if constexpr (MAXT <= 16) {
+        if (has_next) {
+          ns = setup_of(nit);
+          next_setup = true;
         }
       }
-      wave_lds_sync();  // the last gathers precede the next chunk's c2p / p2c stores
-    };
-    if (active) {
-      const bool lin = (kc + kKC <= L) && (qw - kc - (kKC - 1) >= -kMid) && (qw + 15 - kc <= kMid);
-      if (lin)
-        chunk(std::true_type{}, std::true_type{});
-      else if (kc + kKC <= L)
-        chunk(std::false_type{}, std::true_type{});
-      else
-        chunk(std::false_type{}, std::false_type{});
-    }
-  }
-  if (nt < MAXT) {  // key tiles past the sequence take no part in the softmax
+      if (!active) return;
+      float4_t o[4];
 #pragma unroll
-    for (int T = 0; T < MAXT; ++T)
-      if (T >= nt)
+      for (int dt = 0; dt < 4; ++dt) o[dt] = (float4_t){0.f, 0.f, 0.f, 0.f};
+      typedef __attribute__((address_space(3))) short4_t lds_short4_t;
+      const int tr_sw = (2 * g + (lc >> 3)) & 7;
+      const int tr_lane = (4 * g + (lc >> 2)) * kD + 4 * (lc & 1);  // row and half offset of this source lane
+      const int tr_c = (lc >> 1) & 1;                                // 16-byte chunk within the 32-byte d slice
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sc[T][i] = -INFINITY;
-  }
-  // The stage buffers are free from here on, except for the V rows in flight
-  // (context only; waited for before the P.V pass).
-  stage_barrier();
-  half_t* const v_lo = (nchunks & 1) ? stage1 : stage0;        // V rows [0, kVRowsA)
-  half_t* const v_hi = (nchunks & 1) ? stage0 : stage1;        // V rows [kVRowsA, v_rows)
-  if constexpr (OUT == GD_ATTN_OUT_CONTEXT && MAXT * 16 > kVRowsA) {
-    if (v_rows > kVRowsA) issue_v(v_hi, kVRowsA, v_rows);
-  }
-
-  float inv_sum = 0.f;
-  if (OUT != GD_ATTN_OUT_BIAS) {
-    float mx = -INFINITY;
+      for (int c = 0; c < MAXT / 4; ++c) {
+        if (c >= nchunks) break;
 #pragma unroll
-    for (int T = 0; T < MAXT; ++T)
+        for (int pr = 0; pr < 2; ++pr) {
+          const int T = 4 * c + 2 * pr;
+          if (T >= nt) break;  // uniform; nt is at most one past the last pair's first tile
+          const int row0 = 16 * T;
+          const lds_half_t* vsrc = row0 < kVRowsA ? v_lo + row0 * kD : v_hi + (row0 - kVRowsA) * kD;
+          // Unnormalised P of key tiles T, T + 1 as the A operand, split into
+          // fp16 hi (truncated) + lo (the exact fp32 remainder, rounded).  Tiles
+          // at or past nt hold exp(-inf) = 0.
+          half8_t pa, pl;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[T][i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mref = mx == -INFINITY ? 0.f : mx;
-    constexpr float kLog2e = 1.4426950408889634f;
-    // exp(s - m) = 2^(s log2e - m log2e) as one fma per score; the rounding
-    // of m log2e scales the whole row alike and cancels in the normalisation.
-    const float mref_l2 = mref * kLog2e;
-    float sum = 0.f;
+          for (int i = 0; i < 4; i += 2) {
 #pragma unroll
-    for (int T = 0; T < MAXT; ++T)
+            for (int u = 0; u < 2; ++u) {
+              const float x0 = sc[T + u][i], x1 = sc[T + u][i + 1];
+              const half2_t hi = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(x0, x1));
+              pa[4 * u + i] = hi[0];
+              pa[4 * u + i + 1] = hi[1];
+              pl[4 * u + i] = (half_t)(x0 - (float)hi[0]);
+              pl[4 * u + i + 1] = (half_t)(x1 - (float)hi[1]);
+            }
+          }
+          half8_t vb[4];
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) {
+            const lds_half_t* a = vsrc + tr_lane + (((2 * dt + tr_c) ^ tr_sw) << 3);
+            const short4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)a);
+            const short4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(a + 16 * kD));
+            const half4_t h0 = __builtin_bit_cast(half4_t, v0), h1 = __builtin_bit_cast(half4_t, v1);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              vb[dt][i] = h0[i];
+              vb[dt][4 + i] = h1[i];
+            }
+          }
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) o[dt] = mfma16x16x32(pa, vb[dt], o[dt]);
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) o[dt] = mfma16x16x32(pl, vb[dt], o[dt]);
+        }
+      }
+      // lane holds O[qw + 4g + i][16 dt + lc]: stage 16 x 64 in LDS, write 128-byte rows
+      // (the softmax sum of query row r sits in lanes with lc = r)
+      half_t* ot = scratch_lds + wave * kScratchWave;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float e = __builtin_amdgcn_exp2f(fmaf(sc[T][i], kLog2e, -mref_l2));  // v_exp_f32; exp2(-inf) = 0
-        sc[T][i] = e;
-        sum += e;
+        const float inv_row = __shfl(inv_sum, 4 * g + i, 64);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) ot[(4 * g + i) * 72 + 16 * dt + lc] = (half_t)(o[dt][i] * inv_row);
       }
-    sum += __shfl_xor(sum, 16, 64);
-    sum += __shfl_xor(sum, 32, 64);
-    inv_sum = sum > 0.f ? 1.0f / sum : 0.f;
-    // The context path scales O once at the end instead of every probability.
-    if (OUT == GD_ATTN_OUT_PROBS) {
-#pragma unroll
-      for (int T = 0; T < MAXT; ++T)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sc[T][i] *= inv_sum;
-    }
-  }
-
-  if (OUT == GD_ATTN_OUT_PROBS || OUT == GD_ATTN_OUT_BIAS) {
-    // Stage this wave's 16 rows x L in LDS (rows padded by 16 bytes so the
-    // 8-byte column stores of a wave hit distinct banks), then write 16-byte
-    // row segments.
-    const int rs = L + 8;
-    // waves 0-2 stage in stage0, 3-5 in stage1, 6-7 in the scratch buffer
-    constexpr int kRowsWave = 16 * (16 * MAXT + 8);
-    static_assert(3 * kRowsWave <= kStage && 2 * kRowsWave <= kWaves * kScratchWave, "probability staging");
-    half_t* rows = (wave < 3 ? stage0 : (wave < 6 ? stage1 : scratch_lds)) + (wave % 3) * kRowsWave;
-    if (active) {
-#pragma unroll
-      for (int T = 0; T < MAXT; ++T)
-        if (T < nt) {
-          half4_t v;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) v[i] = (half_t)sc[T][i];
-          *reinterpret_cast<half4_t*>(rows + lc * rs + 16 * T + 4 * g) = v;
-        }
       wave_lds_sync();
-      const int per_row = L / 8;  // 16-byte pieces per row
-      for (int pce = lane; pce < 16 * per_row; pce += 64) {
-        const int r = pce / per_row, cpos = pce - r * per_row;
-        *reinterpret_cast<half8_t*>(out + (((int64_t)b * H + h) * L + qw + r) * L + cpos * 8) =
-            *reinterpret_cast<const half8_t*>(rows + r * rs + cpos * 8);
+      {
+        const int r = lane >> 3, cpos = lane & 7;  // 8 rows x 8 pieces per pass
+#pragma unroll
+        for (int pass = 0; pass < 2; ++pass) {
+          const int row = r + 8 * pass;
+          *reinterpret_cast<half8_t*>(out + ((int64_t)b * L + qw + row) * ldo + (int64_t)h * kD + cpos * 8) =
+              *reinterpret_cast<const half8_t*>(ot + row * 72 + cpos * 8);
+        }
       }
-    }
-    return;
-  }
+    }();
 
-  // ---- context: O = P V with V row-major in LDS, P (hi + lo) as the A operand ----
-  // The B operand (keys x d) is read with ds_read_b64_tr_b16: in each 16-lane
-  // group, source lane s names 4 consecutive halfs and output lane j receives
-  // element j % 4 of source lanes j / 4, 4 + j / 4, 8 + j / 4, 12 + j / 4.
-  // Source lane lc of group g names V[r0 + lc / 4][16 dt + 4 (lc % 4) ..] with
-  // r0 = 16 T + 4 g, so lane (g, lc) receives V[16 T + 4 g + i][16 dt + lc],
-  // i = 0..3: the B fragment of the keys that pa holds for tile T (and, from
-  // r0 + 16, for tile T + 1).  The swizzle term (row >> 1) & 7 of those rows
-  // is (2 g + lc / 8) & 7 for every 16-aligned tile base.
-  wait_vmcnt<0>();
-  stage_barrier();  // every wave's V rows have landed
-  if (!active) return;
-  float4_t o[4];
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt) o[dt] = (float4_t){0.f, 0.f, 0.f, 0.f};
-  typedef __attribute__((address_space(3))) short4_t lds_short4_t;
-  const int tr_sw = (2 * g + (lc >> 3)) & 7;
-  const int tr_lane = (4 * g + (lc >> 2)) * kD + 4 * (lc & 1);  // row and half offset of this source lane
-  const int tr_c = (lc >> 1) & 1;                                // 16-byte chunk within the 32-byte d slice
-#pragma unroll
-  for (int c = 0; c < MAXT / 4; ++c) {
-    if (c >= nchunks) break;
-#pragma unroll
-    for (int pr = 0; pr < 2; ++pr) {
-      const int T = 4 * c + 2 * pr;
-      if (T >= nt) break;  // uniform; nt is at most one past the last pair's first tile
-      const int row0 = 16 * T;
-      const half_t* vsrc = row0 < kVRowsA ? v_lo + row0 * kD : v_hi + (row0 - kVRowsA) * kD;
-      // Unnormalised P of key tiles T, T + 1 as the A operand, split into
-      // fp16 hi (truncated) + lo (the exact fp32 remainder, rounded).  Tiles
-      // at or past nt hold exp(-inf) = 0.
-      half8_t pa, pl;
-#pragma unroll
-      for (int i = 0; i < 4; i += 2) {
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const float x0 = sc[T + u][i], x1 = sc[T + u][i + 1];
-          const half2_t hi = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(x0, x1));
-          pa[4 * u + i] = hi[0];
-          pa[4 * u + i + 1] = hi[1];
-          pl[4 * u + i] = (half_t)(x0 - (float)hi[0]);
-          pl[4 * u + i + 1] = (half_t)(x1 - (float)hi[1]);
-        }
-      }
-      half8_t vb[4];
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        const half_t* a = vsrc + tr_lane + (((2 * dt + tr_c) ^ tr_sw) << 3);
-        const short4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(lds_void_t*)a);
-        const short4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(lds_void_t*)(a + 16 * kD));
-        const half4_t h0 = __builtin_bit_cast(half4_t, v0), h1 = __builtin_bit_cast(half4_t, v1);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          vb[dt][i] = h0[i];
-          vb[dt][4 + i] = h1[i];
-        }
-      }
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) o[dt] = mfma16x16x32(pa, vb[dt], o[dt]);
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) o[dt] = mfma16x16x32(pl, vb[dt], o[dt]);
-    }
+    if (!has_next) break;
+    if (!next_setup) ns = setup_of(nit);
+    cur = nit;
+    cs = ns;
+    item = next;
   }
-  // lane holds O[qw + 4g + i][16 dt + lc]: stage 16 x 64 in LDS, write 128-byte rows
-  // (the softmax sum of query row r sits in lanes with lc = r)
-  half_t* ot = scratch_lds + wave * kScratchWave;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float inv_row = __shfl(inv_sum, 4 * g + i, 64);
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) ot[(4 * g + i) * 72 + 16 * dt + lc] = (half_t)(o[dt][i] * inv_row);
+}
+
+// Compute units of the current device (cached per device).
+int device_cu_count() {
+  static std::atomic<int> cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev].store(n, std::memory_order_relaxed);
   }
-  wave_lds_sync();
-  {
-    const int r = lane >> 3, cpos = lane & 7;  // 8 rows x 8 pieces per pass
-#pragma unroll
-    for (int pass = 0; pass < 2; ++pass) {
-      const int row = r + 8 * pass;
-      *reinterpret_cast<half8_t*>(out + ((int64_t)b * L + qw + row) * ldo + (int64_t)h * kD + cpos * 8) =
-          *reinterpret_cast<const half8_t*>(ot + row * 72 + cpos * 8);
-    }
-  }
+  return n;
 }
 
 template <int MAXT>
 int launch2(const AttentionArgs& a, hipStream_t stream) {
   const int ntq = (int)((a.L + kQT - 1) / kQT);
-  const dim3 grid((unsigned)(a.B * a.H * ntq)), block(kThreads);
+  const int64_t items = a.B * a.H * ntq;
+  const int64_t cus = attention_persistent<MAXT>() ? device_cu_count() : items;
+  const dim3 grid((unsigned)(items < cus ? items : cus)), block(kThreads);
   auto hq = static_cast<const half_t*>(a.q);
   auto hk = static_cast<const half_t*>(a.k);
   auto hv = static_cast<const half_t*>(a.v);
@@ -612,11 +737,12 @@ int launch2(const AttentionArgs& a, hipStream_t stream) {
   auto hpq = static_cast<const half_t*>(a.pq);
   auto hm = static_cast<const half_t*>(a.mask);
   auto ho = static_cast<half_t*>(a.out);
-#define GD_ATTN2(OUTK)                                                                                             \
-  hipLaunchKernelGGL((deberta_attention_kernel<MAXT, OUTK>), grid, block, 0, stream, hq, hk, hv, a.qsb, a.qsh,      \
-                     a.qsl, a.ksb, a.ksh, a.ksl, a.vsb, a.vsh, a.vsl, hpk, hpq, a.pksh, a.pksp, a.pqsh, a.pqsp, hm,  \
-                     a.mask_kind, (int)a.B, (int)a.H, (int)a.L, (int)a.P, a.bucket_size, a.scale_qk, a.scale16, ho, \
-                     a.ldo)
+  // element strides in 32 bits (checked by launch_deberta_attention)
+#define GD_ATTN2(OUTK)                                                                                            \
+  hipLaunchKernelGGL((deberta_attention_kernel<MAXT, OUTK>), grid, block, 0, stream, hq, hk, hv, (int)a.qsb,     \
+                     (int)a.qsh, (int)a.qsl, (int)a.ksb, (int)a.ksh, (int)a.ksl, (int)a.vsb, (int)a.vsh, (int)a.vsl, \
+                     hpk, hpq, (int)a.pksh, (int)a.pksp, (int)a.pqsh, (int)a.pqsp, hm, a.mask_kind, (int)a.B,       \
+                     (int)a.H, (int)a.L, (int)a.P, a.bucket_size, a.scale_qk, a.scale16, ho, (int)a.ldo)
   switch (a.output) {
     case GD_ATTN_OUT_PROBS:
       GD_ATTN2(GD_ATTN_OUT_PROBS);
@@ -661,6 +787,8 @@ int ensure_relative_index_table(hipStream_t stream) {
 
 int launch_deberta_attention(const AttentionArgs& a, hipStream_t stream) {
   if (a.bucket_size != 256 || a.P != 512) return fail(GD_ERR_SHAPE, "attention: bucket size 256 and 512 positions");
+  for (int64_t st : {a.qsb, a.qsh, a.qsl, a.ksb, a.ksh, a.ksl, a.vsb, a.vsh, a.vsl, a.pksh, a.pksp, a.pqsh, a.pqsp, a.ldo})
+    if (st < 0 || st > INT32_MAX) return fail(GD_ERR_SHAPE, "attention: strides must lie in [0, 2^31)");
   GD_RETURN_IF_ERROR(ensure_relative_index_table(stream));
   if (a.L <= 64) return launch2<4>(a, stream);
   if (a.L <= 128) return launch2<8>(a, stream);
