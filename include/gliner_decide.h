@@ -195,8 +195,12 @@ typedef struct gd_table {
  *               (key-only mask; padded query rows attend to valid keys)
  *   context   = P . V                              (SDPA, :386-394)
  * head_dim must be 64, seq_len a multiple of 16 in [16, 512], positions 512,
- * bucket_size 256.  Replaces the default relative-bias + SDPA chain and the
- * generic path (:397-409). */
+ * bucket_size 256; element strides below 2^31.  The first call on a device
+ * fills that device's relative index table (a small kernel and a stream
+ * synchronisation); made on a stream that is capturing a graph it returns
+ * GD_ERR_UNSUPPORTED instead, so a caller that captures makes one attention
+ * call (or creates a classifier) on the device beforehand.  Replaces the
+ * default relative-bias + SDPA chain and the generic path (:397-409). */
 int gd_deberta_attention(gd_bhld q, gd_bhld k, gd_bhld v, gd_table pos_key, gd_table pos_query,
                          const void* mask, int32_t mask_kind, int64_t batch, int64_t heads,
                          int64_t seq_len, int64_t head_dim, int64_t positions,
