@@ -197,10 +197,6 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     }
   };
   constexpr int kStageOps = 1 + 2 * (kWin / 8 / kWaves);
-  auto rel = [&](int r) -> int {  // idx(r) from the device table
-    r = r < -(L - 1) ? -(L - 1) : (r > L - 1 ? L - 1 : r);
-    return g_rel_idx[r + kRelSpan];
-  };
   auto rel_arith = [&](int r) -> int {  // idx(r) computed: no memory wait in front of a DMA
     return relative_index(r < -(L - 1) ? -(L - 1) : r, 256, 512);
   };
@@ -239,23 +235,29 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     int win_tab;
     half_t mval;
   };
+  // The global loads are unconditional (clamped rows; values of rows past
+  // the sequence are never used) and the window indices come from the LDS
+  // index table.  An item's set-up reads are issued before its stage DMA: any
+  // vmcnt wait the compiler places among them (it does not count the DMA,
+  // which is inline assembly) then cannot wait for that DMA.
+  auto rel_lds = [&](int r) -> int {
+    r = r < -(L - 1) ? -(L - 1) : (r > L - 1 ? L - 1 : r);
+    return idx_tab[r + L - 1];
+  };
   auto setup_of = [&](const Item& it) -> Setup {
     Setup su;
     const int q0 = it.qt * kQT, qw = q0 + 16 * wave;
-    su.mval = t < L ? mask[(int64_t)it.b * L + t] : (half_t)0;
+    su.mval = mask[(int64_t)it.b * L + (t < L ? t : L - 1)];
     if (lane < 32)
-      su.win_tab = rel(qw - 16 * lane - 15);
+      su.win_tab = rel_lds(qw - 16 * lane - 15);
     else if (lane < 48)
-      su.win_tab = rel(qw - kKC * (lane - 32) - (kKC - 1));
+      su.win_tab = rel_lds(qw - kKC * (lane - 32) - (kKC - 1));
     else
-      su.win_tab = window_lo(q0, kKC * (lane - 48), rel);
-    su.qf0 = half8_t{};
-    su.qf1 = half8_t{};
-    if (qw < L) {
-      const half_t* qrow = Q + (int64_t)it.b * qsb + (int64_t)it.h * qsh + (int64_t)(qw + lc) * qsl;
-      su.qf0 = *reinterpret_cast<const half8_t*>(qrow + 8 * g);
-      su.qf1 = *reinterpret_cast<const half8_t*>(qrow + 32 + 8 * g);
-    }
+      su.win_tab = window_lo(q0, kKC * (lane - 48), rel_lds);
+    const int qr = qw + lc < L ? qw + lc : L - 1;
+    const half_t* qrow = Q + (int64_t)it.b * qsb + (int64_t)it.h * qsh + (int64_t)qr * qsl;
+    su.qf0 = *reinterpret_cast<const half8_t*>(qrow + 8 * g);
+    su.qf1 = *reinterpret_cast<const half8_t*>(qrow + 32 + 8 * g);
     return su;
   };
 
@@ -266,9 +268,10 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   const int n_idx = 2 * L - 1;
   const int16_t id0 = t < n_idx ? g_rel_idx[t - (L - 1) + kRelSpan] : (int16_t)0;
   const int16_t id1 = t + kThreads < n_idx ? g_rel_idx[t + kThreads - (L - 1) + kRelSpan] : (int16_t)0;
-  Setup cs = setup_of(cur);
   if (t < n_idx) idx_tab[t] = id0;
   if (t + kThreads < n_idx) idx_tab[t + kThreads] = id1;
+  stage_barrier();  // the index table is complete (setup_of reads it)
+  Setup cs = setup_of(cur);
 
   for (;;) {
     const int next = item + (int)gridDim.x;
@@ -526,14 +529,12 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
         if (last_in_1 && has_next) issue_v(v_lo, 0, v_rows < kVRowsA ? v_rows : kVRowsA);
         if (MAXT * 16 > kVRowsA && v_rows > kVRowsA) issue_v(v_hi, kVRowsA, v_rows);  // no next item here
       }
-      if (has_next) {  // after every V row
+      if (has_next) {  // after every V row; the set-up reads before the stage DMA (see setup_of)
         nit = decode(next);
+        ns = setup_of(nit);
+        next_setup = true;
         stage0_of(nit, stages3);
         next_staged = true;
-        if constexpr (OUT != GD_ATTN_OUT_CONTEXT) {
-          ns = setup_of(nit);
-          next_setup = true;
-        }
       }
 
       float inv_sum = 0.f;
@@ -617,19 +618,13 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       // V[16 T + 4 g + i][16 dt + lc], i = 0..3: the B fragment of the keys
       // that pa holds for tile T (and, from r0 + 16, for tile T + 1).  The
       // swizzle term (row >> 1) & 7 of those rows is (2 g + lc / 8) & 7 for
-      // every 16-aligned tile base.  The next item's stage, issued after the
-      // V rows (kStageOps DMA instructions), may stay in flight.
+      // every 16-aligned tile base.  The next item's stage (the last kStageOps
+      // DMA instructions, issued after the V rows) may stay in flight.
       if (next_staged)
         wait_vmcnt<kStageOps>();
       else
         wait_vmcnt<0>();
       stage_barrier();  // every wave's V rows have landed
-      if constexpr (MAXT <= 16) {
-        if (has_next) {
-          ns = setup_of(nit);
-          next_setup = true;
-        }
-      }
       if (!active) return;
       float4_t o[4];
 #pragma unroll
