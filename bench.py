@@ -51,6 +51,9 @@ def parse():
                             "out_proj", "ffn_up_gelu", "ffn_down"],
                    help="only run this kernel (--kernel-iters launches on rotating buffers) followed by a 256 MiB "
                         "torch copy, for rocprofv3 counter runs; prints the kernel table, no JSON line")
+    p.add_argument("--serving", action="store_true",
+                   help="time the JSONL runner instead (4096 text examples: JSON parse, schema formatting and "
+                        "tokenization, H2D, forward, D2H, decode) and print its own JSON line")
     return p.parse_args()
 
 
@@ -227,6 +230,45 @@ def bucket_mix_rate(model, passes=2):
                 passes=passes, sample="bucket mix: 4096 rows over L32..L512, B=32 batches, inputs in HBM")
 
 
+def serving_rate(weights, cfg, passes=2):
+    """Rows/s of the JSONL runner (RawCLI.swift:104-171) from JSONL text to
+    decoded predictions, with the compiled-graph classifier the runner uses:
+    JSON parse, schema formatting and tokenization, H2D, forward, D2H and
+    decode, batches of 32.  Rows grouped by length (the runner's default) and,
+    for comparison, by (L, Hh, O) as the reference groups them.  One untimed
+    pass of each captures every shape's graph; each timed pass starts from an
+    empty tokenizer cache."""
+    import json as _json
+    import torch
+    from gliner_decide import GLiNERDecideClassifier
+    from gliner_decide import raw_cli
+    from gliner_decide.synthetic import serving_examples, word_level_frontend
+    model = GLiNERDecideClassifier(weights, cfg, use_compiled_graph=True)
+    fe = word_level_frontend()
+    lines = [_json.dumps(e) for e in serving_examples()]
+
+    def once(by_length):
+        fe._cache.clear()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        res = raw_cli.run_examples(raw_cli.iter_jsonl(lines), fe, model, total=len(lines),
+                                   group_by_length=by_length)
+        wall = time.perf_counter() - t0
+        return wall, sum(r["inferenceMilliseconds"] for r in res) / 1e3, \
+            sum(r["preprocessingMilliseconds"] for r in res) / 1e3
+
+    out = {}
+    for by_length in (True, False):
+        once(by_length)
+        wall, gpu_s, tok_s = min(once(by_length) for _ in range(passes))
+        out["length" if by_length else "shape"] = dict(rows_s=round(len(lines) / wall, 1), wall_s=round(wall, 4),
+                                                         gpu_forward_s=round(gpu_s, 4), tokenize_s=round(tok_s, 4))
+    return dict(value=out["length"]["rows_s"], unit="rows/s", rows=len(lines), passes=passes,
+                grouped_by_length=out["length"], grouped_by_shape=out["shape"],
+                sample="4096 JSONL text examples (token counts exp(U(ln 8, ln 512)), 1-2 tasks x 2-10 labels), "
+                       "synthetic word-level tokenizer, batches of 32, compiled graphs")
+
+
 def calibration_copy(nbytes=256 << 20):
     """A plain device copy of known size: rocprofv3 FETCH_SIZE / WRITE_SIZE of
     this dispatch calibrate the counters against bytes actually moved."""
@@ -318,6 +360,15 @@ def main():
     t = time.perf_counter()
     weights = synthetic_weights(cfg, seed=4)
     log(f"weights generated in {time.perf_counter() - t:.1f} s")
+    if args.serving:
+        srv = serving_rate(weights, cfg)
+        log(f"serving: {srv}")
+        print(json.dumps({"metric": "rows/s, JSONL serving (text to decisions), 24L encoder + cls head",
+                          "value": srv["value"], "unit": "rows/s", "n_gpus": 1, "higher_is_better": True,
+                          "dtype": "f16", "data": "synthetic (seeded texts and task schemas; random-init weights)",
+                          "config": {"workload": "JSONL runner over the bucket-mix text workload", "batch": 32},
+                          "serving": srv}), flush=True)
+        return
     model = GLiNERDecideClassifier(weights, cfg, use_compiled_graph=args.compiled)
     log(f"model on device: {model.device_bytes / 2**20:.0f} MiB")
     if args.workload == "classify":

@@ -17,18 +17,54 @@ DEFAULT_BUCKETS = (32, 64, 96, 128, 256, 512)
 
 @dataclass(frozen=True)
 class DecisionTask:
-    """A task head: its label names and whether it is multi-label."""
+    """A task head (NativeTokenizer.swift:25-44): its label names, whether it
+    is multi-label, an optional prompt and optional per-label descriptions."""
 
     name: str
     labels: tuple
     multi_label: bool = False
+    prompt: str | None = None
+    label_descriptions: dict | None = None
+
+    @classmethod
+    def from_json(cls, obj: dict) -> "DecisionTask":
+        """The reference's Codable form: `name`, `labels`, `multiLabel` are
+        required, `prompt` and `labelDescriptions` optional."""
+        missing = [k for k in ("name", "labels", "multiLabel") if k not in obj]
+        if missing:
+            raise ValueError(f"decision task is missing {', '.join(missing)}")
+        if not isinstance(obj["name"], str):
+            raise ValueError("decision task name must be a string")
+        labels = obj["labels"]
+        if not isinstance(labels, list) or not all(isinstance(x, str) for x in labels):
+            raise ValueError("decision task labels must be a list of strings")
+        if not isinstance(obj["multiLabel"], bool):
+            raise ValueError("decision task multiLabel must be a boolean")
+        desc = obj.get("labelDescriptions")
+        if desc is not None and not (isinstance(desc, dict) and all(isinstance(v, str) for v in desc.values())):
+            raise ValueError("decision task labelDescriptions must map labels to strings")
+        prompt = obj.get("prompt")
+        if prompt is not None and not isinstance(prompt, str):
+            raise ValueError("decision task prompt must be a string")
+        return cls(obj["name"], tuple(labels), obj["multiLabel"], prompt, desc)
+
+    def to_json(self) -> dict:
+        out = {"name": self.name, "labels": list(self.labels), "multiLabel": self.multi_label}
+        if self.prompt is not None:
+            out["prompt"] = self.prompt
+        if self.label_descriptions is not None:
+            out["labelDescriptions"] = dict(self.label_descriptions)
+        return out
 
 
 @dataclass
-class Prediction:
+class Prediction:  # RawCLI.swift:5-9
     task: str
     labels: list
     probabilities: list
+
+    def to_json(self) -> dict:
+        return {"task": self.task, "labels": list(self.labels), "probabilities": list(self.probabilities)}
 
 
 def decode(logits, row: int, tasks) -> list:

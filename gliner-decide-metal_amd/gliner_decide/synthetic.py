@@ -267,3 +267,51 @@ def bucket_mix(seed: int = 5, count: int = 4096, batch: int = 32, vocab: int = 1
             out.append(Batch(arrays["input_ids"], arrays["attention_mask"], arrays["marker_indices"],
                              arrays["marker_mask"], tasks, valid))
     return out
+
+
+# Text workload of the JSONL runner: a word-level tokenizer over synthetic
+# words (every word one token, as in the id-level workloads above) and
+# examples whose total token counts follow the bucket mix.
+SERVING_WORDS = 60000
+
+
+def word_level_frontend(words: int = SERVING_WORDS):
+    """NativeDecisionTokenizer over a word-level vocabulary: the reference's
+    added tokens ([PAD] 0, [CLS] 1, [SEP] 2, [UNK] 3, [MASK] 4, [P], [L],
+    [SEP_TEXT], [SEP_STRUCT], [DESCRIPTION] at 128001..128005), punctuation,
+    task and label names, and `words` synthetic words w0, w1, ... from id
+    2000 on."""
+    from tokenizers import Tokenizer, models, pre_tokenizers
+    from .frontend import NativeDecisionTokenizer
+    specials = {"[PAD]": PAD_ID, "[CLS]": CLS_ID, "[SEP]": SEP_ID, "[UNK]": 3, "[MASK]": 4,
+                "[P]": PROMPT_MARKER_ID, "[L]": LABEL_MARKER_ID, "[SEP_TEXT]": SEP_TEXT_ID,
+                "[SEP_STRUCT]": SEP_STRUCT_ID, "[DESCRIPTION]": 128005}
+    vocab = dict(specials)
+    vocab.update({"(": OPEN_ID, ")": CLOSE_ID, ".": 1012, ":": 1013})
+    vocab.update({f"task{i}": 1100 + i for i in range(8)})
+    vocab.update({f"l{i}": 1200 + i for i in range(32)})
+    vocab.update({f"w{i}": 2000 + i for i in range(words)})
+    tok = Tokenizer(models.WordLevel(vocab, unk_token="[UNK]"))
+    tok.pre_tokenizer = pre_tokenizers.WhitespaceSplit()
+    tok.add_special_tokens(list(specials))
+    return NativeDecisionTokenizer.from_tokenizer(tok, specials)
+
+
+def serving_examples(seed: int = 7, count: int = 4096, words: int = SERVING_WORDS, min_len: int = 8,
+                     max_len: int = 512) -> list:
+    """JSONL example objects {"id", "text", "tasks"}: 1-2 single-label tasks
+    of 2-10 labels, total token counts exp(U(ln 8, ln 512)) (schema + text +
+    the final "."; at least one text word), text words drawn Zipf(1.1) over
+    the synthetic vocabulary."""
+    r = _rng(seed, "serving")
+    lengths = np.exp(r.uniform(np.log(min_len), np.log(max_len), size=count))
+    out = []
+    for i in range(count):
+        labels = [int(r.integers(2, 11)) for _ in range(int(r.integers(1, 3)))]
+        tasks = [{"name": f"task{t}", "labels": [f"l{j}" for j in range(n)], "multiLabel": False}
+                 for t, n in enumerate(labels)]
+        schema = sum(6 + 2 * n for n in labels) + len(labels)  # groups, [SEP_STRUCT]s, [SEP_TEXT]
+        n_words = int(min(max(1, round(lengths[i]) - schema - 1), max_len - schema - 1))
+        ranks = np.minimum(r.zipf(1.1, size=n_words), words) - 1
+        out.append({"id": f"s{i}", "text": " ".join(f"w{k}" for k in ranks), "tasks": tasks})
+    return out

@@ -247,7 +247,10 @@ int gd_classifier_create(gd_classifier** out, const gd_weight_store* store, cons
 void gd_classifier_destroy(gd_classifier* model);
 
 /* Pre-allocates activation memory for batches up to max_batch x max_seq_len
- * with up to max_heads x max_options markers. */
+ * with up to max_heads x max_options markers.  What is kept is the two
+ * products: any later call with B*L <= max_batch*max_seq_len tokens and
+ * B*Hh*O <= max_batch*max_heads*max_options markers fits without growing it
+ * (growing it drops the captured graphs). */
 int gd_classifier_reserve(gd_classifier* model, int64_t max_batch, int64_t max_seq_len,
                           int64_t max_heads, int64_t max_options);
 
