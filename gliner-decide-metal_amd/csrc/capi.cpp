@@ -252,7 +252,7 @@ int gd_classifier_create(gd_classifier** out, const gd_weight_store* store, cons
                          void* stream) {
   clear_error();
   GD_CHECK_ARG(out && store, "null output or store");
-  GD_CHECK_ARG((flags & ~(GD_USE_FUSED_KERNELS | GD_USE_COMPILED_GRAPH | GD_USE_GENERIC_ATTENTION)) == 0,
+  GD_CHECK_ARG((flags & ~(GD_USE_FUSED_KERNELS | GD_USE_COMPILED_GRAPH | GD_USE_GENERIC_ATTENTION | GD_FULL_ROWS)) == 0,
                "unknown flags 0x%x", flags);
   gd_config cfg;
   if (config) {

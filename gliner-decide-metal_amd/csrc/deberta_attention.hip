@@ -127,8 +127,8 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K, const half_t* __restrict__ V, int qsb, int qsh,
     int qsl, int ksb, int ksh, int ksl, int vsb, int vsh, int vsl, const half_t* __restrict__ PK,
     const half_t* __restrict__ PQ, int pksh, int pksp, int pqsh, int pqsp, const half_t* __restrict__ mask,
-    int mask_kind, int B, int H, int L, int P, int bucket_size, float scale_qk, float scale16,
-    half_t* __restrict__ out, int ldo) {
+    int mask_kind, const int* __restrict__ row_len, int B, int H, int L, int P, int bucket_size, float scale_qk,
+    float scale16, half_t* __restrict__ out, int ldo) {
   // Two stage buffers and the per-wave scratch.  The stage DMA is inline
   // assembly the compiler does not track, so its reads of a stage never wait
   // for the next stage's loads in flight; the kernel orders them itself
@@ -151,8 +151,6 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int lc = lane & 15;  // MFMA output column: the lane's query
   const int g = lane >> 4;   // lane group
-  const int nt = L >> 4;
-  const int nchunks = (L + kKC - 1) / kKC;
   const float inv_scale16 = 1.0f / scale16;  // correctly rounded fp32 reciprocal
   half_t* c2p_w = scratch_lds + wave * kScratchWave;
   half_t* p2c_w = c2p_w + 16 * kC2PStride;
@@ -182,10 +180,11 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     return w < 0 ? 0 : (w > 512 - kWin ? 512 - kWin : w);
   };
   // Stage of key chunk kc into buffer st: kStageOps DMA instructions per wave.
-  auto issue_stage = [&](lds_half_t* st, const half_t* Kb, const half_t* PKh, const half_t* PQh, int kc, int wlo) {
-    {  // K rows: 8 blocks of 8 rows, one per wave
+  auto issue_stage = [&](lds_half_t* st, const half_t* Kb, const half_t* PKh, const half_t* PQh, int kc, int wlo,
+                         int klim) {
+    {  // K rows: 8 blocks of 8 rows, one per wave; rows from klim on repeat row klim - 1
       int key = kc + wave * 8 + blk_row;
-      key = key < L ? key : L - 1;
+      key = key < klim ? key : klim - 1;
       load_lds16(Kb + (int64_t)key * ksl + blk_chunk * 8, st + wave * 512);
     }
 #pragma unroll
@@ -208,21 +207,30 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   // XCD.  Each item's first stage and per-thread set-up reads are issued
   // while the previous item finishes (last chunk, softmax, P.V, stores), into
   // the stage buffer that item no longer needs. ----
+  // `len` is the item's row extent: positions from len on take no part (keys
+  // past it are neither read nor weighted, queries past it are not computed);
+  // L without a row-extent array.  `klim` = max(len, 1) bounds row reads.
   struct Item {
-    int b, h, qt;
+    int b, h, qt, len, klim;
   };
   auto decode = [&](int item) -> Item {
     int bid = item;
     if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
     const int bh = bid / ntq;
-    return Item{__builtin_amdgcn_readfirstlane(bh / H), __builtin_amdgcn_readfirstlane(bh % H),
-                __builtin_amdgcn_readfirstlane(bid % ntq)};
+    const int b = __builtin_amdgcn_readfirstlane(bh / H);
+    int len = L;
+    if (row_len != nullptr) {
+      len = __builtin_amdgcn_readfirstlane(row_len[b]);
+      len = len < 0 ? 0 : (len > L ? L : len);
+    }
+    return Item{b, __builtin_amdgcn_readfirstlane(bh % H), __builtin_amdgcn_readfirstlane(bid % ntq), len,
+                len > 0 ? len : 1};
   };
   // Window start of chunk 0 per query tile (at most 4), lane qt of w0_tab.
   const int w0_tab = window_lo(kQT * (lane & 3), 0, rel_arith);
   auto stage0_of = [&](const Item& it, lds_half_t* st) {
     issue_stage(st, K + (int64_t)it.b * ksb + (int64_t)it.h * ksh, PK + (int64_t)it.h * pksh,
-                PQ + (int64_t)it.h * pqsh, 0, __builtin_amdgcn_readlane(w0_tab, it.qt));
+                PQ + (int64_t)it.h * pqsh, 0, __builtin_amdgcn_readlane(w0_tab, it.qt), it.klim);
   };
   // Per-thread set-up reads of an item: its key-mask entry, its lane of the
   // window table and the Q fragments.  Window table (read with readlane):
@@ -254,7 +262,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       su.win_tab = rel_lds(qw - kKC * (lane - 32) - (kKC - 1));
     else
       su.win_tab = window_lo(q0, kKC * (lane - 48), rel_lds);
-    const int qr = qw + lc < L ? qw + lc : L - 1;
+    const int qr = qw + lc < it.klim ? qw + lc : it.klim - 1;
     const half_t* qrow = Q + (int64_t)it.b * qsb + (int64_t)it.h * qsh + (int64_t)qr * qsl;
     su.qf0 = *reinterpret_cast<const half8_t*>(qrow + 8 * g);
     su.qf1 = *reinterpret_cast<const half8_t*>(qrow + 32 + 8 * g);
@@ -297,7 +305,14 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       const int b = cur.b, h = cur.h;
       const int q0 = cur.qt * kQT;
       const int qw = q0 + 16 * wave;
-      const bool active = qw < L;
+      // Key tiles and chunks of this item: up to its row extent.  An item
+      // whose queries all lie past the extent computes nothing; it runs one
+      // chunk step (its first stage is already in flight) and loads no V.
+      const bool live = q0 < cur.len;
+      const int nt = live ? (cur.len + 15) >> 4 : 0;
+      const int nchunks = live ? (nt + 3) >> 2 : 1;
+      const int klim = cur.klim;
+      const bool active = qw < cur.len;
       const half_t* Kb = K + (int64_t)b * ksb + (int64_t)h * ksh;
       const half_t* PKh = PK + (int64_t)h * pksh;
       const half_t* PQh = PQ + (int64_t)h * pqsh;
@@ -317,12 +332,12 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       // ---- V for the P.V pass: rows [row_lo, row_hi) of the (b, h) slice
       // land row-major and swizzled like K at rows 0.. of an LDS buffer, by
       // DMA (placement: after the chunk loop).  Rows past the sequence repeat
-      // row L - 1; their probabilities are exactly 0. ----
-      const int v_rows = ((L + 31) >> 5) << 5;  // the P.V tile pairs reach this far
+      // row klim - 1; their probabilities are exactly 0. ----
+      const int v_rows = ((16 * nt + 31) >> 5) << 5;  // the P.V tile pairs reach this far
       auto issue_v = [&](lds_half_t* dst, int row_lo, int row_hi) {
         for (int blk = wave; 8 * blk < row_hi - row_lo; blk += kWaves) {  // uniform
           int key = row_lo + 8 * blk + blk_row;
-          key = key < L ? key : L - 1;
+          key = key < klim ? key : klim - 1;
           load_lds16(Vb + (int64_t)key * vsl + blk_chunk * 8, dst + blk * 512);
         }
       };
@@ -337,7 +352,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
         half_t* const st = stages + (c & 1) * kStage;
         lds_half_t* const so = stages3 + ((c + 1) & 1) * kStage;  // free: every wave is done with stage c - 1
         if (c + 1 < nchunks) {
-          issue_stage(so, Kb, PKh, PQh, (c + 1) * kKC, win(48 + c + 1));
+          issue_stage(so, Kb, PKh, PQh, (c + 1) * kKC, win(48 + c + 1), klim);
         } else if constexpr (OUT == GD_ATTN_OUT_CONTEXT) {  // V rows into the free buffer
           if (!(c & 1) || !has_next) issue_v(so, 0, v_rows < kVRowsA ? v_rows : kVRowsA);
         }
@@ -496,10 +511,11 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
           wave_lds_sync();  // the last gathers precede the next chunk's c2p / p2c stores
         };
         if (active) {
-          const bool lin = (kc + kKC <= L) && (qw - kc - (kKC - 1) >= -kMid) && (qw + 15 - kc <= kMid);
+          const bool full = kc + kKC <= 16 * nt;
+          const bool lin = full && (qw - kc - (kKC - 1) >= -kMid) && (qw + 15 - kc <= kMid);
           if (lin)
             chunk(std::true_type{}, std::true_type{});
-          else if (kc + kKC <= L)
+          else if (full)
             chunk(std::false_type{}, std::true_type{});
           else
             chunk(std::false_type{}, std::false_type{});
@@ -736,7 +752,8 @@ int launch2(const AttentionArgs& a, hipStream_t stream) {
 #define GD_ATTN2(OUTK)                                                                                            \
   hipLaunchKernelGGL((deberta_attention_kernel<MAXT, OUTK>), grid, block, 0, stream, hq, hk, hv, (int)a.qsb,     \
                      (int)a.qsh, (int)a.qsl, (int)a.ksb, (int)a.ksh, (int)a.ksl, (int)a.vsb, (int)a.vsh, (int)a.vsl, \
-                     hpk, hpq, (int)a.pksh, (int)a.pksp, (int)a.pqsh, (int)a.pqsp, hm, a.mask_kind, (int)a.B,       \
+                     hpk, hpq, (int)a.pksh, (int)a.pksp, (int)a.pqsh, (int)a.pqsp, hm, a.mask_kind, a.row_len,      \
+                     (int)a.B,                                                                                      \
                      (int)a.H, (int)a.L, (int)a.P, a.bucket_size, a.scale_qk, a.scale16, ho, (int)a.ldo)
   switch (a.output) {
     case GD_ATTN_OUT_PROBS:
@@ -754,7 +771,46 @@ int launch2(const AttentionArgs& a, hipStream_t stream) {
   return GD_OK;
 }
 
+// One workgroup (4 waves) per batch row.
+__global__ __launch_bounds__(256) void row_extent_kernel(const half_t* __restrict__ mask,
+                                                         const int32_t* __restrict__ markers,
+                                                         const float* __restrict__ marker_mask, int L, int slots,
+                                                         int32_t* __restrict__ out) {
+  const int b = blockIdx.x;
+  int ext = 0;
+  for (int l = threadIdx.x; l < L; l += 256)
+    if ((float)mask[(int64_t)b * L + l] > 0.f) ext = l + 1;  // l grows: the last hit is the largest
+  for (int s = threadIdx.x; s < slots; s += 256)
+    if (marker_mask[(int64_t)b * slots + s] > 0.f) {
+      const int p = markers[(int64_t)b * slots + s];
+      const int e = (p >= 0 && p < L) ? p + 1 : 1;
+      ext = e > ext ? e : ext;
+    }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const int o = __shfl_xor(ext, off, 64);
+    ext = o > ext ? o : ext;
+  }
+  __shared__ int wave_max[4];
+  if ((threadIdx.x & 63) == 0) wave_max[threadIdx.x >> 6] = ext;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int m = wave_max[0];
+    for (int w = 1; w < 4; ++w) m = wave_max[w] > m ? wave_max[w] : m;
+    out[b] = m;
+  }
+}
+
 }  // namespace
+
+int launch_row_extent(const void* mask, const int32_t* markers, const float* marker_mask, int64_t B, int64_t L,
+                      int64_t slots, int32_t* out, hipStream_t stream) {
+  if (B <= 0) return GD_OK;
+  hipLaunchKernelGGL(row_extent_kernel, dim3((unsigned)B), dim3(256), 0, stream, static_cast<const half_t*>(mask),
+                     markers, marker_mask, (int)L, (int)slots, out);
+  GD_LAUNCH_CHECK();
+  return GD_OK;
+}
 
 int ensure_relative_index_table(hipStream_t stream) {
   static std::mutex mu;
@@ -782,6 +838,8 @@ int ensure_relative_index_table(hipStream_t stream) {
 
 int launch_deberta_attention(const AttentionArgs& a, hipStream_t stream) {
   if (a.bucket_size != 256 || a.P != 512) return fail(GD_ERR_SHAPE, "attention: bucket size 256 and 512 positions");
+  if (a.row_len != nullptr && a.output != GD_ATTN_OUT_CONTEXT)
+    return fail(GD_ERR_INVALID_ARGUMENT, "attention: row extents apply to the context output only");
   for (int64_t st : {a.qsb, a.qsh, a.qsl, a.ksb, a.ksh, a.ksl, a.vsb, a.vsh, a.vsl, a.pksh, a.pksp, a.pqsh, a.pqsp, a.ldo})
     if (st < 0 || st > INT32_MAX) return fail(GD_ERR_SHAPE, "attention: strides must lie in [0, 2^31)");
   GD_RETURN_IF_ERROR(ensure_relative_index_table(stream));

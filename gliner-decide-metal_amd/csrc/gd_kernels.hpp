@@ -42,9 +42,19 @@ struct AttentionArgs {
   int output;      // GD_ATTN_OUT_*
   void* out;
   int64_t ldo;
+  // Optional row extents [B] (context output only): keys at or past row_len[b]
+  // are not read, queries at or past it are not computed (their output rows
+  // hold copies or are left as they were).
+  const int32_t* row_len = nullptr;
 };
 
 int launch_deberta_attention(const AttentionArgs& args, hipStream_t stream);
+
+// Row extents for the attention: out[b] = max(last l with mask[b, l] > 0,
+// last position read by a marker slot of row b with marker_mask > 0
+// (position 0 for an out-of-range index)) + 1, or 0.
+int launch_row_extent(const void* mask, const int32_t* markers, const float* marker_mask, int64_t B, int64_t L,
+                      int64_t slots, int32_t* out, hipStream_t stream);
 
 int launch_relative_bias_general(const void* q, const void* k, const void* pos_key, const void* pos_query,
                                  const int32_t* c2p, const int32_t* p2c, const void* key_mask, float scale, int64_t B,

@@ -247,7 +247,6 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(const half_t* __restr
 // remaining MFMAs.  The epilogue stages the fp16 tile through the stage
 // buffers and writes 16-byte coalesced row segments.
 // ---------------------------------------------------------------------------
-constexpr int kThreads8 = 512;
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
@@ -279,14 +278,14 @@ struct StageLayout {
 template <int V>
 using ic = std::integral_constant<int, V>;
 
-template <int BM, int BN, int WAVES_M, int BK, int NSTAGE, int EPI>
-__global__ __launch_bounds__(kThreads8) void gemm_nt_lds_kernel(const half_t* __restrict__ A,
+template <int BM, int BN, int WAVES_M, int BK, int NSTAGE, int EPI, int NW>
+__global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __restrict__ A,
                                                                 const half_t* __restrict__ W,
                                                                 const half_t* __restrict__ bias,
                                                                 half_t* __restrict__ C, int M, int N, int K,
                                                                 int64_t lda, int64_t ldc, int tiles_m, int tiles_n) {
   using Lay = StageLayout<BK>;
-  constexpr int NW = 8;
+  constexpr int NT = 64 * NW;  // threads
   constexpr int WAVES_N = NW / WAVES_M;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int TM = WM / 32, TN = WN / 32;
@@ -454,23 +453,23 @@ __global__ __launch_bounds__(kThreads8) void gemm_nt_lds_kernel(const half_t* __
   __syncthreads();  // all waves done reading the stage buffers; every load landed
 
   constexpr int CHUNKS_PER_ROW = BN / 8;
-  constexpr int ROWS_PER_PASS = kThreads8 / CHUNKS_PER_ROW;
+  constexpr int ROWS_PER_PASS = NT / CHUNKS_PER_ROW;
   const int cc = t % CHUNKS_PER_ROW;
   if constexpr (GELU_TABLE) {
     // ---- GELU epilogue: table into st1, C through st0 in two passes ----
     // All of this thread's table pieces are loaded before any is stored, so
     // the L2 latency is paid once.
     constexpr int kPieces = kGeluEntries / 8;
-    constexpr int kPerThread = (kPieces + kThreads8 - 1) / kThreads8;
+    constexpr int kPerThread = (kPieces + NT - 1) / NT;
     half8_t piece[kPerThread];
 #pragma unroll
     for (int r = 0; r < kPerThread; ++r) {
-      const int i = t + r * kThreads8;
+      const int i = t + r * NT;
       if (i < kPieces) piece[r] = *reinterpret_cast<const half8_t*>(g_gelu_table + 8 * i);
     }
 #pragma unroll
     for (int r = 0; r < kPerThread; ++r) {
-      const int i = t + r * kThreads8;
+      const int i = t + r * NT;
       if (i < kPieces) *reinterpret_cast<half8_t*>(st1 + 8 * i) = piece[r];
     }
     __syncthreads();
@@ -540,14 +539,14 @@ __global__ __launch_bounds__(kThreads8) void gemm_nt_lds_kernel(const half_t* __
   }
 }
 
-template <int BM, int BN, int WAVES_M, int BK, int NSTAGE>
+template <int BM, int BN, int WAVES_M, int BK, int NSTAGE, int NW = 8>
 int launch_lds_tile(const half_t* A, const half_t* W, const half_t* bias, half_t* C, int M, int N, int K, int64_t lda,
                     int64_t ldc, int epi, hipStream_t stream) {
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = N / BN;
-  const dim3 grid(tiles_m * tiles_n), block(kThreads8);
+  const dim3 grid(tiles_m * tiles_n), block(64 * NW);
 #define GD_LDS_GEMM(E)                                                                                               \
-  hipLaunchKernelGGL((gemm_nt_lds_kernel<BM, BN, WAVES_M, BK, NSTAGE, E>), grid, block, 0, stream, A, W, bias, C, M, N, \
+  hipLaunchKernelGGL((gemm_nt_lds_kernel<BM, BN, WAVES_M, BK, NSTAGE, E, NW>), grid, block, 0, stream, A, W, bias, C, M, N, \
                      K, lda, ldc, tiles_m, tiles_n)
   switch (epi) {
     case GD_EPI_NONE: GD_LDS_GEMM(GD_EPI_NONE); break;

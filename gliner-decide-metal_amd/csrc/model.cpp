@@ -260,6 +260,7 @@ int Classifier::reserve(int64_t B, int64_t L, int64_t Hh, int64_t O) {
   GD_RETURN_IF_ERROR(A((size_t)nm * 4, &ws_.markers));
   GD_RETURN_IF_ERROR(A((size_t)nm * 4, &ws_.marker_mask));
   GD_RETURN_IF_ERROR(A((size_t)nm * 2, &ws_.logits));
+  GD_RETURN_IF_ERROR(A((size_t)nt * 4, &ws_.row_len));  // B <= B * L
   ws_bytes_ = device_bytes_ - before;
   ws_tokens_ = nt;
   ws_markers_ = nm;
@@ -267,7 +268,8 @@ int Classifier::reserve(int64_t B, int64_t L, int64_t Hh, int64_t O) {
 }
 
 // One encoder layer (DeBERTa.swift:296-428).
-int Classifier::layer_forward(int li, const void* mask, int64_t B, int64_t L, hipStream_t stream, StageHook* hook) {
+int Classifier::layer_forward(int li, const void* mask, int64_t B, int64_t L, hipStream_t stream, StageHook* hook,
+                              const int32_t* row_len) {
   const Layer& Ly = layers_[li];
   const int64_t C = cfg_.hidden_size, F = cfg_.intermediate_size, H = cfg_.num_attention_heads, D = C / H;
   const int64_t T = B * L;
@@ -310,6 +312,7 @@ int Classifier::layer_forward(int li, const void* mask, int64_t B, int64_t L, hi
   a.output = GD_ATTN_OUT_CONTEXT;
   a.out = ws_.ctx;
   a.ldo = C;
+  a.row_len = row_len;
   GD_RETURN_IF_ERROR(launch_deberta_attention(a, stream));
   if (hook) {
     std::snprintf(name, sizeof name, "layer_%d_attention", li);
@@ -341,14 +344,14 @@ int Classifier::layer_forward(int li, const void* mask, int64_t B, int64_t L, hi
 }
 
 int Classifier::encode_into_workspace(const int32_t* ids, const void* mask, int64_t B, int64_t L, int num_layers,
-                                      hipStream_t stream, StageHook* hook) {
+                                      hipStream_t stream, StageHook* hook, const int32_t* row_len) {
   const int64_t T = B * L;
   if (hook) hook->begin(stream);
   GD_RETURN_IF_ERROR(launch_embedding_layer_norm(ids, mask, word_emb_, emb_g_, emb_b_, ws_.hidden, T,
                                                  cfg_.hidden_size, cfg_.vocab_size, cfg_.layer_norm_eps, err_flag_,
                                                  stream));
   if (hook) hook->end("embedding", stream);
-  for (int i = 0; i < num_layers; ++i) GD_RETURN_IF_ERROR(layer_forward(i, mask, B, L, stream, hook));
+  for (int i = 0; i < num_layers; ++i) GD_RETURN_IF_ERROR(layer_forward(i, mask, B, L, stream, hook, row_len));
   return GD_OK;
 }
 
@@ -357,7 +360,16 @@ int Classifier::forward(const int32_t* ids, const void* mask, const int32_t* mar
                         StageHook* hook) {
   const int64_t C = cfg_.hidden_size, CH = cfg_.classifier_hidden;
   const int64_t M = B * Hh * O;
-  GD_RETURN_IF_ERROR(encode_into_workspace(ids, mask, B, L, cfg_.num_hidden_layers, stream, hook));
+  // Each row's attention stops at its extent (unless GD_FULL_ROWS): every
+  // position the classifier reads lies before it, and positions past it are
+  // masked keys that feed nothing before it.
+  const int32_t* row_len = nullptr;
+  if (!(flags_ & GD_FULL_ROWS)) {
+    row_len = static_cast<const int32_t*>(ws_.row_len);
+    GD_RETURN_IF_ERROR(launch_row_extent(mask, markers, marker_mask, B, L, Hh * O, static_cast<int32_t*>(ws_.row_len),
+                                         stream));
+  }
+  GD_RETURN_IF_ERROR(encode_into_workspace(ids, mask, B, L, cfg_.num_hidden_layers, stream, hook, row_len));
   // classifier (:430-444)
   if (hook) hook->begin(stream);
   GD_RETURN_IF_ERROR(launch_marker_rows(markers, static_cast<int32_t*>(ws_.marker_rows), B, L, Hh * O, err_flag_,

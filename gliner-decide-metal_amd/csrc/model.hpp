@@ -54,6 +54,7 @@ class Classifier {
   struct Workspace {
     void *hidden = nullptr, *qkv = nullptr, *ctx = nullptr, *tmp = nullptr, *ffn = nullptr;
     void *marker_rows = nullptr, *inner = nullptr;
+    void* row_len = nullptr;  // int32 [B]: per-row attention extents of classify
     void *ids = nullptr, *mask = nullptr, *markers = nullptr, *marker_mask = nullptr, *logits = nullptr;
   };
   using ShapeKey = std::tuple<int64_t, int64_t, int64_t, int64_t>;
@@ -67,9 +68,10 @@ class Classifier {
              hipStream_t stream);
   int upload_concat(const WeightStore& store, const std::vector<std::string>& keys,
                     const std::vector<std::vector<int64_t>>& shapes, void** out, hipStream_t stream);
-  int layer_forward(int li, const void* mask, int64_t B, int64_t L, hipStream_t stream, StageHook* hook);
+  int layer_forward(int li, const void* mask, int64_t B, int64_t L, hipStream_t stream, StageHook* hook,
+                    const int32_t* row_len = nullptr);
   int encode_into_workspace(const int32_t* ids, const void* mask, int64_t B, int64_t L, int num_layers,
-                            hipStream_t stream, StageHook* hook);
+                            hipStream_t stream, StageHook* hook, const int32_t* row_len = nullptr);
   int forward(const int32_t* ids, const void* mask, const int32_t* markers, const float* marker_mask, int64_t B,
               int64_t L, int64_t Hh, int64_t O, void* logits, hipStream_t stream, StageHook* hook);
   void release_graphs();

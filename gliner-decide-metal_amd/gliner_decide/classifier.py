@@ -92,12 +92,16 @@ class GLiNERDecideClassifier:
     use_fast_attention=False (explicit-score path) is not built and raises.
     use_custom_relative_kernel / use_fused_attention_kernel are accepted for
     API compatibility: the fused relative-bias + softmax + P.V kernel is the
-    only attention path, so both select it.
+    only attention path, so both select it.  full_rows (no counterpart in the
+    reference) makes classify compute every position; by default each row's
+    attention stops at its extent (last unmasked or marker-read position + 1),
+    which leaves the logits unchanged.
     """
 
     def __init__(self, weights, configuration: DeBERTaV2Configuration | None = None, use_fused_kernels: bool = False,
                  use_compiled_graph: bool = False, use_fast_attention: bool = True,
-                 use_custom_relative_kernel: bool = False, use_fused_attention_kernel: bool = False):
+                 use_custom_relative_kernel: bool = False, use_fused_attention_kernel: bool = False,
+                 full_rows: bool = False):
         require_gpu()
         self._lib = N.lib()
         self.configuration = configuration or DeBERTaV2Configuration.default()
@@ -114,6 +118,8 @@ class GLiNERDecideClassifier:
             flags |= N.GD_USE_COMPILED_GRAPH
         if not use_fast_attention:
             flags |= N.GD_USE_GENERIC_ATTENTION
+        if full_rows:
+            flags |= N.GD_FULL_ROWS
         cfg = self.configuration.to_native()
         h = C.c_void_p()
         N.check(self._lib.gd_classifier_create(C.byref(h), store.handle, C.byref(cfg), flags, stream_handle()))

@@ -237,6 +237,14 @@ typedef struct gd_classifier gd_classifier;
 #define GD_USE_FUSED_KERNELS 1u    /* useFusedKernels: residual LN keeps x + residual in fp32 */
 #define GD_USE_COMPILED_GRAPH 2u   /* useCompiledGraph: capture each shape's forward in a hipGraph */
 #define GD_USE_GENERIC_ATTENTION 4u /* useFastAttention = false (explicit-score path) -- unsupported */
+/* No counterpart in the reference.  By default classify computes each row's
+ * attention only up to its extent: the larger of (last position with
+ * attention_mask > 0) + 1 and (last position a marker slot with
+ * marker_mask > 0 reads) + 1.  Positions past the extent are masked keys and
+ * feed no position before it, so the logits are the same; their hidden
+ * states are not computed.  GD_FULL_ROWS computes every position, as the
+ * reference's graph does (encode and layer_forward always do). */
+#define GD_FULL_ROWS 8u
 
 /* Loads and checks the weights (key names and shapes of
  * DeBERTa.swift:127-149, 199-208, 228-229), uploads them to the current

@@ -79,6 +79,43 @@ def test_encoder_and_logits_small_model_padded():
     assert np.max(np.abs(got_logits - want_logits)) <= 2e-3
 
 
+@pytest.mark.parametrize("L", [128, 256, 512])
+def test_row_extents_leave_logits_unchanged(L):
+    """classify stops each row's attention at its extent (last unmasked or
+    marker-read position + 1); the logits must equal those of the full
+    computation (GD_FULL_ROWS) bit for bit: rows of different lengths, a
+    marker past the last unmasked token, an all-masked row, a mask with holes,
+    a one-token row, and a masked marker slot pointing past the extent."""
+    from gliner_decide import DecisionInput, GLiNERDecideClassifier
+    from gliner_decide.config import DeBERTaV2Configuration
+    from gliner_decide.synthetic import synthetic_weights
+    pc = DeBERTaV2Configuration(num_hidden_layers=2, vocab_size=3000)
+    w = synthetic_weights(pc, seed=13)
+    fast = GLiNERDecideClassifier(w, pc)
+    full = GLiNERDecideClassifier(w, pc, full_rows=True)
+    r = np.random.default_rng(L)
+    B = 6
+    ids = r.integers(1000, 3000, size=(B, L)).astype(np.int32)
+    lengths = np.array([L, 40, 17, 0, L // 2 + 3, 1])
+    mask = (np.arange(L)[None] < lengths[:, None]).astype(np.float16)
+    mask[4, 20:30] = 0  # holes
+    ids[mask == 0] = 0
+    mi = np.zeros((B, 2, 3), np.int32)
+    mm = np.zeros((B, 2, 3), np.float32)
+    for b in range(B):
+        n = max(int(lengths[b]), 4)
+        mi[b] = r.integers(0, n, size=(2, 3))
+        mm[b] = 1
+    mi[2, 1, 2] = L - 7  # a marker past the row's last unmasked token
+    mi[1, 0, 1], mm[1, 0, 1] = L - 1, 0  # masked slot: does not extend the row
+    mm[5, 1] = 0
+    inp = DecisionInput(ids, mask, mi, mm)
+    a = fast.classify(inp).logits.float().cpu().numpy()
+    b_ = full.classify(inp).logits.float().cpu().numpy()
+    assert np.all(np.isfinite(a)) and np.all(a[mm == 0] == -10000.0)
+    np.testing.assert_array_equal(a, b_)
+
+
 def test_compiled_graph_replays_match_eager():
     from gliner_decide import DecisionInput, GLiNERDecideClassifier
     from gliner_decide.config import DeBERTaV2Configuration
