@@ -213,9 +213,22 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   struct Item {
     int b, h, qt, len, klim;
   };
+  // Remap: item w + j gridDim.x (workgroup w on XCD w % 8, round j) becomes
+  // local index l = w / 8 + j G (G = gridDim.x / 8) of XCD w % 8's contiguous
+  // share, so the two query tiles of a (b, h) (l = 2m, 2m + 1 at L = 256) run
+  // side by side on one XCD and share their K, V and table reads through its
+  // L2.  On odd rounds l is swapped with its partner (l ^ 1): a workgroup's
+  // successive items alternate between the pair's query tiles, which differ
+  // in cost under row extents (when G and the share are even, the pairs stay
+  // within a round).
+  const bool swap_rounds = ((nblk >> 3) & 1) == 0 && ((gridDim.x >> 3) & 1) == 0 && gridDim.x >= 8;
   auto decode = [&](int item) -> Item {
     int bid = item;
-    if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+    if ((nblk & 7) == 0) {
+      int l = bid >> 3;
+      if (swap_rounds) l ^= (l / (int)(gridDim.x >> 3)) & 1;
+      bid = (bid & 7) * (nblk >> 3) + l;
+    }
     const int bh = bid / ntq;
     const int b = __builtin_amdgcn_readfirstlane(bh / H);
     int len = L;
