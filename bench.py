@@ -206,17 +206,20 @@ def bucket_mix_rate(model, passes=2):
     shape's workspace exists."""
     import torch
     from gliner_decide import DecisionInput
+    from gliner_decide.decode import row_extents
     from gliner_decide.synthetic import bucket_mix
     batches = []
     for x in bucket_mix(seed=5):
-        ids, mask, mk, mm = DecisionInput(**x.arrays()).to_device()
+        a = x.arrays()
+        ids, mask, mk, mm = DecisionInput(**a).to_device()
         out = torch.empty((ids.shape[0], mk.shape[1], mk.shape[2]), dtype=torch.float16, device=ids.device)
-        batches.append((ids, mask, mk, mm, out, x.valid_rows))
+        batches.append((ids, mask, mk, mm, out, x.valid_rows, a))
     rows = sum(b[5] for b in batches)
 
     def one_pass():
-        for ids, mask, mk, mm, out, _ in batches:
-            model.classify_device(ids, mask, mk, mm, out)
+        for ids, mask, mk, mm, out, _, a in batches:
+            total = int(row_extents(a["attention_mask"], a["marker_indices"], a["marker_mask"]).sum())
+            model.classify_device(ids, mask, mk, mm, out, total_tokens=total)
 
     one_pass()
     torch.cuda.synchronize()
@@ -227,7 +230,8 @@ def bucket_mix_rate(model, passes=2):
     elapsed = time.perf_counter() - t0
     assert all(torch.isfinite(b[4].float()).all() for b in batches)
     return dict(value=round(rows * passes / elapsed, 1), unit="rows/s", rows=rows, batches=len(batches),
-                passes=passes, sample="bucket mix: 4096 rows over L32..L512, B=32 batches, inputs in HBM")
+                passes=passes, sample="bucket mix: 4096 rows over L32..L512, B=32 batches, inputs in HBM, "
+                                      "packed rows")
 
 
 def serving_rate(weights, cfg, passes=2):
@@ -347,6 +351,7 @@ def main():
     import torch
     from gliner_decide import DecisionInput, GLiNERDecideClassifier
     from gliner_decide.config import DeBERTaV2Configuration
+    from gliner_decide.decode import row_extents
     from gliner_decide.synthetic import classification_batch, long_context_batch, synthetic_weights
 
     torch.cuda.set_device(0)
@@ -379,23 +384,39 @@ def main():
         batch = long_context_batch(seed=6)
         wl = dict(workload="24L encoder + classifier, B=64 L=512 full rows, 3 heads (20/20/8 labels)",
                   global_batch=64, seq_len=512)
-    ids, mask, markers, mmask = DecisionInput(**batch.arrays()).to_device()
+    host = batch.arrays()
+    ids, mask, markers, mmask = DecisionInput(**host).to_device()
     B, L = ids.shape
     _, Hh, O_ = markers.shape
     model.reserve(B, L, Hh, O_)
     logits = torch.empty((B, Hh, O_), dtype=torch.float16, device=ids.device)
+
+    def step():
+        # the packed forward's token count comes from the host copy of the
+        # batch (what a tokenizer knows), every step
+        total = int(row_extents(host["attention_mask"], host["marker_indices"], host["marker_mask"]).sum())
+        model.classify_device(ids, mask, markers, mmask, logits, total_tokens=total)
+
+    def timed(fn, steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
     for _ in range(args.warmup):
-        model.classify_device(ids, mask, markers, mmask, logits)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        model.classify_device(ids, mask, markers, mmask, logits)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+        step()
+    elapsed = timed(step, args.steps)
     ms = elapsed * 1000 / args.steps
     rows_s = B * args.steps / elapsed
     assert torch.isfinite(logits.float()).all()
-    log(f"e2e: {ms:.3f} ms/step, {rows_s:.1f} rows/s")
+    log(f"e2e: {ms:.3f} ms/step, {rows_s:.1f} rows/s (packed rows)")
+    padded = lambda: model.classify_device(ids, mask, markers, mmask, logits)  # noqa: E731
+    for _ in range(args.warmup):
+        padded()
+    padded_s = timed(padded, args.steps)
+    log(f"e2e padded: {padded_s * 1000 / args.steps:.3f} ms/step, {B * args.steps / padded_s:.1f} rows/s")
 
     kernels = measure_kernels(cfg, args.kernel_iters)
     for k, v in kernels.items():
@@ -428,7 +449,7 @@ def main():
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic (seeded ids/lengths; random-init N(0,0.02) fp16 weights of DeBERTa-v3-large + GLiNER head)",
-        "config": dict(wl, parallelism="single GPU", compiled_graph=args.compiled),
+        "config": dict(wl, parallelism="single GPU", compiled_graph=args.compiled, rows="packed"),
         "roofline": roof,
         "cpu_baseline": cpu,
         "kernels": {k: dict({kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()},
@@ -439,6 +460,7 @@ def main():
         "relbias_softmax_gbs": round(kernels["relbias_softmax"]["gbs"], 1),
         "relbias_softmax_frac_hbm": round(kernels["relbias_softmax"]["gbs"] / HBM_PEAK_GBS, 4),
         "bucket_mix_rows_s": mix,
+        "padded_rows_s": round(B * args.steps / padded_s, 2),
         "relative_bias_gbs": round(kernels["relative_bias"]["gbs"], 1),
         "relative_bias_frac_hbm": round(kernels["relative_bias"]["gbs"] / HBM_PEAK_GBS, 4),
     }

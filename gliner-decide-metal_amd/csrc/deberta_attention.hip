@@ -127,8 +127,8 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K, const half_t* __restrict__ V, int qsb, int qsh,
     int qsl, int ksb, int ksh, int ksl, int vsb, int vsh, int vsl, const half_t* __restrict__ PK,
     const half_t* __restrict__ PQ, int pksh, int pksp, int pqsh, int pqsp, const half_t* __restrict__ mask,
-    int mask_kind, const int* __restrict__ row_len, int B, int H, int L, int P, int bucket_size, float scale_qk,
-    float scale16, half_t* __restrict__ out, int ldo) {
+    int mask_kind, const int* __restrict__ row_len, const int* __restrict__ row_off, int B, int H, int L, int P,
+    int bucket_size, float scale_qk, float scale16, half_t* __restrict__ out, int ldo) {
   // Two stage buffers and the per-wave scratch.  The stage DMA is inline
   // assembly the compiler does not track, so its reads of a stage never wait
   // for the next stage's loads in flight; the kernel orders them itself
@@ -210,8 +210,13 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   // `len` is the item's row extent: positions from len on take no part (keys
   // past it are neither read nor weighted, queries past it are not computed);
   // L without a row-extent array.  `klim` = max(len, 1) bounds row reads.
+  // `row0` is the token row of (b, 0) with packed rows (row_off[b]), else -1.
   struct Item {
-    int b, h, qt, len, klim;
+    int b, h, qt, len, klim, row0;
+  };
+  // Q / K / V of (b, h): row 0 of the batch row's slice.
+  auto slice_base = [&](const half_t* X, const int b, const int h, const int row0, int sb, int sh, int sl) {
+    return X + (row0 >= 0 ? (int64_t)row0 * sl : (int64_t)b * sb) + (int64_t)h * sh;
   };
   // Remap: item w + j gridDim.x (workgroup w on XCD w % 8, round j) becomes
   // local index l = w / 8 + j G (G = gridDim.x / 8) of XCD w % 8's contiguous
@@ -236,13 +241,14 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       len = __builtin_amdgcn_readfirstlane(row_len[b]);
       len = len < 0 ? 0 : (len > L ? L : len);
     }
+    const int row0 = row_off != nullptr ? __builtin_amdgcn_readfirstlane(row_off[b]) : -1;
     return Item{b, __builtin_amdgcn_readfirstlane(bh % H), __builtin_amdgcn_readfirstlane(bid % ntq), len,
-                len > 0 ? len : 1};
+                len > 0 ? len : 1, row0};
   };
   // Window start of chunk 0 per query tile (at most 4), lane qt of w0_tab.
   const int w0_tab = window_lo(kQT * (lane & 3), 0, rel_arith);
   auto stage0_of = [&](const Item& it, lds_half_t* st) {
-    issue_stage(st, K + (int64_t)it.b * ksb + (int64_t)it.h * ksh, PK + (int64_t)it.h * pksh,
+    issue_stage(st, slice_base(K, it.b, it.h, it.row0, ksb, ksh, ksl), PK + (int64_t)it.h * pksh,
                 PQ + (int64_t)it.h * pqsh, 0, __builtin_amdgcn_readlane(w0_tab, it.qt), it.klim);
   };
   // Per-thread set-up reads of an item: its key-mask entry, its lane of the
@@ -276,7 +282,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     else
       su.win_tab = window_lo(q0, kKC * (lane - 48), rel_lds);
     const int qr = qw + lc < it.klim ? qw + lc : it.klim - 1;
-    const half_t* qrow = Q + (int64_t)it.b * qsb + (int64_t)it.h * qsh + (int64_t)qr * qsl;
+    const half_t* qrow = slice_base(Q, it.b, it.h, it.row0, qsb, qsh, qsl) + (int64_t)qr * qsl;
     su.qf0 = *reinterpret_cast<const half8_t*>(qrow + 8 * g);
     su.qf1 = *reinterpret_cast<const half8_t*>(qrow + 32 + 8 * g);
     return su;
@@ -326,10 +332,10 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       const int nchunks = live ? (nt + 3) >> 2 : 1;
       const int klim = cur.klim;
       const bool active = qw < cur.len;
-      const half_t* Kb = K + (int64_t)b * ksb + (int64_t)h * ksh;
+      const half_t* Kb = slice_base(K, b, h, cur.row0, ksb, ksh, ksl);
       const half_t* PKh = PK + (int64_t)h * pksh;
       const half_t* PQh = PQ + (int64_t)h * pqsh;
-      const half_t* Vb = V + (int64_t)b * vsb + (int64_t)h * vsh;
+      const half_t* Vb = slice_base(V, b, h, cur.row0, vsb, vsh, vsl);
       const half8_t qf0 = cs.qf0, qf1 = cs.qf1;
       const int win_tab = cs.win_tab;
       auto win = [&](int j) -> int { return __builtin_amdgcn_readlane(win_tab, j); };
@@ -721,8 +727,11 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
 #pragma unroll
         for (int pass = 0; pass < 2; ++pass) {
           const int row = r + 8 * pass;
-          *reinterpret_cast<half8_t*>(out + ((int64_t)b * L + qw + row) * ldo + (int64_t)h * kD + cpos * 8) =
-              *reinterpret_cast<const half8_t*>(ot + row * 72 + cpos * 8);
+          // packed rows: rows past the extent belong to the next batch row
+          if (cur.row0 < 0 || qw + row < cur.len)
+            *reinterpret_cast<half8_t*>(out + ((cur.row0 >= 0 ? (int64_t)cur.row0 : (int64_t)b * L) + qw + row) * ldo +
+                                        (int64_t)h * kD + cpos * 8) =
+                *reinterpret_cast<const half8_t*>(ot + row * 72 + cpos * 8);
         }
       }
     }();
@@ -766,6 +775,7 @@ int launch2(const AttentionArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL((deberta_attention_kernel<MAXT, OUTK>), grid, block, 0, stream, hq, hk, hv, (int)a.qsb,     \
                      (int)a.qsh, (int)a.qsl, (int)a.ksb, (int)a.ksh, (int)a.ksl, (int)a.vsb, (int)a.vsh, (int)a.vsl, \
                      hpk, hpq, (int)a.pksh, (int)a.pksp, (int)a.pqsh, (int)a.pqsp, hm, a.mask_kind, a.row_len,      \
+                     a.row_off,                                                                                     \
                      (int)a.B,                                                                                      \
                      (int)a.H, (int)a.L, (int)a.P, a.bucket_size, a.scale_qk, a.scale16, ho, (int)a.ldo)
   switch (a.output) {
@@ -814,6 +824,33 @@ __global__ __launch_bounds__(256) void row_extent_kernel(const half_t* __restric
   }
 }
 
+// One workgroup per batch row b: its offset is the sum of the extents before
+// it (B is a batch size, so the O(B^2) reads are few).
+__global__ __launch_bounds__(256) void pack_rows_kernel(const int32_t* __restrict__ row_len, int B, int L,
+                                                        int64_t total, int32_t* __restrict__ row_off,
+                                                        int32_t* __restrict__ row_map,
+                                                        int32_t* __restrict__ error_flag) {
+  const int b = blockIdx.x;
+  int part = 0;
+  for (int i = threadIdx.x; i < b; i += 256) part += row_len[i];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off, 64);
+  __shared__ int wave_sum[4];
+  if ((threadIdx.x & 63) == 0) wave_sum[threadIdx.x >> 6] = part;
+  __syncthreads();
+  const int64_t off = (int64_t)wave_sum[0] + wave_sum[1] + wave_sum[2] + wave_sum[3];
+  const int len = row_len[b];
+  if (threadIdx.x == 0) {
+    row_off[b] = (int32_t)off;
+    if (b == B - 1) {
+      row_off[B] = (int32_t)(off + len);
+      if (off + len != total && error_flag) atomicOr(error_flag, 1);
+    }
+  }
+  for (int l = threadIdx.x; l < len; l += 256)
+    if (off + l < total) row_map[off + l] = b * L + l;
+}
+
 }  // namespace
 
 int launch_row_extent(const void* mask, const int32_t* markers, const float* marker_mask, int64_t B, int64_t L,
@@ -821,6 +858,15 @@ int launch_row_extent(const void* mask, const int32_t* markers, const float* mar
   if (B <= 0) return GD_OK;
   hipLaunchKernelGGL(row_extent_kernel, dim3((unsigned)B), dim3(256), 0, stream, static_cast<const half_t*>(mask),
                      markers, marker_mask, (int)L, (int)slots, out);
+  GD_LAUNCH_CHECK();
+  return GD_OK;
+}
+
+int launch_pack_rows(const int32_t* row_len, int64_t B, int64_t L, int64_t total, int32_t* row_off, int32_t* row_map,
+                     int32_t* error_flag, hipStream_t stream) {
+  if (B <= 0) return GD_OK;
+  hipLaunchKernelGGL(pack_rows_kernel, dim3((unsigned)B), dim3(256), 0, stream, row_len, (int)B, (int)L, total,
+                     row_off, row_map, error_flag);
   GD_LAUNCH_CHECK();
   return GD_OK;
 }
@@ -853,6 +899,8 @@ int launch_deberta_attention(const AttentionArgs& a, hipStream_t stream) {
   if (a.bucket_size != 256 || a.P != 512) return fail(GD_ERR_SHAPE, "attention: bucket size 256 and 512 positions");
   if (a.row_len != nullptr && a.output != GD_ATTN_OUT_CONTEXT)
     return fail(GD_ERR_INVALID_ARGUMENT, "attention: row extents apply to the context output only");
+  if (a.row_off != nullptr && a.row_len == nullptr)
+    return fail(GD_ERR_INVALID_ARGUMENT, "attention: packed rows need row extents");
   for (int64_t st : {a.qsb, a.qsh, a.qsl, a.ksb, a.ksh, a.ksl, a.vsb, a.vsh, a.vsl, a.pksh, a.pksp, a.pqsh, a.pqsp, a.ldo})
     if (st < 0 || st > INT32_MAX) return fail(GD_ERR_SHAPE, "attention: strides must lie in [0, 2^31)");
   GD_RETURN_IF_ERROR(ensure_relative_index_table(stream));

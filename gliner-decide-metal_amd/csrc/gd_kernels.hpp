@@ -11,9 +11,12 @@ namespace gd {
 int launch_residual_layer_norm(const void* x, const void* residual, const void* gamma, const void* beta, void* out,
                                int64_t rows, int64_t cols, float eps, uint32_t flags, hipStream_t stream);
 
+// row_map (optional, device int32 [tokens]): output row t embeds token
+// row_map[t] of ids / mask, which hold `sources` tokens (packed rows).
 int launch_embedding_layer_norm(const int32_t* ids, const void* mask, const void* table, const void* gamma,
                                 const void* beta, void* out, int64_t tokens, int64_t cols, int64_t vocab, float eps,
-                                int32_t* error_flag, hipStream_t stream);
+                                int32_t* error_flag, hipStream_t stream, const int32_t* row_map = nullptr,
+                                int64_t sources = 0);
 
 // Fills the per-device GELU table used by the GELU epilogue (first call per
 // device; refuses while `stream` is capturing a graph).
@@ -46,6 +49,10 @@ struct AttentionArgs {
   // are not read, queries at or past it are not computed (their output rows
   // hold copies or are left as they were).
   const int32_t* row_len = nullptr;
+  // Optional packed rows [B] (context output, with row_len): token (b, l) of
+  // Q, K, V and the output is row row_off[b] + l (the batch strides unused);
+  // output rows at or past row_len[b] are not written.
+  const int32_t* row_off = nullptr;
 };
 
 int launch_deberta_attention(const AttentionArgs& args, hipStream_t stream);
@@ -55,6 +62,12 @@ int launch_deberta_attention(const AttentionArgs& args, hipStream_t stream);
 // (position 0 for an out-of-range index)) + 1, or 0.
 int launch_row_extent(const void* mask, const int32_t* markers, const float* marker_mask, int64_t B, int64_t L,
                       int64_t slots, int32_t* out, hipStream_t stream);
+
+// Packed rows from the extents: row_off[b] = sum of row_len[0, b) (B + 1
+// entries) and row_map[row_off[b] + l] = b * L + l for l < row_len[b], for
+// packed rows below `total`; a sum other than `total` raises the error flag.
+int launch_pack_rows(const int32_t* row_len, int64_t B, int64_t L, int64_t total, int32_t* row_off,
+                     int32_t* row_map, int32_t* error_flag, hipStream_t stream);
 
 int launch_relative_bias_general(const void* q, const void* k, const void* pos_key, const void* pos_query,
                                  const int32_t* c2p, const int32_t* p2c, const void* key_mask, float scale, int64_t B,
@@ -69,8 +82,11 @@ int launch_fused_attention_general(const void* q, const void* k, const void* v, 
 int launch_relative_index_table(int32_t* out, int n, int bucket_size, int max_position, hipStream_t stream);
 
 // Classifier head helpers (head.hip).
+// rows_out[b, s] = token row of marker s of batch row b: b * seq_len +
+// position, or row_off[b] + position with packed rows (row_off optional).
 int launch_marker_rows(const int32_t* marker_indices, int32_t* rows_out, int64_t batch, int64_t seq_len,
-                       int64_t markers_per_row, int32_t* error_flag, hipStream_t stream);
+                       int64_t markers_per_row, int32_t* error_flag, hipStream_t stream,
+                       const int32_t* row_off = nullptr);
 int launch_head_output(const void* inner, const void* w2, const void* b2, const float* marker_mask, void* logits,
                        int64_t rows, int64_t width, hipStream_t stream);
 

@@ -21,6 +21,7 @@
 //   * workgroups are dispatched round-robin over the 8 XCDs; the tile order is
 //     remapped so each XCD works on a compact 4-tile-row band and its private
 //     L2 serves the A rows and W columns it shares.
+#include <atomic>
 #include <cmath>
 #include <cstring>
 #include <mutex>
@@ -631,6 +632,21 @@ int ensure_gelu_table(hipStream_t stream) {
   return GD_OK;
 }
 
+namespace {
+// Compute units of the current device (cached per device).
+int64_t gemm_cu_count() {
+  static std::atomic<int> cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+}  // namespace
+
 int launch_linear(const void* a, const void* w, const void* bias, void* c, int64_t m, int64_t n, int64_t k, int64_t lda,
                   int64_t ldc, const int32_t* a_rows, int64_t a_row_count, int epilogue_kind, hipStream_t stream) {
   if (m == 0) return GD_OK;
@@ -647,16 +663,23 @@ int launch_linear(const void* a, const void* w, const void* bias, void* c, int64
     return launch_tile<64, 128, true>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
   }
   if (M >= 2048) {
-    // 256 x 256 tiles (two 64-deep stages, 128 KiB of LDS) when they fill
-    // whole waves of the 256 CUs; else 256 x 192 (two stages, 112 KiB) when
-    // those do (the fused QKV projection, N = 3072); else 256 x 128 (three
-    // stages, 144 KiB).
-    const int tiles_m = (M + 255) / 256;
-    const int t256 = tiles_m * (N / 256);
-    if (N % 256 == 0 && (t256 % 256 == 0 || t256 >= 512))
-      return launch_lds_tile<256, 256, 2, 64, 2>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
-    if (N % 192 == 0 && (tiles_m * (N / 192)) % 256 == 0)
-      return launch_lds_tile<256, 192, 4, 64, 2>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
+    // 256-row tiles: 256 x 256 (two 64-deep stages, 128 KiB of LDS), 256 x 192
+    // (two stages, 112 KiB) or 256 x 128 (three stages, 144 KiB), whichever
+    // finishes first: rounds of one tile per CU, each costing the tile's
+    // measured time relative to a 256 x 128 tile (1.9, 1.35, 1; K = 1024 and
+    // 4096 alike).  Ties keep the larger tile.
+    const int64_t tiles_m = (M + 255) / 256;
+    const int64_t cus = gemm_cu_count();
+    auto rounds = [&](int bn) { return (double)((tiles_m * (N / bn) + cus - 1) / cus); };
+    int bn = 128;
+    double best = rounds(128);
+    if (N % 192 == 0 && rounds(192) * 1.35 <= best) {
+      bn = 192;
+      best = rounds(192) * 1.35;
+    }
+    if (N % 256 == 0 && rounds(256) * 1.9 <= best) bn = 256;
+    if (bn == 256) return launch_lds_tile<256, 256, 2, 64, 2>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
+    if (bn == 192) return launch_lds_tile<256, 192, 4, 64, 2>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
     return launch_lds_tile<256, 128, 4, 64, 3>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
   }
   if (M >= 1024) return launch_tile<128, 128, false>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);

@@ -14,7 +14,7 @@ namespace {
 
 __global__ void marker_rows_kernel(const int32_t* __restrict__ marker_indices, int32_t* __restrict__ rows_out,
                                    int64_t total, int64_t seq_len, int64_t markers_per_row,
-                                   int32_t* __restrict__ error_flag) {
+                                   int32_t* __restrict__ error_flag, const int32_t* __restrict__ row_off) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= total) return;
   const int64_t b = i / markers_per_row;
@@ -23,7 +23,7 @@ __global__ void marker_rows_kernel(const int32_t* __restrict__ marker_indices, i
     if (error_flag) atomicOr(error_flag, 1);
     m = 0;
   }
-  rows_out[i] = (int32_t)(b * seq_len + m);
+  rows_out[i] = (int32_t)((row_off ? (int64_t)row_off[b] : b * seq_len) + m);
 }
 
 // One wave per marker row: v = fp16(inner[row] . w2 + b2);
@@ -53,11 +53,11 @@ __global__ __launch_bounds__(256) void head_output_kernel(const half_t* __restri
 }  // namespace
 
 int launch_marker_rows(const int32_t* marker_indices, int32_t* rows_out, int64_t batch, int64_t seq_len,
-                       int64_t markers_per_row, int32_t* error_flag, hipStream_t stream) {
+                       int64_t markers_per_row, int32_t* error_flag, hipStream_t stream, const int32_t* row_off) {
   const int64_t total = batch * markers_per_row;
   if (total == 0) return GD_OK;
   hipLaunchKernelGGL(marker_rows_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, marker_indices,
-                     rows_out, total, seq_len, markers_per_row, error_flag);
+                     rows_out, total, seq_len, markers_per_row, error_flag, row_off);
   GD_LAUNCH_CHECK();
   return GD_OK;
 }

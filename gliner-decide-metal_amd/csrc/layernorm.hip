@@ -151,6 +151,20 @@ __global__ __launch_bounds__(256) void residual_ln_generic_kernel(const half_t* 
   }
 }
 
+// Output row t of the embedding reads token row_map[t] of ids / mask (packed
+// rows), or token t without a map; a map entry outside [0, sources) reads
+// token 0 and raises the error flag.
+__device__ __forceinline__ int64_t source_row(const int32_t* __restrict__ row_map, int64_t t, int64_t sources,
+                                              int32_t* __restrict__ error_flag, int lane) {
+  if (row_map == nullptr) return t;
+  int64_t s = row_map[t];
+  if (s < 0 || s >= sources) {
+    if (error_flag && lane == 0) atomicOr(error_flag, 1);
+    s = 0;
+  }
+  return s;
+}
+
 template <int VPL>
 __global__ __launch_bounds__(256) void embedding_ln_kernel(const int32_t* __restrict__ ids,
                                                            const half_t* __restrict__ mask,
@@ -158,18 +172,20 @@ __global__ __launch_bounds__(256) void embedding_ln_kernel(const int32_t* __rest
                                                            const half_t* __restrict__ gamma,
                                                            const half_t* __restrict__ beta, half_t* __restrict__ out,
                                                            int64_t tokens, int64_t vocab, float eps,
-                                                           int32_t* __restrict__ error_flag) {
+                                                           int32_t* __restrict__ error_flag,
+                                                           const int32_t* __restrict__ row_map, int64_t sources) {
   const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (t >= tokens) return;
-  int64_t id = ids[t];
+  const int64_t src = source_row(row_map, t, sources, error_flag, lane);
+  int64_t id = ids[src];
   if (id < 0 || id >= vocab) {
     if (error_flag && lane == 0) atomicOr(error_flag, 1);
     id = 0;
   }
   RowVec<VPL> r;
   const float sum = load_row_sum<VPL>(table, nullptr, id, lane, false, r);
-  const float m = (float)mask[t];
+  const float m = (float)mask[src];
   // out = fp16(fp16(LN) * fp16(mask)); for the usual 0/1 mask this is LN or 0.
   normalize_store<VPL>(r, sum, gamma, beta, out, t, lane, eps, m);
 }
@@ -181,11 +197,14 @@ __global__ __launch_bounds__(256) void embedding_ln_generic_kernel(const int32_t
                                                                    const half_t* __restrict__ beta,
                                                                    half_t* __restrict__ out, int64_t tokens,
                                                                    int64_t cols, int64_t vocab, float eps,
-                                                                   int32_t* __restrict__ error_flag) {
+                                                                   int32_t* __restrict__ error_flag,
+                                                                   const int32_t* __restrict__ row_map,
+                                                                   int64_t sources) {
   const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (t >= tokens) return;
-  int64_t id = ids[t];
+  const int64_t src = source_row(row_map, t, sources, error_flag, lane);
+  int64_t id = ids[src];
   if (id < 0 || id >= vocab) {
     if (error_flag && lane == 0) atomicOr(error_flag, 1);
     id = 0;
@@ -200,7 +219,7 @@ __global__ __launch_bounds__(256) void embedding_ln_generic_kernel(const int32_t
     sq += d * d;
   }
   const float inv = 1.0f / sqrtf(wave_sum(sq) / (float)cols + eps);
-  const float m = (float)mask[t];
+  const float m = (float)mask[src];
   half_t* orow = out + t * cols;
   for (int64_t j = lane; j < cols; j += 64) {
     const float y = ((float)xr[j] - mean) * inv * (float)gamma[j] + (float)beta[j];
@@ -240,7 +259,7 @@ int launch_residual_layer_norm(const void* x, const void* residual, const void* 
 
 int launch_embedding_layer_norm(const int32_t* ids, const void* mask, const void* table, const void* gamma,
                                 const void* beta, void* out, int64_t tokens, int64_t cols, int64_t vocab, float eps,
-                                int32_t* error_flag, hipStream_t stream) {
+                                int32_t* error_flag, hipStream_t stream, const int32_t* row_map, int64_t sources) {
   if (tokens == 0) return GD_OK;
   const dim3 block(256);
   const dim3 grid((unsigned)((tokens + kRowsPerBlock - 1) / kRowsPerBlock));
@@ -252,10 +271,10 @@ int launch_embedding_layer_norm(const int32_t* ids, const void* mask, const void
   const bool vec_ok = aligned16(table) && aligned16(gamma) && aligned16(beta) && aligned16(out);
   if (vec_ok && cols == 1024) {
     hipLaunchKernelGGL(embedding_ln_kernel<2>, grid, block, 0, stream, ids, M, T, G, Bt, O, tokens, vocab, eps,
-                       error_flag);
+                       error_flag, row_map, sources);
   } else {
     hipLaunchKernelGGL(embedding_ln_generic_kernel, grid, block, 0, stream, ids, M, T, G, Bt, O, tokens, cols, vocab,
-                       eps, error_flag);
+                       eps, error_flag, row_map, sources);
   }
   GD_LAUNCH_CHECK();
   return GD_OK;

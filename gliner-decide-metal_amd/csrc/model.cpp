@@ -261,6 +261,8 @@ int Classifier::reserve(int64_t B, int64_t L, int64_t Hh, int64_t O) {
   GD_RETURN_IF_ERROR(A((size_t)nm * 4, &ws_.marker_mask));
   GD_RETURN_IF_ERROR(A((size_t)nm * 2, &ws_.logits));
   GD_RETURN_IF_ERROR(A((size_t)nt * 4, &ws_.row_len));  // B <= B * L
+  GD_RETURN_IF_ERROR(A((size_t)(nt + 1) * 4, &ws_.row_off));
+  GD_RETURN_IF_ERROR(A((size_t)nt * 4, &ws_.row_map));
   ws_bytes_ = device_bytes_ - before;
   ws_tokens_ = nt;
   ws_markers_ = nm;
@@ -269,10 +271,10 @@ int Classifier::reserve(int64_t B, int64_t L, int64_t Hh, int64_t O) {
 
 // One encoder layer (DeBERTa.swift:296-428).
 int Classifier::layer_forward(int li, const void* mask, int64_t B, int64_t L, hipStream_t stream, StageHook* hook,
-                              const int32_t* row_len) {
+                              const Rows& rows) {
   const Layer& Ly = layers_[li];
   const int64_t C = cfg_.hidden_size, F = cfg_.intermediate_size, H = cfg_.num_attention_heads, D = C / H;
-  const int64_t T = B * L;
+  const int64_t T = rows.tokens >= 0 ? rows.tokens : B * L;
   const float eps = cfg_.layer_norm_eps;
   const uint32_t ln_flags = (flags_ & GD_USE_FUSED_KERNELS) ? 0u : GD_LN_SUM_F16;
   char name[48];
@@ -312,7 +314,8 @@ int Classifier::layer_forward(int li, const void* mask, int64_t B, int64_t L, hi
   a.output = GD_ATTN_OUT_CONTEXT;
   a.out = ws_.ctx;
   a.ldo = C;
-  a.row_len = row_len;
+  a.row_len = rows.len;
+  a.row_off = rows.off;
   GD_RETURN_IF_ERROR(launch_deberta_attention(a, stream));
   if (hook) {
     std::snprintf(name, sizeof name, "layer_%d_attention", li);
@@ -344,48 +347,60 @@ int Classifier::layer_forward(int li, const void* mask, int64_t B, int64_t L, hi
 }
 
 int Classifier::encode_into_workspace(const int32_t* ids, const void* mask, int64_t B, int64_t L, int num_layers,
-                                      hipStream_t stream, StageHook* hook, const int32_t* row_len) {
-  const int64_t T = B * L;
+                                      hipStream_t stream, StageHook* hook, const Rows& rows) {
+  const int64_t T = rows.tokens >= 0 ? rows.tokens : B * L;
   if (hook) hook->begin(stream);
   GD_RETURN_IF_ERROR(launch_embedding_layer_norm(ids, mask, word_emb_, emb_g_, emb_b_, ws_.hidden, T,
                                                  cfg_.hidden_size, cfg_.vocab_size, cfg_.layer_norm_eps, err_flag_,
-                                                 stream));
+                                                 stream, rows.map, B * L));
   if (hook) hook->end("embedding", stream);
-  for (int i = 0; i < num_layers; ++i) GD_RETURN_IF_ERROR(layer_forward(i, mask, B, L, stream, hook, row_len));
+  for (int i = 0; i < num_layers; ++i) GD_RETURN_IF_ERROR(layer_forward(i, mask, B, L, stream, hook, rows));
   return GD_OK;
 }
 
 int Classifier::forward(const int32_t* ids, const void* mask, const int32_t* markers, const float* marker_mask,
                         int64_t B, int64_t L, int64_t Hh, int64_t O, void* logits, hipStream_t stream,
-                        StageHook* hook) {
+                        StageHook* hook, int64_t packed_tokens) {
   const int64_t C = cfg_.hidden_size, CH = cfg_.classifier_hidden;
   const int64_t M = B * Hh * O;
   // Each row's attention stops at its extent (unless GD_FULL_ROWS): every
   // position the classifier reads lies before it, and positions past it are
-  // masked keys that feed nothing before it.
-  const int32_t* row_len = nullptr;
-  if (!(flags_ & GD_FULL_ROWS)) {
-    row_len = static_cast<const int32_t*>(ws_.row_len);
+  // masked keys that feed nothing before it.  Packed, every kernel runs on
+  // the extents' tokens only, batch row after batch row.
+  const bool packed = packed_tokens >= 0;
+  Rows rows;
+  if (packed || !(flags_ & GD_FULL_ROWS)) {
+    rows.len = static_cast<const int32_t*>(ws_.row_len);
     GD_RETURN_IF_ERROR(launch_row_extent(mask, markers, marker_mask, B, L, Hh * O, static_cast<int32_t*>(ws_.row_len),
                                          stream));
   }
-  GD_RETURN_IF_ERROR(encode_into_workspace(ids, mask, B, L, cfg_.num_hidden_layers, stream, hook, row_len));
+  if (packed) {
+    rows.off = static_cast<const int32_t*>(ws_.row_off);
+    rows.map = static_cast<const int32_t*>(ws_.row_map);
+    rows.tokens = packed_tokens;
+    GD_RETURN_IF_ERROR(launch_pack_rows(rows.len, B, L, packed_tokens, static_cast<int32_t*>(ws_.row_off),
+                                        static_cast<int32_t*>(ws_.row_map), err_flag_, stream));
+  }
+  const int64_t T = packed ? packed_tokens : B * L;
+  GD_RETURN_IF_ERROR(encode_into_workspace(ids, mask, B, L, cfg_.num_hidden_layers, stream, hook, rows));
   // classifier (:430-444)
   if (hook) hook->begin(stream);
   GD_RETURN_IF_ERROR(launch_marker_rows(markers, static_cast<int32_t*>(ws_.marker_rows), B, L, Hh * O, err_flag_,
-                                        stream));
+                                        stream, rows.off));
   GD_RETURN_IF_ERROR(launch_linear(ws_.hidden, cls0_w_, cls0_b_, ws_.inner, M, CH, C, C, CH,
-                                   static_cast<const int32_t*>(ws_.marker_rows), B * L, GD_EPI_BIAS_RELU, stream));
+                                   static_cast<const int32_t*>(ws_.marker_rows), T > 0 ? T : 1, GD_EPI_BIAS_RELU,
+                                   stream));
   GD_RETURN_IF_ERROR(launch_head_output(ws_.inner, cls2_w_, cls2_b_, marker_mask, logits, M, CH, stream));
   if (hook) hook->end("classifier", stream);
   return GD_OK;
 }
 
 int Classifier::classify(const int32_t* ids, const void* mask, const int32_t* markers, const float* marker_mask,
-                         int64_t B, int64_t L, int64_t Hh, int64_t O, void* logits, hipStream_t stream) {
+                         int64_t B, int64_t L, int64_t Hh, int64_t O, void* logits, hipStream_t stream,
+                         int64_t packed_tokens) {
   GD_RETURN_IF_ERROR(reserve(B, L, Hh, O));
   if (!(flags_ & GD_USE_COMPILED_GRAPH))
-    return forward(ids, mask, markers, marker_mask, B, L, Hh, O, logits, stream, nullptr);
+    return forward(ids, mask, markers, marker_mask, B, L, Hh, O, logits, stream, nullptr, packed_tokens);
 
   // Compiled path (MLX compile, DeBERTa.swift:175-186, 249-261): the forward
   // for one shape is captured once into a hipGraph over the context's staging
@@ -396,7 +411,7 @@ int Classifier::classify(const int32_t* ids, const void* mask, const int32_t* ma
   GD_HIP_CHECK(hipMemcpyAsync(ws_.mask, mask, (size_t)T * 2, hipMemcpyDeviceToDevice, stream));
   GD_HIP_CHECK(hipMemcpyAsync(ws_.markers, markers, (size_t)M * 4, hipMemcpyDeviceToDevice, stream));
   GD_HIP_CHECK(hipMemcpyAsync(ws_.marker_mask, marker_mask, (size_t)M * 4, hipMemcpyDeviceToDevice, stream));
-  const ShapeKey key{B, L, Hh, O};
+  const ShapeKey key{B, L, Hh, O, packed_tokens};
   auto it = graphs_.find(key);
   if (it == graphs_.end()) {
     GraphEntry ge;
@@ -406,7 +421,8 @@ int Classifier::classify(const int32_t* ids, const void* mask, const int32_t* ma
     if (!capture_stream_) GD_HIP_CHECK(hipStreamCreateWithFlags(&capture_stream_, hipStreamNonBlocking));
     GD_HIP_CHECK(hipStreamBeginCapture(capture_stream_, hipStreamCaptureModeThreadLocal));
     int st = forward(static_cast<const int32_t*>(ws_.ids), ws_.mask, static_cast<const int32_t*>(ws_.markers),
-                     static_cast<const float*>(ws_.marker_mask), B, L, Hh, O, ws_.logits, capture_stream_, nullptr);
+                     static_cast<const float*>(ws_.marker_mask), B, L, Hh, O, ws_.logits, capture_stream_, nullptr,
+                     packed_tokens);
     hipGraph_t graph = nullptr;
     hipError_t e = hipStreamEndCapture(capture_stream_, &graph);
     (void)hipGetLastError();
@@ -436,7 +452,7 @@ int Classifier::encode(const int32_t* ids, const void* mask, int64_t B, int64_t 
                        hipStream_t stream) {
   GD_RETURN_IF_ERROR(reserve(B, L, 1, 1));
   const int n = num_layers < 0 ? cfg_.num_hidden_layers : std::min(num_layers, cfg_.num_hidden_layers);
-  GD_RETURN_IF_ERROR(encode_into_workspace(ids, mask, B, L, n, stream, nullptr));
+  GD_RETURN_IF_ERROR(encode_into_workspace(ids, mask, B, L, n, stream, nullptr, Rows{}));
   GD_HIP_CHECK(hipMemcpyAsync(hidden_out, ws_.hidden, (size_t)B * L * cfg_.hidden_size * 2, hipMemcpyDeviceToDevice,
                               stream));
   return GD_OK;
@@ -448,7 +464,7 @@ int Classifier::layer(int li, const void* hidden_in, const void* mask, int64_t B
   GD_RETURN_IF_ERROR(reserve(B, L, 1, 1));
   const size_t bytes = (size_t)B * L * cfg_.hidden_size * 2;
   GD_HIP_CHECK(hipMemcpyAsync(ws_.hidden, hidden_in, bytes, hipMemcpyDeviceToDevice, stream));
-  GD_RETURN_IF_ERROR(layer_forward(li, mask, B, L, stream, nullptr));
+  GD_RETURN_IF_ERROR(layer_forward(li, mask, B, L, stream, nullptr, Rows{}));
   GD_HIP_CHECK(hipMemcpyAsync(hidden_out, ws_.hidden, bytes, hipMemcpyDeviceToDevice, stream));
   return GD_OK;
 }

@@ -31,8 +31,10 @@ class Classifier {
   ~Classifier();
   int init(const WeightStore& store, const gd_config& cfg, uint32_t flags, hipStream_t stream);
   int reserve(int64_t B, int64_t L, int64_t Hh, int64_t O);
+  // packed_tokens >= 0: the forward runs on packed rows (the sum of the row
+  // extents, which it must equal); -1: every row is B x L tokens.
   int classify(const int32_t* ids, const void* mask, const int32_t* markers, const float* marker_mask, int64_t B,
-               int64_t L, int64_t Hh, int64_t O, void* logits, hipStream_t stream);
+               int64_t L, int64_t Hh, int64_t O, void* logits, hipStream_t stream, int64_t packed_tokens = -1);
   int classify_profiled(const int32_t* ids, const void* mask, const int32_t* markers, const float* marker_mask,
                         int64_t B, int64_t L, int64_t Hh, int64_t O, void* logits, gd_profile_event* events,
                         int capacity, int* count, hipStream_t stream);
@@ -55,9 +57,11 @@ class Classifier {
     void *hidden = nullptr, *qkv = nullptr, *ctx = nullptr, *tmp = nullptr, *ffn = nullptr;
     void *marker_rows = nullptr, *inner = nullptr;
     void* row_len = nullptr;  // int32 [B]: per-row attention extents of classify
+    void* row_off = nullptr;  // int32 [B + 1]: packed rows: first token row of each batch row
+    void* row_map = nullptr;  // int32 [T]: packed rows: token index b * L + l of each packed row
     void *ids = nullptr, *mask = nullptr, *markers = nullptr, *marker_mask = nullptr, *logits = nullptr;
   };
-  using ShapeKey = std::tuple<int64_t, int64_t, int64_t, int64_t>;
+  using ShapeKey = std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t>;  // B, L, Hh, O, packed tokens
   struct GraphEntry {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
@@ -68,12 +72,21 @@ class Classifier {
              hipStream_t stream);
   int upload_concat(const WeightStore& store, const std::vector<std::string>& keys,
                     const std::vector<std::vector<int64_t>>& shapes, void** out, hipStream_t stream);
+  // Rows: every (b, l) without `rows`; with it, the row extents and (packed)
+  // the offsets, the row map and the token count.
+  struct Rows {
+    const int32_t* len = nullptr;
+    const int32_t* off = nullptr;
+    const int32_t* map = nullptr;
+    int64_t tokens = -1;
+  };
   int layer_forward(int li, const void* mask, int64_t B, int64_t L, hipStream_t stream, StageHook* hook,
-                    const int32_t* row_len = nullptr);
+                    const Rows& rows);
   int encode_into_workspace(const int32_t* ids, const void* mask, int64_t B, int64_t L, int num_layers,
-                            hipStream_t stream, StageHook* hook, const int32_t* row_len = nullptr);
+                            hipStream_t stream, StageHook* hook, const Rows& rows);
   int forward(const int32_t* ids, const void* mask, const int32_t* markers, const float* marker_mask, int64_t B,
-              int64_t L, int64_t Hh, int64_t O, void* logits, hipStream_t stream, StageHook* hook);
+              int64_t L, int64_t Hh, int64_t O, void* logits, hipStream_t stream, StageHook* hook,
+              int64_t packed_tokens = -1);
   void release_graphs();
 
   gd_config cfg_{};

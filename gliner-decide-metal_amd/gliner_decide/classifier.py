@@ -17,6 +17,7 @@ import torch
 
 from . import _native as N
 from .config import DeBERTaV2Configuration
+from .decode import row_extents
 from .device import require_gpu, stream_handle
 from .weights import WeightStore
 
@@ -126,6 +127,7 @@ class GLiNERDecideClassifier:
         self._h = h
         self.use_fused_kernels = use_fused_kernels
         self.use_compiled_graph = use_compiled_graph
+        self.full_rows = full_rows
 
     @property
     def device_bytes(self) -> int:
@@ -135,21 +137,33 @@ class GLiNERDecideClassifier:
         N.check(self._lib.gd_classifier_reserve(self._h, batch, seq_len, max_heads, max_options))
 
     def classify_device(self, ids: torch.Tensor, mask: torch.Tensor, markers: torch.Tensor, marker_mask: torch.Tensor,
-                        out: torch.Tensor | None = None) -> torch.Tensor:
+                        out: torch.Tensor | None = None, total_tokens: int | None = None) -> torch.Tensor:
         """Enqueues the forward on the current stream; inputs already on the GPU
-        with the library dtypes (int32, fp16, int32, fp32).  No sync."""
+        with the library dtypes (int32, fp16, int32, fp32).  No sync.  With
+        total_tokens (the sum of `row_extents`) the forward runs on packed
+        rows (gd_classifier_classify_packed)."""
         B, L = ids.shape
         _, Hh, O = markers.shape
         if out is None:
             out = torch.empty((B, Hh, O), dtype=torch.float16, device=ids.device)
-        N.check(self._lib.gd_classifier_classify(self._h, ids.data_ptr(), mask.data_ptr(), markers.data_ptr(),
-                                                 marker_mask.data_ptr(), B, L, Hh, O, out.data_ptr(),
-                                                 stream_handle()))
+        if total_tokens is None:
+            N.check(self._lib.gd_classifier_classify(self._h, ids.data_ptr(), mask.data_ptr(), markers.data_ptr(),
+                                                     marker_mask.data_ptr(), B, L, Hh, O, out.data_ptr(),
+                                                     stream_handle()))
+        else:
+            N.check(self._lib.gd_classifier_classify_packed(self._h, ids.data_ptr(), mask.data_ptr(),
+                                                            markers.data_ptr(), marker_mask.data_ptr(), B, L, Hh, O,
+                                                            int(total_tokens), out.data_ptr(), stream_handle()))
         return out
 
     def classify(self, inp: DecisionInput, collect_profile: bool = False) -> InferenceResult:
         """`classify(_:collectProfile:)` (DeBERTa.swift:244-272): runs the
-        forward and synchronises (MLX `eval`)."""
+        forward and synchronises (MLX `eval`).  Host-array inputs run on packed
+        rows (their extents are known on the host) unless full_rows was set;
+        tensors already on the GPU run padded."""
+        total = None
+        if not self.full_rows and not collect_profile and not isinstance(inp.attention_mask, torch.Tensor):
+            total = int(row_extents(inp.attention_mask, inp.marker_indices, inp.marker_mask).sum())
         ids, mask, markers, mmask = inp.to_device()
         B, L, Hh, O = inp.shape
         out = torch.empty((B, Hh, O), dtype=torch.float16, device=ids.device)
@@ -164,7 +178,7 @@ class GLiNERDecideClassifier:
                                                               out.data_ptr(), arr, cap, C.byref(n), stream_handle()))
             events = [ProfileEvent(arr[i].name.decode(), int(arr[i].milliseconds * 1e6)) for i in range(n.value)]
         else:
-            self.classify_device(ids, mask, markers, mmask, out)
+            self.classify_device(ids, mask, markers, mmask, out, total_tokens=total)
         torch.cuda.current_stream().synchronize()
         return InferenceResult(out, time.perf_counter_ns() - start, events)
 

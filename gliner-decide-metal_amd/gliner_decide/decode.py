@@ -124,6 +124,23 @@ def make_batch_chunk(arrays: dict, start: int, end: int, pad_to: int):
     return {k: np.concatenate([v, np.repeat(v[valid - 1:valid], pad, axis=0)], axis=0) for k, v in chunk.items()}, valid
 
 
+def row_extents(attention_mask, marker_indices, marker_mask) -> np.ndarray:
+    """Per-row extents [B] (int64): the larger of (last l with
+    attention_mask[b, l] > 0) + 1 and (last position read by a marker slot of
+    row b with marker_mask > 0) + 1, where a marker outside [0, L) reads
+    position 0; 0 for a row with neither.  Every position the classifier reads
+    lies before the extent; its sum is the token count of packed rows."""
+    mask = np.asarray(attention_mask, dtype=np.float32)
+    B, L = mask.shape
+    valid = mask > 0
+    last = np.where(valid.any(axis=1), L - np.argmax(valid[:, ::-1], axis=1), 0)
+    mi = np.asarray(marker_indices).reshape(B, -1).astype(np.int64)
+    mm = np.asarray(marker_mask, dtype=np.float32).reshape(B, -1) > 0
+    pos = np.where((mi >= 0) & (mi < L), mi + 1, 1)
+    mark = np.where(mm, pos, 0).max(axis=1, initial=0)
+    return np.maximum(last, mark).astype(np.int64)
+
+
 def group_by_shape(items, key=lambda x: x):
     """RawCLI.swift:135-139: group requests by (L, Hh, O); insertion order."""
     groups: dict = {}

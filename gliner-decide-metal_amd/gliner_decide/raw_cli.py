@@ -30,7 +30,7 @@ from pathlib import Path
 
 import numpy as np
 
-from .decode import DEFAULT_BUCKETS, decode
+from .decode import DEFAULT_BUCKETS, decode, row_extents
 from .frontend import NativeDecisionTokenizer, tasks_from_json
 
 
@@ -155,8 +155,11 @@ class _DeviceBatches:
         out = torch.empty((B, Hh, O), dtype=torch.float16, device=self.device)
         host = torch.empty((B, Hh, O), dtype=torch.float16, pin_memory=True)
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)] + [torch.cuda.Event()]
+        total = None
+        if not getattr(self.model, "full_rows", False):
+            total = int(row_extents(inp.attention_mask, inp.marker_indices, inp.marker_mask).sum())
         ev[0].record()
-        self.model.classify_device(*up, out)
+        self.model.classify_device(*up, out, total_tokens=total)
         ev[1].record()
         host.copy_(out, non_blocking=True)
         ev[2].record()

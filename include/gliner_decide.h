@@ -272,6 +272,23 @@ int gd_classifier_classify(gd_classifier* model, const int32_t* input_ids, const
                            int64_t seq_len, int64_t max_heads, int64_t max_options, void* logits_out,
                            void* stream);
 
+/* classify on packed rows.  No counterpart in the reference (it pads every
+ * row to the bucket); the logits are those of gd_classifier_classify.  Row b's
+ * extent is the larger of (last l with attention_mask[b, l] > 0) + 1 and
+ * (last position read by a marker slot of row b with marker_mask > 0) + 1 (an
+ * out-of-range marker reads position 0); only the extents' tokens run through
+ * the embedding, the GEMMs and the LayerNorms, batch row after batch row.
+ * total_tokens must equal the sum of the extents (0 <= total_tokens <= B * L):
+ * the caller's tokenizer knows it; a different value sets the device error
+ * flag (gd_classifier_check_device_errors reports GD_ERR_DEVICE_INDEX) and
+ * leaves the logits undefined.  Same shapes and rules as gd_classifier_classify
+ * otherwise; with GD_USE_COMPILED_GRAPH each (shape, total_tokens) is
+ * captured once. */
+int gd_classifier_classify_packed(gd_classifier* model, const int32_t* input_ids, const void* attention_mask,
+                                  const int32_t* marker_indices, const float* marker_mask, int64_t batch,
+                                  int64_t seq_len, int64_t max_heads, int64_t max_options, int64_t total_tokens,
+                                  void* logits_out, void* stream);
+
 /* Encoder only: writes the final hidden states [B, L, hidden] fp16 after
  * `num_layers` layers (num_layers < 0 = all). */
 int gd_classifier_encode(gd_classifier* model, const int32_t* input_ids, const void* attention_mask,

@@ -79,24 +79,13 @@ def test_encoder_and_logits_small_model_padded():
     assert np.max(np.abs(got_logits - want_logits)) <= 2e-3
 
 
-@pytest.mark.parametrize("L", [128, 256, 512])
-def test_row_extents_leave_logits_unchanged(L):
-    """classify stops each row's attention at its extent (last unmasked or
-    marker-read position + 1); the logits must equal those of the full
-    computation (GD_FULL_ROWS) bit for bit: rows of different lengths, a
-    marker past the last unmasked token, an all-masked row, a mask with holes,
-    a one-token row, and a masked marker slot pointing past the extent."""
-    from gliner_decide import DecisionInput, GLiNERDecideClassifier
-    from gliner_decide.config import DeBERTaV2Configuration
-    from gliner_decide.synthetic import synthetic_weights
-    pc = DeBERTaV2Configuration(num_hidden_layers=2, vocab_size=3000)
-    w = synthetic_weights(pc, seed=13)
-    fast = GLiNERDecideClassifier(w, pc)
-    full = GLiNERDecideClassifier(w, pc, full_rows=True)
-    r = np.random.default_rng(L)
-    B = 6
+def _extent_batch(L, seed, B=6):
+    """Rows of different lengths, a marker past the row's last unmasked
+    token, an all-masked row, a mask with holes, a one-token row, and a
+    masked marker slot pointing past the extent."""
+    r = np.random.default_rng(seed)
     ids = r.integers(1000, 3000, size=(B, L)).astype(np.int32)
-    lengths = np.array([L, 40, 17, 0, L // 2 + 3, 1])
+    lengths = np.array([L, 40, 17, 0, L // 2 + 3, 1])[:B]
     mask = (np.arange(L)[None] < lengths[:, None]).astype(np.float16)
     mask[4, 20:30] = 0  # holes
     ids[mask == 0] = 0
@@ -109,11 +98,70 @@ def test_row_extents_leave_logits_unchanged(L):
     mi[2, 1, 2] = L - 7  # a marker past the row's last unmasked token
     mi[1, 0, 1], mm[1, 0, 1] = L - 1, 0  # masked slot: does not extend the row
     mm[5, 1] = 0
+    return ids, mask, mi, mm
+
+
+def _small_pair(seed=13, **flags):
+    from gliner_decide import GLiNERDecideClassifier
+    from gliner_decide.config import DeBERTaV2Configuration
+    from gliner_decide.synthetic import synthetic_weights
+    pc = DeBERTaV2Configuration(num_hidden_layers=2, vocab_size=3000)
+    w = synthetic_weights(pc, seed=seed)
+    return GLiNERDecideClassifier(w, pc, **flags), GLiNERDecideClassifier(w, pc, full_rows=True), w, pc
+
+
+@pytest.mark.parametrize("L", [128, 256, 512])
+def test_row_extents_leave_logits_unchanged(L):
+    """classify stops each row's attention at its extent (last unmasked or
+    marker-read position + 1); the logits must equal those of the full
+    computation (GD_FULL_ROWS) bit for bit.  The packed forward (only the
+    extents' tokens through every kernel) must agree within fp16 rounding of
+    the differently tiled small GEMMs."""
+    from gliner_decide import DecisionInput
+    fast, full, _, _ = _small_pair()
+    ids, mask, mi, mm = _extent_batch(L, L)
     inp = DecisionInput(ids, mask, mi, mm)
-    a = fast.classify(inp).logits.float().cpu().numpy()
-    b_ = full.classify(inp).logits.float().cpu().numpy()
+    dev = inp.to_device()
+    a = fast.classify_device(*dev).float().cpu().numpy()
+    b_ = full.classify_device(*dev).float().cpu().numpy()
     assert np.all(np.isfinite(a)) and np.all(a[mm == 0] == -10000.0)
     np.testing.assert_array_equal(a, b_)
+    packed = fast.classify(inp).logits.float().cpu().numpy()  # host arrays: packed rows
+    assert np.all(packed[mm == 0] == -10000.0)
+    assert np.max(np.abs(packed - a)) <= 2e-3
+
+
+def test_packed_rows_match_padded_at_full_size():
+    """B=32, L=256, lengths U[40, 256] (the classification workload's
+    layout): packed rows (4.9k of 8.2k tokens) give the padded forward's
+    logits bit for bit (both run the 256-row MFMA GEMM tiles), eagerly and
+    through a captured graph; a wrong token total raises the device flag."""
+    from gliner_decide import DecisionInput
+    from gliner_decide._native import GlinerDecideError
+    from gliner_decide.decode import row_extents
+    from gliner_decide.synthetic import classification_batch
+    fast, full, w, pc = _small_pair(seed=17)
+    batch = classification_batch(seed=4, vocab=3000)
+    a = batch.arrays()
+    a["input_ids"] = np.where(a["input_ids"] >= 3000, a["input_ids"] % 3000, a["input_ids"])  # marker ids
+    total = int(row_extents(a["attention_mask"], a["marker_indices"], a["marker_mask"]).sum())
+    assert 2048 < total < 8192
+    dev = DecisionInput(**a).to_device()
+    padded = fast.classify_device(*dev).float().cpu().numpy()
+    packed = fast.classify_device(*dev, total_tokens=total).float().cpu().numpy()
+    np.testing.assert_array_equal(packed, padded)
+    from gliner_decide import GLiNERDecideClassifier
+    graph = GLiNERDecideClassifier(w, pc, use_compiled_graph=True)
+    for _ in range(3):
+        g = graph.classify_device(*dev, total_tokens=total).float().cpu().numpy()
+        np.testing.assert_array_equal(g, padded)
+    fast.check_device_errors()
+    fast.classify_device(*dev, total_tokens=total - 1)
+    with pytest.raises(GlinerDecideError):
+        fast.check_device_errors()
+    fast.check_device_errors()  # cleared
+    with pytest.raises(GlinerDecideError):
+        fast.classify_device(*dev, total_tokens=8192 + 1)
 
 
 def test_compiled_graph_replays_match_eager():

@@ -107,3 +107,28 @@ def test_bucket_mix_workload():
         # padded rows copy the last valid row (main.swift:22-49)
         if x.valid_rows < 32:
             assert (x.input_ids[x.valid_rows:] == x.input_ids[x.valid_rows - 1]).all()
+
+
+def test_row_extents_definition():
+    """decode.row_extents against the definition written as loops: the larger
+    of (last unmasked position + 1) and (last position an unmasked marker slot
+    reads + 1), out-of-range markers reading position 0."""
+    from gliner_decide.decode import row_extents
+    r = np.random.default_rng(3)
+    for _ in range(50):
+        B, L, S = int(r.integers(1, 6)), int(r.integers(1, 40)), int(r.integers(1, 6))
+        mask = (r.random((B, L)) < r.random()).astype(np.float16)
+        mi = r.integers(-3, L + 3, size=(B, 1, S)).astype(np.int32)
+        mm = (r.random((B, 1, S)) < 0.6).astype(np.float32)
+        want = []
+        for b in range(B):
+            e = 0
+            for l in range(L):
+                if mask[b, l] > 0:
+                    e = l + 1
+            for s in range(S):
+                if mm[b, 0, s] > 0:
+                    p = mi[b, 0, s] if 0 <= mi[b, 0, s] < L else 0
+                    e = max(e, p + 1)
+            want.append(e)
+        assert row_extents(mask, mi, mm).tolist() == want
