@@ -100,12 +100,16 @@ constexpr int kGeluHalf = 18 * 1024;      // entries per sign
 constexpr int kGeluEntries = 2 * kGeluHalf;
 __device__ __attribute__((aligned(16))) half_t g_gelu_table[kGeluEntries];
 
-__device__ __forceinline__ half_t gelu_from_table(half_t y, const half_t* tab) {
+// The table may be split over two LDS buffers: entries [0, split) in tab,
+// the rest in tab2.
+__device__ __forceinline__ half_t gelu_from_table(half_t y, const half_t* tab, const half_t* tab2 = nullptr,
+                                                  uint32_t split = kGeluEntries) {
   const uint32_t u = __builtin_bit_cast(uint16_t, y);
   const uint32_t mag = u & 0x7FFFu;
   const uint32_t idx = (u >> 15) * kGeluHalf + (mag < (uint32_t)kGeluHalf ? mag : kGeluHalf - 1);
   const half_t big = (u >> 15) ? (half_t)(y * (half_t)0) : y;
-  const half_t small = tab[idx];
+  const half_t* p = idx < split ? tab + idx : tab2 + (idx - split);
+  const half_t small = *p;
   return mag < (uint32_t)kGeluHalf ? small : big;
 }
 
@@ -303,12 +307,16 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
   static_assert(RPA % 32 == 0 && NSTAGE * RPA >= BM, "epilogue staging must fit in the stage buffers");
   static_assert((NSTAGE - 1) * LPS < 64, "vmcnt range");
 
-  // The GELU epilogue of a tile whose stage buffer holds 128 rows of C reads
-  // the GELU table from LDS: st1 is sized for it and C goes through st0 in
-  // two passes of RPA rows.
-  constexpr bool GELU_TABLE = EPI == GD_EPI_BIAS_GELU && NSTAGE == 2 && RPA == 128 && BM == 2 * RPA && WM == RPA;
+  // The GELU epilogue reads the correctly rounded table from LDS: with two
+  // stages st1 is sized for all of it; with more, its first STAGE entries go
+  // to st1 and the rest to st2.  C then goes through st0 in passes of RPA
+  // rows, each wave's WM rows inside one pass.
+  constexpr bool GELU_TABLE = EPI == GD_EPI_BIAS_GELU && RPA % WM == 0 &&
+                              (NSTAGE == 2 || 2 * STAGE >= kGeluEntries);
+  constexpr int TAB1 = NSTAGE == 2 || kGeluEntries <= STAGE ? kGeluEntries : STAGE;  // entries in st1
   __shared__ __attribute__((aligned(1024))) half_t st0[STAGE];
-  __shared__ __attribute__((aligned(1024))) half_t st1[GELU_TABLE && kGeluEntries > STAGE ? kGeluEntries : STAGE];
+  __shared__ __attribute__((aligned(1024)))
+  half_t st1[GELU_TABLE && NSTAGE == 2 && kGeluEntries > STAGE ? kGeluEntries : STAGE];
   __shared__ __attribute__((aligned(1024))) half_t st2[NSTAGE > 2 ? STAGE : 8];
   __shared__ __attribute__((aligned(1024))) half_t st3[NSTAGE > 3 ? STAGE : 8];
   __shared__ __attribute__((aligned(1024))) half_t st4[NSTAGE > 4 ? STAGE : 8];
@@ -457,7 +465,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
   constexpr int ROWS_PER_PASS = NT / CHUNKS_PER_ROW;
   const int cc = t % CHUNKS_PER_ROW;
   if constexpr (GELU_TABLE) {
-    // ---- GELU epilogue: table into st1, C through st0 in two passes ----
+    // ---- GELU epilogue: table into st1 (and st2), C through st0 in passes ----
     // All of this thread's table pieces are loaded before any is stored, so
     // the L2 latency is paid once.
     constexpr int kPieces = kGeluEntries / 8;
@@ -471,9 +479,11 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
 #pragma unroll
     for (int r = 0; r < kPerThread; ++r) {
       const int i = t + r * NT;
-      if (i < kPieces) *reinterpret_cast<half8_t*>(st1 + 8 * i) = piece[r];
+      if (i < kPieces) *reinterpret_cast<half8_t*>(8 * i < TAB1 ? st1 + 8 * i : stage(ic<2 % NSTAGE>{}) + (8 * i - TAB1)) =
+          piece[r];
     }
     __syncthreads();
+    const half_t* tab2 = stage(ic<2 % NSTAGE>{});
     half_t res[TM][TN][16];
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
@@ -481,22 +491,27 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) res[i][j][e] = gelu_from_table((half_t)(acc[i][j][e] + b), st1);
+        for (int e = 0; e < 16; ++e)
+          res[i][j][e] = gelu_from_table((half_t)(acc[i][j][e] + b), st1, tab2, (uint32_t)TAB1);
     }
+    constexpr int NPASS = (BM + RPA - 1) / RPA;
 #pragma unroll
-    for (int pass = 0; pass < 2; ++pass) {
-      if (wm == pass) {  // this wave's WM = RPA rows are rows [pass * RPA, (pass + 1) * RPA) of the tile
+    for (int pass = 0; pass < NPASS; ++pass) {
+      const int row_lo = wm * WM - pass * RPA;  // this wave's first row within the pass
+      if (row_lo >= 0 && row_lo < RPA) {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e)
-              st0[(i * 32 + 4 * lk + 8 * (e >> 2) + (e & 3)) * BN + wn * WN + j * 32 + lr] = res[i][j][e];
+              st0[(row_lo + i * 32 + 4 * lk + 8 * (e >> 2) + (e & 3)) * BN + wn * WN + j * 32 + lr] = res[i][j][e];
       }
       __syncthreads();
+      constexpr int kPassRowsMax = RPA;
+      const int pass_rows = BM - pass * RPA < kPassRowsMax ? BM - pass * RPA : kPassRowsMax;
 #pragma unroll 4
-      for (int r = t / CHUNKS_PER_ROW; r < RPA; r += ROWS_PER_PASS) {
+      for (int r = t / CHUNKS_PER_ROW; r < pass_rows; r += ROWS_PER_PASS) {
         const int row = tile_m * BM + pass * RPA + r;
         if (row < M)
           *reinterpret_cast<half8_t*>(C + (int64_t)row * ldc + tile_n * BN + cc * 8) =

@@ -193,12 +193,14 @@ def _ordered16(a):
     return np.where(i < 0, -(i & 0x7FFF), i)
 
 
-@pytest.mark.parametrize("m,n", [(248, 256), (2048, 256), (8192, 4096)])  # small-M, 256x128 and 256x256 kernels
+@pytest.mark.parametrize("m,n", [(248, 256), (2048, 256), (4896, 4096), (8192, 4096)])
 def test_gelu_epilogue_every_fp16_input(m, n):
     """x @ I^T + 0 reproduces x exactly, so the GELU epilogue sees every finite
     fp16 value once (63488 = 248 x 256).  Against the correctly rounded GELU:
-    at most 1 ulp anywhere, and only for values next to a rounding boundary;
-    the 256x256 kernel reads the correctly rounded table and matches exactly."""
+    at most 1 ulp anywhere (the small-M kernel's erfc form), and only for
+    values next to a rounding boundary; the 256-row tile kernels (256x128 at
+    M = 2048 and 4896, 256x256 at 8192) read the correctly rounded table and
+    match exactly."""
     vals = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
     vals = vals[np.isfinite(vals)]
     x = np.zeros((m, n), np.float16)
@@ -211,7 +213,7 @@ def test_gelu_epilogue_every_fp16_input(m, n):
     want = O.gelu(vals.astype(np.float64))
     d = np.abs(_ordered16(got) - _ordered16(want))
     assert d.max() <= 1, f"{d.max()} ulp at x={vals[np.argmax(d)]}"
-    assert (d > 0).sum() <= (0 if n % 256 == 0 and m >= 8192 else 64)
+    assert (d > 0).sum() <= (0 if m >= 2048 else 64)
     if n == 4096:  # |x| >= 8, infinities and NaN take the table-free branch
         special = np.array([8.0, -8.0, 65504.0, -65504.0, np.inf, -np.inf, np.nan], np.float16)
         x2 = np.zeros((m, n), np.float16)
