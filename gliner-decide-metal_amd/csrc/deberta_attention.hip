@@ -127,8 +127,9 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K, const half_t* __restrict__ V, int qsb, int qsh,
     int qsl, int ksb, int ksh, int ksl, int vsb, int vsh, int vsl, const half_t* __restrict__ PK,
     const half_t* __restrict__ PQ, int pksh, int pksp, int pqsh, int pqsp, const half_t* __restrict__ mask,
-    int mask_kind, const int* __restrict__ row_len, const int* __restrict__ row_off, int B, int H, int L, int P,
-    int bucket_size, float scale_qk, float scale16, half_t* __restrict__ out, int ldo) {
+    int mask_kind, const int* __restrict__ row_len, const int* __restrict__ row_off, const int* __restrict__ sched,
+    int n_sched, int B, int H, int L, int P, int bucket_size, float scale_qk, float scale16, half_t* __restrict__ out,
+    int ldo) {
   // Two stage buffers and the per-wave scratch.  The stage DMA is inline
   // assembly the compiler does not track, so its reads of a stage never wait
   // for the next stage's loads in flight; the kernel orders them itself
@@ -227,9 +228,18 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   // in cost under row extents (when G and the share are even, the pairs stay
   // within a round).
   const bool swap_rounds = ((nblk >> 3) & 1) == 0 && ((gridDim.x >> 3) & 1) == 0 && gridDim.x >= 8;
+  // With a schedule (row extents; built per forward by
+  // attention_schedule_kernel) item slot s holds bh * ntq + qt, or -1 for an
+  // empty slot, which runs as a query tile past every row's extent.
+  const int n_items = sched != nullptr ? n_sched : nblk;
   auto decode = [&](int item) -> Item {
     int bid = item;
-    if ((nblk & 7) == 0) {
+    bool empty = false;
+    if (sched != nullptr) {
+      bid = __builtin_amdgcn_readfirstlane(sched[item]);
+      empty = bid < 0;
+      bid = empty ? 0 : bid;
+    } else if ((nblk & 7) == 0) {
       int l = bid >> 3;
       if (swap_rounds) l ^= (l / (int)(gridDim.x >> 3)) & 1;
       bid = (bid & 7) * (nblk >> 3) + l;
@@ -242,7 +252,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       len = len < 0 ? 0 : (len > L ? L : len);
     }
     const int row0 = row_off != nullptr ? __builtin_amdgcn_readfirstlane(row_off[b]) : -1;
-    return Item{b, __builtin_amdgcn_readfirstlane(bh % H), __builtin_amdgcn_readfirstlane(bid % ntq), len,
+    return Item{b, __builtin_amdgcn_readfirstlane(bh % H), empty ? ntq : __builtin_amdgcn_readfirstlane(bid % ntq), len,
                 len > 0 ? len : 1, row0};
   };
   // Window start of chunk 0 per query tile (at most 4), lane qt of w0_tab.
@@ -302,7 +312,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
 
   for (;;) {
     const int next = item + (int)gridDim.x;
-    const bool has_next = kPersistent && next < nblk;  // uniform
+    const bool has_next = kPersistent && next < n_items;  // uniform
     Item nit = cur;  // decoded once the chunk loop is done
     bool next_staged = false, next_setup = false;
     Setup ns;  // the next item's set-up reads, once issued
@@ -775,7 +785,7 @@ int launch2(const AttentionArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL((deberta_attention_kernel<MAXT, OUTK>), grid, block, 0, stream, hq, hk, hv, (int)a.qsb,     \
                      (int)a.qsh, (int)a.qsl, (int)a.ksb, (int)a.ksh, (int)a.ksl, (int)a.vsb, (int)a.vsh, (int)a.vsl, \
                      hpk, hpq, (int)a.pksh, (int)a.pksp, (int)a.pqsh, (int)a.pqsp, hm, a.mask_kind, a.row_len,      \
-                     a.row_off,                                                                                     \
+                     a.row_off, a.sched, a.n_sched,                                                                 \
                      (int)a.B,                                                                                      \
                      (int)a.H, (int)a.L, (int)a.P, a.bucket_size, a.scale_qk, a.scale16, ho, (int)a.ldo)
   switch (a.output) {
@@ -821,6 +831,63 @@ __global__ __launch_bounds__(256) void row_extent_kernel(const half_t* __restric
     int m = wave_max[0];
     for (int w = 1; w < 4; ++w) m = wave_max[w] > m ? wave_max[w] : m;
     out[b] = m;
+  }
+}
+
+// Item schedule of the persistent attention under row extents (L <= 256,
+// one workgroup per CU, G workgroups).  Items differ in cost (chunks up to
+// the extent, active waves), so the (b, h) pairs are ranked by their cost
+// (largest first; equal costs by index) and dealt in rounds of G / 2 over CU
+// pairs (w, w + 8: one XCD), snaking (odd rounds run the pairs backwards),
+// each pair's two query tiles side by side (swapped on odd rounds); with one
+// query tile, items are dealt over all G workgroups the same way.  sched[w +
+// r G] = bh * ntq + qt is workgroup w's item of round r, -1 where a round has
+// no item.  Costs, in thousandths of a full chunk: 1000 per chunk with two
+// waves per SIMD active, 775 with one, plus 600 for the tail.
+__device__ __forceinline__ int attention_item_cost(int len, int qt) {
+  const int q0 = qt * kQT;
+  if (q0 >= len) return 50;
+  const int nch = (((len + 15) >> 4) + 3) >> 2;
+  const int active = min(kWaves, (len - q0 + 15) >> 4);
+  return nch * (active > 4 ? 1000 : 775) + 600;
+}
+
+constexpr int kSchedMaxPairs = 2048;
+
+__global__ __launch_bounds__(1024) void attention_schedule_kernel(const int32_t* __restrict__ row_len, int B, int H,
+                                                                  int L, int G, int32_t* __restrict__ sched,
+                                                                  int n_slots) {
+  __shared__ int cost[kSchedMaxPairs];
+  const int t = threadIdx.x;
+  const int ntq = (L + kQT - 1) / kQT;
+  const int n = B * H;
+  for (int i = t; i < n; i += 1024) {
+    const int len = row_len[i / H];
+    int c = 0;
+    for (int qt = 0; qt < ntq; ++qt) c += attention_item_cost(len, qt);
+    cost[i] = c;
+  }
+  for (int s = t; s < n_slots; s += 1024) sched[s] = -1;
+  __syncthreads();  // costs complete; the -1 stores land before any item store below
+  for (int i = t; i < n; i += 1024) {
+    const int ci = cost[i];
+    int rank = 0;
+    for (int j = 0; j < n; ++j) {
+      const int cj = cost[j];
+      rank += (cj > ci) || (cj == ci && j < i);
+    }
+    if (ntq == 2) {
+      const int P = G >> 1;  // CU pairs
+      const int r = rank / P, pp = rank - r * P;
+      const int p = (r & 1) ? P - 1 - pp : pp;
+      const int w0 = (p & 7) | ((p >> 3) << 4), w1 = w0 | 8;
+      const int qa = r & 1;
+      sched[w0 + r * G] = i * 2 + qa;
+      sched[w1 + r * G] = i * 2 + (1 - qa);
+    } else {
+      const int r = rank / G, pp = rank - r * G;
+      sched[((r & 1) ? G - 1 - pp : pp) + r * G] = i;
+    }
   }
 }
 
@@ -895,12 +962,34 @@ int ensure_relative_index_table(hipStream_t stream) {
   return GD_OK;
 }
 
+int attention_schedule_slots(int64_t B, int64_t H, int64_t L) {
+  const int64_t ntq = (L + kQT - 1) / kQT;
+  const int64_t items = B * H * ntq;
+  const int64_t G = items < device_cu_count() ? items : device_cu_count();
+  if (L > 256 || ntq > 2 || B * H > kSchedMaxPairs || G % 16 != 0) return 0;
+  return (int)((items + G - 1) / G * G);
+}
+
+int launch_attention_schedule(const int32_t* row_len, int64_t B, int64_t H, int64_t L, int32_t* sched,
+                              hipStream_t stream) {
+  const int n_slots = attention_schedule_slots(B, H, L);
+  if (n_slots == 0) return GD_OK;
+  const int64_t items = B * H * ((L + kQT - 1) / kQT);
+  const int G = (int)(items < device_cu_count() ? items : device_cu_count());
+  hipLaunchKernelGGL(attention_schedule_kernel, dim3(1), dim3(1024), 0, stream, row_len, (int)B, (int)H, (int)L, G,
+                     sched, n_slots);
+  GD_LAUNCH_CHECK();
+  return GD_OK;
+}
+
 int launch_deberta_attention(const AttentionArgs& a, hipStream_t stream) {
   if (a.bucket_size != 256 || a.P != 512) return fail(GD_ERR_SHAPE, "attention: bucket size 256 and 512 positions");
   if (a.row_len != nullptr && a.output != GD_ATTN_OUT_CONTEXT)
     return fail(GD_ERR_INVALID_ARGUMENT, "attention: row extents apply to the context output only");
   if (a.row_off != nullptr && a.row_len == nullptr)
     return fail(GD_ERR_INVALID_ARGUMENT, "attention: packed rows need row extents");
+  if (a.sched != nullptr && (a.row_len == nullptr || a.n_sched != attention_schedule_slots(a.B, a.H, a.L)))
+    return fail(GD_ERR_INVALID_ARGUMENT, "attention: schedule does not match the launch");
   for (int64_t st : {a.qsb, a.qsh, a.qsl, a.ksb, a.ksh, a.ksl, a.vsb, a.vsh, a.vsl, a.pksh, a.pksp, a.pqsh, a.pqsp, a.ldo})
     if (st < 0 || st > INT32_MAX) return fail(GD_ERR_SHAPE, "attention: strides must lie in [0, 2^31)");
   GD_RETURN_IF_ERROR(ensure_relative_index_table(stream));

@@ -53,7 +53,18 @@ struct AttentionArgs {
   // Q, K, V and the output is row row_off[b] + l (the batch strides unused);
   // output rows at or past row_len[b] are not written.
   const int32_t* row_off = nullptr;
+  // Optional item schedule (with row_len; launch_attention_schedule):
+  // n_sched = attention_schedule_slots(B, H, L) entries.
+  const int32_t* sched = nullptr;
+  int n_sched = 0;
 };
+
+// Slots of the persistent attention's item schedule for (B, H, L), 0 when
+// that launch takes no schedule (L > 256, or more than 2048 (b, h) pairs).
+int attention_schedule_slots(int64_t B, int64_t H, int64_t L);
+// Builds the schedule from the row extents (one workgroup; once per forward).
+int launch_attention_schedule(const int32_t* row_len, int64_t B, int64_t H, int64_t L, int32_t* sched,
+                              hipStream_t stream);
 
 int launch_deberta_attention(const AttentionArgs& args, hipStream_t stream);
 

@@ -245,7 +245,7 @@ int Classifier::reserve(int64_t B, int64_t L, int64_t Hh, int64_t O) {
   device_bytes_ -= ws_bytes_;
   const int64_t before = device_bytes_;
   ws_ = Workspace{};
-  ws_tokens_ = ws_markers_ = 0;
+  ws_tokens_ = ws_markers_ = ws_sched_cap_ = 0;
   auto A = [&](size_t bytes, void** p) { return device_alloc(bytes, p, workspace_allocs_); };
   GD_RETURN_IF_ERROR(A((size_t)nt * C * 2, &ws_.hidden));
   GD_RETURN_IF_ERROR(A((size_t)nt * 3 * C * 2, &ws_.qkv));
@@ -263,9 +263,13 @@ int Classifier::reserve(int64_t B, int64_t L, int64_t Hh, int64_t O) {
   GD_RETURN_IF_ERROR(A((size_t)nt * 4, &ws_.row_len));  // B <= B * L
   GD_RETURN_IF_ERROR(A((size_t)(nt + 1) * 4, &ws_.row_off));
   GD_RETURN_IF_ERROR(A((size_t)nt * 4, &ws_.row_map));
+  // schedule slots: at most B * H * ceil(L / 128) items (<= nt * H / 16) plus a round
+  const int64_t sched_cap = nt * std::max<int64_t>(cfg_.num_attention_heads, 16) / 16 + 1024;
+  GD_RETURN_IF_ERROR(A((size_t)sched_cap * 4, &ws_.sched));
   ws_bytes_ = device_bytes_ - before;
   ws_tokens_ = nt;
   ws_markers_ = nm;
+  ws_sched_cap_ = sched_cap;
   return GD_OK;
 }
 
@@ -316,6 +320,8 @@ int Classifier::layer_forward(int li, const void* mask, int64_t B, int64_t L, hi
   a.ldo = C;
   a.row_len = rows.len;
   a.row_off = rows.off;
+  a.sched = rows.sched;
+  a.n_sched = rows.n_sched;
   GD_RETURN_IF_ERROR(launch_deberta_attention(a, stream));
   if (hook) {
     std::snprintf(name, sizeof name, "layer_%d_attention", li);
@@ -380,6 +386,15 @@ int Classifier::forward(const int32_t* ids, const void* mask, const int32_t* mar
     rows.tokens = packed_tokens;
     GD_RETURN_IF_ERROR(launch_pack_rows(rows.len, B, L, packed_tokens, static_cast<int32_t*>(ws_.row_off),
                                         static_cast<int32_t*>(ws_.row_map), err_flag_, stream));
+  }
+  if (rows.len) {  // one item schedule for every layer's attention
+    const int n = attention_schedule_slots(B, cfg_.num_attention_heads, L);
+    if (n > 0 && n <= ws_sched_cap_) {
+      GD_RETURN_IF_ERROR(launch_attention_schedule(rows.len, B, cfg_.num_attention_heads, L,
+                                                   static_cast<int32_t*>(ws_.sched), stream));
+      rows.sched = static_cast<const int32_t*>(ws_.sched);
+      rows.n_sched = n;
+    }
   }
   const int64_t T = packed ? packed_tokens : B * L;
   GD_RETURN_IF_ERROR(encode_into_workspace(ids, mask, B, L, cfg_.num_hidden_layers, stream, hook, rows));

@@ -59,6 +59,7 @@ class Classifier {
     void* row_len = nullptr;  // int32 [B]: per-row attention extents of classify
     void* row_off = nullptr;  // int32 [B + 1]: packed rows: first token row of each batch row
     void* row_map = nullptr;  // int32 [T]: packed rows: token index b * L + l of each packed row
+    void* sched = nullptr;    // int32 [sched_cap]: attention item schedule under row extents
     void *ids = nullptr, *mask = nullptr, *markers = nullptr, *marker_mask = nullptr, *logits = nullptr;
   };
   using ShapeKey = std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t>;  // B, L, Hh, O, packed tokens
@@ -79,6 +80,8 @@ class Classifier {
     const int32_t* off = nullptr;
     const int32_t* map = nullptr;
     int64_t tokens = -1;
+    const int32_t* sched = nullptr;
+    int n_sched = 0;
   };
   int layer_forward(int li, const void* mask, int64_t B, int64_t L, hipStream_t stream, StageHook* hook,
                     const Rows& rows);
@@ -101,7 +104,7 @@ class Classifier {
   void *cls0_w_ = nullptr, *cls0_b_ = nullptr, *cls2_w_ = nullptr, *cls2_b_ = nullptr;
   int32_t* err_flag_ = nullptr;
   Workspace ws_;
-  int64_t ws_tokens_ = 0, ws_markers_ = 0;
+  int64_t ws_tokens_ = 0, ws_markers_ = 0, ws_sched_cap_ = 0;
   std::map<ShapeKey, GraphEntry> graphs_;
   hipStream_t capture_stream_ = nullptr;  // default priority, non-blocking
 };
