@@ -677,6 +677,24 @@ int launch_linear(const void* a, const void* w, const void* bias, void* c, int64
     if (M >= 1024) return launch_tile<128, 128, true>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
     return launch_tile<64, 128, true>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
   }
+  if (M >= 2048 && N % 256 == 0) {
+    // Whole rounds of 256 x 256 tiles (one tile per CU) over the first rows
+    // and, when the rows left over fit one round of 128 x 128 tiles, those in
+    // a second launch: a last round of a few large tiles is slower than one
+    // of many small ones (FFN-up at 4,896 rows: 44 + 18.5 us against 71.5 us).
+    // Both kernels accumulate in the same order and read the GELU table.
+    const int64_t cus = gemm_cu_count();
+    const int64_t m_tiles_round = cus / (N / 256);
+    const int64_t full_rows = m_tiles_round > 0 ? M / (m_tiles_round * 256) * (m_tiles_round * 256) : 0;
+    const int64_t rest = M - full_rows;
+    if (full_rows > 0 && rest > 0 && (rest + 127) / 128 * (N / 128) <= cus) {
+      const int st =
+          launch_lds_tile<256, 256, 2, 64, 2>(A, Wt, Bv, Cm, (int)full_rows, N, K, lda, ldc, epilogue_kind, stream);
+      if (st != GD_OK) return st;
+      return launch_lds_tile<128, 128, 2, 64, 2>(A + full_rows * lda, Wt, Bv, Cm + full_rows * ldc, (int)rest, N, K,
+                                                 lda, ldc, epilogue_kind, stream);
+    }
+  }
   if (M >= 2048) {
     // 256-row tiles: 256 x 256 (two 64-deep stages, 128 KiB of LDS), 256 x 192
     // (two stages, 112 KiB) or 256 x 128 (three stages, 144 KiB), whichever
