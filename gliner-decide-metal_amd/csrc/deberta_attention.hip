@@ -894,7 +894,7 @@ __global__ __launch_bounds__(1024) void attention_schedule_kernel(const int32_t*
 // One workgroup per batch row b: its offset is the sum of the extents before
 // it (B is a batch size, so the O(B^2) reads are few).
 __global__ __launch_bounds__(256) void pack_rows_kernel(const int32_t* __restrict__ row_len, int B, int L,
-                                                        int64_t total, int32_t* __restrict__ row_off,
+                                                        int64_t total, int exact, int32_t* __restrict__ row_off,
                                                         int32_t* __restrict__ row_map,
                                                         int32_t* __restrict__ error_flag) {
   const int b = blockIdx.x;
@@ -911,11 +911,13 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(const int32_t* __restric
     row_off[b] = (int32_t)off;
     if (b == B - 1) {
       row_off[B] = (int32_t)(off + len);
-      if (off + len != total && error_flag) atomicOr(error_flag, 1);
+      if ((exact ? off + len != total : off + len > total) && error_flag) atomicOr(error_flag, 1);
     }
   }
   for (int l = threadIdx.x; l < len; l += 256)
     if (off + l < total) row_map[off + l] = b * L + l;
+  if (b == B - 1)  // rows past the extents (a capacity above their sum) embed token 0
+    for (int64_t t = off + len + threadIdx.x; t < total; t += 256) row_map[t] = 0;
 }
 
 }  // namespace
@@ -929,11 +931,11 @@ int launch_row_extent(const void* mask, const int32_t* markers, const float* mar
   return GD_OK;
 }
 
-int launch_pack_rows(const int32_t* row_len, int64_t B, int64_t L, int64_t total, int32_t* row_off, int32_t* row_map,
-                     int32_t* error_flag, hipStream_t stream) {
+int launch_pack_rows(const int32_t* row_len, int64_t B, int64_t L, int64_t total, bool exact, int32_t* row_off,
+                     int32_t* row_map, int32_t* error_flag, hipStream_t stream) {
   if (B <= 0) return GD_OK;
   hipLaunchKernelGGL(pack_rows_kernel, dim3((unsigned)B), dim3(256), 0, stream, row_len, (int)B, (int)L, total,
-                     row_off, row_map, error_flag);
+                     exact ? 1 : 0, row_off, row_map, error_flag);
   GD_LAUNCH_CHECK();
   return GD_OK;
 }

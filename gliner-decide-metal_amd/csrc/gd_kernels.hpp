@@ -76,8 +76,10 @@ int launch_row_extent(const void* mask, const int32_t* markers, const float* mar
 
 // Packed rows from the extents: row_off[b] = sum of row_len[0, b) (B + 1
 // entries) and row_map[row_off[b] + l] = b * L + l for l < row_len[b], for
-// packed rows below `total`; a sum other than `total` raises the error flag.
-int launch_pack_rows(const int32_t* row_len, int64_t B, int64_t L, int64_t total, int32_t* row_off,
+// packed rows below `total`.  exact: a sum other than `total` raises the
+// error flag; otherwise `total` is a capacity (a larger sum raises it) and
+// the rows past the sum map to token 0.
+int launch_pack_rows(const int32_t* row_len, int64_t B, int64_t L, int64_t total, bool exact, int32_t* row_off,
                      int32_t* row_map, int32_t* error_flag, hipStream_t stream);
 
 int launch_relative_bias_general(const void* q, const void* k, const void* pos_key, const void* pos_query,

@@ -366,7 +366,7 @@ int Classifier::encode_into_workspace(const int32_t* ids, const void* mask, int6
 
 int Classifier::forward(const int32_t* ids, const void* mask, const int32_t* markers, const float* marker_mask,
                         int64_t B, int64_t L, int64_t Hh, int64_t O, void* logits, hipStream_t stream,
-                        StageHook* hook, int64_t packed_tokens) {
+                        StageHook* hook, int64_t packed_tokens, bool packed_exact) {
   const int64_t C = cfg_.hidden_size, CH = cfg_.classifier_hidden;
   const int64_t M = B * Hh * O;
   // Each row's attention stops at its extent (unless GD_FULL_ROWS): every
@@ -384,8 +384,9 @@ int Classifier::forward(const int32_t* ids, const void* mask, const int32_t* mar
     rows.off = static_cast<const int32_t*>(ws_.row_off);
     rows.map = static_cast<const int32_t*>(ws_.row_map);
     rows.tokens = packed_tokens;
-    GD_RETURN_IF_ERROR(launch_pack_rows(rows.len, B, L, packed_tokens, static_cast<int32_t*>(ws_.row_off),
-                                        static_cast<int32_t*>(ws_.row_map), err_flag_, stream));
+    GD_RETURN_IF_ERROR(launch_pack_rows(rows.len, B, L, packed_tokens, packed_exact,
+                                        static_cast<int32_t*>(ws_.row_off), static_cast<int32_t*>(ws_.row_map),
+                                        err_flag_, stream));
   }
   if (rows.len) {  // one item schedule for every layer's attention
     const int n = attention_schedule_slots(B, cfg_.num_attention_heads, L);
@@ -426,6 +427,12 @@ int Classifier::classify(const int32_t* ids, const void* mask, const int32_t* ma
   GD_HIP_CHECK(hipMemcpyAsync(ws_.mask, mask, (size_t)T * 2, hipMemcpyDeviceToDevice, stream));
   GD_HIP_CHECK(hipMemcpyAsync(ws_.markers, markers, (size_t)M * 4, hipMemcpyDeviceToDevice, stream));
   GD_HIP_CHECK(hipMemcpyAsync(ws_.marker_mask, marker_mask, (size_t)M * 4, hipMemcpyDeviceToDevice, stream));
+  // Packed: one graph per token capacity (the total rounded up to 256, at
+  // most B * L), not per total; the forward checks the sum against it.
+  if (packed_tokens >= 0) {
+    const int64_t cap = (packed_tokens + 255) / 256 * 256;
+    packed_tokens = cap < T ? cap : T;
+  }
   const ShapeKey key{B, L, Hh, O, packed_tokens};
   auto it = graphs_.find(key);
   if (it == graphs_.end()) {
@@ -437,7 +444,7 @@ int Classifier::classify(const int32_t* ids, const void* mask, const int32_t* ma
     GD_HIP_CHECK(hipStreamBeginCapture(capture_stream_, hipStreamCaptureModeThreadLocal));
     int st = forward(static_cast<const int32_t*>(ws_.ids), ws_.mask, static_cast<const int32_t*>(ws_.markers),
                      static_cast<const float*>(ws_.marker_mask), B, L, Hh, O, ws_.logits, capture_stream_, nullptr,
-                     packed_tokens);
+                     packed_tokens, false);
     hipGraph_t graph = nullptr;
     hipError_t e = hipStreamEndCapture(capture_stream_, &graph);
     (void)hipGetLastError();

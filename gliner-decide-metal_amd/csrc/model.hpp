@@ -87,9 +87,10 @@ class Classifier {
                     const Rows& rows);
   int encode_into_workspace(const int32_t* ids, const void* mask, int64_t B, int64_t L, int num_layers,
                             hipStream_t stream, StageHook* hook, const Rows& rows);
+  // packed_exact = false: packed_tokens is a capacity >= the extents' sum.
   int forward(const int32_t* ids, const void* mask, const int32_t* markers, const float* marker_mask, int64_t B,
               int64_t L, int64_t Hh, int64_t O, void* logits, hipStream_t stream, StageHook* hook,
-              int64_t packed_tokens = -1);
+              int64_t packed_tokens = -1, bool packed_exact = true);
   void release_graphs();
 
   gd_config cfg_{};

@@ -155,6 +155,21 @@ def test_packed_rows_match_padded_at_full_size():
     for _ in range(3):
         g = graph.classify_device(*dev, total_tokens=total).float().cpu().numpy()
         np.testing.assert_array_equal(g, padded)
+    # another batch whose total lands in the same 256-token capacity replays
+    # that graph (graphs are keyed by capacity, not by total)
+    a2 = {k: v.copy() for k, v in a.items()}
+    lens = a2["attention_mask"].astype(np.float32).sum(1).astype(int)
+    cut = min(9, (total - 1) % 256)
+    b0 = int(np.argmax(lens))
+    a2["attention_mask"][b0, lens[b0] - cut:] = 0
+    total2 = int(row_extents(a2["attention_mask"], a2["marker_indices"], a2["marker_mask"]).sum())
+    assert total2 == total - cut and (total2 + 255) // 256 == (total + 255) // 256
+    dev2 = DecisionInput(**a2).to_device()
+    eager2 = fast.classify_device(*dev2, total_tokens=total2).float().cpu().numpy()
+    for _ in range(2):
+        g2 = graph.classify_device(*dev2, total_tokens=total2).float().cpu().numpy()
+        np.testing.assert_array_equal(g2, eager2)
+    graph.check_device_errors()
     fast.check_device_errors()
     fast.classify_device(*dev, total_tokens=total - 1)
     with pytest.raises(GlinerDecideError):
