@@ -282,8 +282,9 @@ int gd_classifier_classify(gd_classifier* model, const int32_t* input_ids, const
  * the caller's tokenizer knows it; a different value sets the device error
  * flag (gd_classifier_check_device_errors reports GD_ERR_DEVICE_INDEX) and
  * leaves the logits undefined.  Same shapes and rules as gd_classifier_classify
- * otherwise; with GD_USE_COMPILED_GRAPH each (shape, total_tokens) is
- * captured once. */
+ * otherwise; with GD_USE_COMPILED_GRAPH each shape is captured once per token
+ * capacity (total_tokens rounded up to a multiple of 256, at most B * L), and
+ * that graph serves every total up to the capacity. */
 int gd_classifier_classify_packed(gd_classifier* model, const int32_t* input_ids, const void* attention_mask,
                                   const int32_t* marker_indices, const float* marker_mask, int64_t batch,
                                   int64_t seq_len, int64_t max_heads, int64_t max_options, int64_t total_tokens,
