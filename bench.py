@@ -252,7 +252,7 @@ def serving_rate(weights, cfg, passes=2):
     lines = [_json.dumps(e) for e in serving_examples()]
 
     def once(by_length):
-        fe._cache.clear()
+        fe.clear_cache()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         res = raw_cli.run_examples(raw_cli.iter_jsonl(lines), fe, model, total=len(lines),
@@ -270,7 +270,7 @@ def serving_rate(weights, cfg, passes=2):
     return dict(value=out["length"]["rows_s"], unit="rows/s", rows=len(lines), passes=passes,
                 grouped_by_length=out["length"], grouped_by_shape=out["shape"],
                 sample="4096 JSONL text examples (token counts exp(U(ln 8, ln 512)), 1-2 tasks x 2-10 labels), "
-                       "synthetic word-level tokenizer, batches of 32, compiled graphs")
+                       "synthetic word-level tokenizer in the C++ front end, batches of 32, compiled graphs")
 
 
 def calibration_copy(nbytes=256 << 20):

@@ -2,7 +2,10 @@
 
 Every source under csrc/ is compiled as HIP (device code for gfx950 only,
 packed-fp32 instructions disabled) into objects under _build/, then linked
-into lib/libgliner_decide_hip.so.  Run `python build.py` or call `build()`.
+into lib/libgliner_decide_hip.so.  The decision front end under
+csrc/frontend/ is host C++ and is built with g++ (linked against ICU) into
+lib/libgliner_decide_frontend.so.  Run `python build.py` or call `build()`
+(both libraries).
 """
 
 from __future__ import annotations
@@ -55,6 +58,45 @@ def _compile(src: Path, obj: Path) -> tuple[Path, int, str]:
     return src, p.returncode, log
 
 
+FRONTEND_SRC = CSRC / "frontend"
+FRONTEND_LIB_PATH = LIB_DIR / "libgliner_decide_frontend.so"
+# The decision front end is host code: g++ against ICU (regex, grapheme
+# clusters, case mapping, normal forms).
+FRONTEND_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-fvisibility=hidden", "-Wall", "-Wextra",
+                  f"-I{REPO / 'include'}", f"-I{FRONTEND_SRC}"]
+FRONTEND_LIBS = ["-licui18n", "-licuuc", "-licudata"]
+
+
+def build_frontend(verbose: bool = False) -> Path:
+    """Builds libgliner_decide_frontend.so (CPU only) with g++."""
+    BUILD_DIR.mkdir(exist_ok=True)
+    LIB_DIR.mkdir(exist_ok=True)
+    cxx = os.environ.get("CXX") or shutil.which("g++") or "g++"
+    sources = sorted(FRONTEND_SRC.glob("*.cpp"))
+    objs = [BUILD_DIR / ("frontend_" + s.name + ".o") for s in sources]
+
+    def one(pair):
+        src, obj = pair
+        p = subprocess.run([cxx, "-c", str(src), "-o", str(obj), *FRONTEND_FLAGS], capture_output=True, text=True)
+        return src, p.returncode, p.stdout + p.stderr
+
+    with cf.ThreadPoolExecutor(max_workers=max(1, min(len(sources), 4))) as ex:
+        results = list(ex.map(one, zip(sources, objs)))
+    failures = [f"--- {src.name} ---\n{log}" for src, rc, log in results if rc != 0]
+    if failures:
+        raise RuntimeError("front-end compilation failed:\n" + "\n".join(failures))
+    if verbose:
+        for src, _, log in results:
+            if log.strip():
+                print(f"--- {src.name} ---\n{log}", file=sys.stderr)
+    tmp = FRONTEND_LIB_PATH.with_suffix(".so.tmp")
+    p = subprocess.run([cxx, "-shared", "-o", str(tmp), *map(str, objs), *FRONTEND_LIBS], capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError("front-end link failed:\n" + p.stdout + p.stderr)
+    os.replace(tmp, FRONTEND_LIB_PATH)
+    return FRONTEND_LIB_PATH
+
+
 def build(verbose: bool = False, jobs: int | None = None) -> Path:
     BUILD_DIR.mkdir(exist_ok=True)
     LIB_DIR.mkdir(exist_ok=True)
@@ -78,9 +120,11 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     if p.returncode != 0:
         raise RuntimeError("link failed:\n" + p.stdout + p.stderr)
     os.replace(tmp, LIB_PATH)
+    build_frontend(verbose)
     return LIB_PATH
 
 
 if __name__ == "__main__":
     path = build(verbose="-v" in sys.argv)
     print(path)
+    print(FRONTEND_LIB_PATH)

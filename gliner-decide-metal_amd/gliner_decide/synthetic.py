@@ -276,13 +276,20 @@ SERVING_WORDS = 60000
 
 
 def word_level_frontend(words: int = SERVING_WORDS):
-    """NativeDecisionTokenizer over a word-level vocabulary: the reference's
+    """NativeDecisionTokenizer (the C++ front end) over a word-level
+    vocabulary: the reference's
     added tokens ([PAD] 0, [CLS] 1, [SEP] 2, [UNK] 3, [MASK] 4, [P], [L],
     [SEP_TEXT], [SEP_STRUCT], [DESCRIPTION] at 128001..128005), punctuation,
     task and label names, and `words` synthetic words w0, w1, ... from id
     2000 on."""
-    from tokenizers import Tokenizer, models, pre_tokenizers
+    import json
     from .frontend import NativeDecisionTokenizer
+    return NativeDecisionTokenizer.from_json(json.dumps(word_level_tokenizer_json(words)))
+
+
+def word_level_tokenizer_json(words: int = SERVING_WORDS) -> dict:
+    """The tokenizer.json of word_level_frontend: a WordLevel model behind a
+    WhitespaceSplit pre-tokenizer, the specials as added tokens."""
     specials = {"[PAD]": PAD_ID, "[CLS]": CLS_ID, "[SEP]": SEP_ID, "[UNK]": 3, "[MASK]": 4,
                 "[P]": PROMPT_MARKER_ID, "[L]": LABEL_MARKER_ID, "[SEP_TEXT]": SEP_TEXT_ID,
                 "[SEP_STRUCT]": SEP_STRUCT_ID, "[DESCRIPTION]": 128005}
@@ -291,10 +298,11 @@ def word_level_frontend(words: int = SERVING_WORDS):
     vocab.update({f"task{i}": 1100 + i for i in range(8)})
     vocab.update({f"l{i}": 1200 + i for i in range(32)})
     vocab.update({f"w{i}": 2000 + i for i in range(words)})
-    tok = Tokenizer(models.WordLevel(vocab, unk_token="[UNK]"))
-    tok.pre_tokenizer = pre_tokenizers.WhitespaceSplit()
-    tok.add_special_tokens(list(specials))
-    return NativeDecisionTokenizer.from_tokenizer(tok, specials)
+    added = [{"id": i, "content": t, "single_word": False, "lstrip": False, "rstrip": False, "normalized": False,
+              "special": True} for t, i in specials.items()]
+    return {"version": "1.0", "truncation": None, "padding": None, "added_tokens": added, "normalizer": None,
+            "pre_tokenizer": {"type": "WhitespaceSplit"}, "post_processor": None, "decoder": None,
+            "model": {"type": "WordLevel", "vocab": vocab, "unk_token": "[UNK]"}}
 
 
 def serving_examples(seed: int = 7, count: int = 4096, words: int = SERVING_WORDS, min_len: int = 8,
