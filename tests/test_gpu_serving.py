@@ -21,9 +21,8 @@ pytestmark = pytest.mark.gpu
 VOCAB = 3000
 
 
-def _frontend():
-    from tokenizers import Tokenizer, models, pre_tokenizers
-    from gliner_decide.frontend import NativeDecisionTokenizer
+def _tokenizer_json():
+    """A WordLevel tokenizer.json: the specials as added tokens, 1000 words."""
     specials = ["[PAD]", "[CLS]", "[SEP]", "[UNK]", "[MASK]", "[P]", "[L]", "[SEP_STRUCT]", "[SEP_TEXT]",
                 "[DESCRIPTION]"]
     vocab = {t: i for i, t in enumerate(specials)}
@@ -31,10 +30,17 @@ def _frontend():
         vocab[f"w{i}"] = 1000 + i
     for j, t in enumerate(["(", ")", ".", ":", "intent", "tone", "topic", "a", "b", "c", "d", "e"]):
         vocab[t] = 100 + j
-    tok = Tokenizer(models.WordLevel(vocab, unk_token="[UNK]"))
-    tok.pre_tokenizer = pre_tokenizers.WhitespaceSplit()
-    tok.add_special_tokens(specials)
-    return NativeDecisionTokenizer.from_tokenizer(tok, {s: vocab[s] for s in specials})
+    added = [{"id": vocab[t], "content": t, "single_word": False, "lstrip": False, "rstrip": False,
+              "normalized": False, "special": True} for t in specials]
+    return json.dumps({"version": "1.0", "added_tokens": added, "normalizer": None,
+                       "pre_tokenizer": {"type": "WhitespaceSplit"},
+                       "model": {"type": "WordLevel", "vocab": vocab, "unk_token": "[UNK]"}})
+
+
+def _frontend(backend="native"):
+    """The C++ front end (the runner's default); backend="hf" for the check."""
+    from gliner_decide.frontend import NativeDecisionTokenizer
+    return NativeDecisionTokenizer.from_json(_tokenizer_json(), backend=backend)
 
 
 def _examples(n, seed):
@@ -74,6 +80,7 @@ def test_jsonl_runner_end_to_end(tmp_path):
     w = synthetic_weights(pc, seed=11)
     model = GLiNERDecideClassifier(w, pc, use_compiled_graph=True)
     fe = _frontend()
+    assert fe.backend == "native"
     exs = _examples(96, seed=3)
     path = tmp_path / "in.jsonl"
     path.write_text("\n".join(json.dumps(e) for e in exs))
@@ -82,8 +89,10 @@ def test_jsonl_runner_end_to_end(tmp_path):
     assert json.loads(out.read_text()) == res and [r["id"] for r in res] == [e["id"] for e in exs]
     examples = raw_cli.parse_jsonl(path.read_text())
     lengths = set()
+    hf = _frontend("hf")
     for ex, r in zip(examples, res):
         inp = fe.make_input(ex.text, ex.tasks)
+        np.testing.assert_array_equal(inp.input_ids, hf.make_input(ex.text, ex.tasks).input_ids)
         lengths.add(inp.shape[1])
         alone = model.classify(inp).logits.float().cpu().numpy()
         from gliner_decide.decode import decode
