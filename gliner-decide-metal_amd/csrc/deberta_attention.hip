@@ -127,7 +127,8 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K, const half_t* __restrict__ V, int qsb, int qsh,
     int qsl, int ksb, int ksh, int ksl, int vsb, int vsh, int vsl, const half_t* __restrict__ PK,
     const half_t* __restrict__ PQ, int pksh, int pksp, int pqsh, int pqsp, const half_t* __restrict__ mask,
-    int mask_kind, const int* __restrict__ row_len, const int* __restrict__ row_off, const int* __restrict__ sched,
+    int mask_kind, const int* __restrict__ row_len, const int* __restrict__ row_off, const int* __restrict__ q_len,
+    const int* __restrict__ sched,
     int n_sched, int B, int H, int L, int P, int bucket_size, float scale_qk, float scale16, half_t* __restrict__ out,
     int ldo) {
   // Two stage buffers and the per-wave scratch.  The stage DMA is inline
@@ -212,8 +213,10 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   // past it are neither read nor weighted, queries past it are not computed);
   // L without a row-extent array.  `klim` = max(len, 1) bounds row reads.
   // `row0` is the token row of (b, 0) with packed rows (row_off[b]), else -1.
+  // `qlen` (<= len) bounds the queries computed and stored: q_len[b] when
+  // given (only the rows a later step reads), else len.
   struct Item {
-    int b, h, qt, len, klim, row0;
+    int b, h, qt, len, klim, row0, qlen;
   };
   // Q / K / V of (b, h): row 0 of the batch row's slice.
   auto slice_base = [&](const half_t* X, const int b, const int h, const int row0, int sb, int sh, int sl) {
@@ -252,8 +255,13 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       len = len < 0 ? 0 : (len > L ? L : len);
     }
     const int row0 = row_off != nullptr ? __builtin_amdgcn_readfirstlane(row_off[b]) : -1;
+    int qlen = len;
+    if (q_len != nullptr) {
+      qlen = __builtin_amdgcn_readfirstlane(q_len[b]);
+      qlen = qlen < 0 ? 0 : (qlen > len ? len : qlen);
+    }
     return Item{b, __builtin_amdgcn_readfirstlane(bh % H), empty ? ntq : __builtin_amdgcn_readfirstlane(bid % ntq), len,
-                len > 0 ? len : 1, row0};
+                len > 0 ? len : 1, row0, qlen};
   };
   // Window start of chunk 0 per query tile (at most 4), lane qt of w0_tab.
   const int w0_tab = window_lo(kQT * (lane & 3), 0, rel_arith);
@@ -337,11 +345,11 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       // Key tiles and chunks of this item: up to its row extent.  An item
       // whose queries all lie past the extent computes nothing; it runs one
       // chunk step (its first stage is already in flight) and loads no V.
-      const bool live = q0 < cur.len;
+      const bool live = q0 < cur.qlen;
       const int nt = live ? (cur.len + 15) >> 4 : 0;
       const int nchunks = live ? (nt + 3) >> 2 : 1;
       const int klim = cur.klim;
-      const bool active = qw < cur.len;
+      const bool active = qw < cur.qlen;
       const half_t* Kb = slice_base(K, b, h, cur.row0, ksb, ksh, ksl);
       const half_t* PKh = PK + (int64_t)h * pksh;
       const half_t* PQh = PQ + (int64_t)h * pqsh;
@@ -737,8 +745,9 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
 #pragma unroll
         for (int pass = 0; pass < 2; ++pass) {
           const int row = r + 8 * pass;
-          // packed rows: rows past the extent belong to the next batch row
-          if (cur.row0 < 0 || qw + row < cur.len)
+          // packed rows: rows past the extent belong to the next batch row;
+          // rows from qlen on are not computed
+          if ((cur.row0 < 0 && q_len == nullptr) || qw + row < cur.qlen)
             *reinterpret_cast<half8_t*>(out + ((cur.row0 >= 0 ? (int64_t)cur.row0 : (int64_t)b * L) + qw + row) * ldo +
                                         (int64_t)h * kD + cpos * 8) =
                 *reinterpret_cast<const half8_t*>(ot + row * 72 + cpos * 8);
@@ -785,7 +794,7 @@ int launch2(const AttentionArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL((deberta_attention_kernel<MAXT, OUTK>), grid, block, 0, stream, hq, hk, hv, (int)a.qsb,     \
                      (int)a.qsh, (int)a.qsl, (int)a.ksb, (int)a.ksh, (int)a.ksl, (int)a.vsb, (int)a.vsh, (int)a.vsl, \
                      hpk, hpq, (int)a.pksh, (int)a.pksp, (int)a.pqsh, (int)a.pqsp, hm, a.mask_kind, a.row_len,      \
-                     a.row_off, a.sched, a.n_sched,                                                                 \
+                     a.row_off, a.q_len, a.sched, a.n_sched,                                                        \
                      (int)a.B,                                                                                      \
                      (int)a.H, (int)a.L, (int)a.P, a.bucket_size, a.scale_qk, a.scale16, ho, (int)a.ldo)
   switch (a.output) {
@@ -804,15 +813,17 @@ int launch2(const AttentionArgs& a, hipStream_t stream) {
   return GD_OK;
 }
 
-// One workgroup (4 waves) per batch row.
+// One workgroup (4 waves) per batch row.  Without a mask: the marker part
+// only (the query extent).
 __global__ __launch_bounds__(256) void row_extent_kernel(const half_t* __restrict__ mask,
                                                          const int32_t* __restrict__ markers,
                                                          const float* __restrict__ marker_mask, int L, int slots,
                                                          int32_t* __restrict__ out) {
   const int b = blockIdx.x;
   int ext = 0;
-  for (int l = threadIdx.x; l < L; l += 256)
-    if ((float)mask[(int64_t)b * L + l] > 0.f) ext = l + 1;  // l grows: the last hit is the largest
+  if (mask != nullptr)
+    for (int l = threadIdx.x; l < L; l += 256)
+      if ((float)mask[(int64_t)b * L + l] > 0.f) ext = l + 1;  // l grows: the last hit is the largest
   for (int s = threadIdx.x; s < slots; s += 256)
     if (marker_mask[(int64_t)b * slots + s] > 0.f) {
       const int p = markers[(int64_t)b * slots + s];
@@ -931,6 +942,15 @@ int launch_row_extent(const void* mask, const int32_t* markers, const float* mar
   return GD_OK;
 }
 
+int launch_query_extent(const int32_t* markers, const float* marker_mask, int64_t B, int64_t L, int64_t slots,
+                        int32_t* out, hipStream_t stream) {
+  if (B <= 0) return GD_OK;
+  hipLaunchKernelGGL(row_extent_kernel, dim3((unsigned)B), dim3(256), 0, stream, nullptr, markers, marker_mask,
+                     (int)L, (int)slots, out);
+  GD_LAUNCH_CHECK();
+  return GD_OK;
+}
+
 int launch_pack_rows(const int32_t* row_len, int64_t B, int64_t L, int64_t total, bool exact, int32_t* row_off,
                      int32_t* row_map, int32_t* error_flag, hipStream_t stream) {
   if (B <= 0) return GD_OK;
@@ -990,6 +1010,8 @@ int launch_deberta_attention(const AttentionArgs& a, hipStream_t stream) {
     return fail(GD_ERR_INVALID_ARGUMENT, "attention: row extents apply to the context output only");
   if (a.row_off != nullptr && a.row_len == nullptr)
     return fail(GD_ERR_INVALID_ARGUMENT, "attention: packed rows need row extents");
+  if (a.q_len != nullptr && a.row_len == nullptr)
+    return fail(GD_ERR_INVALID_ARGUMENT, "attention: query extents need row extents");
   if (a.sched != nullptr && (a.row_len == nullptr || a.n_sched != attention_schedule_slots(a.B, a.H, a.L)))
     return fail(GD_ERR_INVALID_ARGUMENT, "attention: schedule does not match the launch");
   for (int64_t st : {a.qsb, a.qsh, a.qsl, a.ksb, a.ksh, a.ksl, a.vsb, a.vsh, a.vsl, a.pksh, a.pksp, a.pqsh, a.pqsp, a.ldo})

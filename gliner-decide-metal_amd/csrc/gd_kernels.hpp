@@ -53,6 +53,9 @@ struct AttentionArgs {
   // Q, K, V and the output is row row_off[b] + l (the batch strides unused);
   // output rows at or past row_len[b] are not written.
   const int32_t* row_off = nullptr;
+  // Optional query extents [B] (with row_len): queries at or past
+  // min(q_len[b], row_len[b]) are neither computed nor stored.
+  const int32_t* q_len = nullptr;
   // Optional item schedule (with row_len; launch_attention_schedule):
   // n_sched = attention_schedule_slots(B, H, L) entries.
   const int32_t* sched = nullptr;
@@ -73,6 +76,11 @@ int launch_deberta_attention(const AttentionArgs& args, hipStream_t stream);
 // (position 0 for an out-of-range index)) + 1, or 0.
 int launch_row_extent(const void* mask, const int32_t* markers, const float* marker_mask, int64_t B, int64_t L,
                       int64_t slots, int32_t* out, hipStream_t stream);
+
+// Query extents: out[b] = last position read by a marker slot of row b with
+// marker_mask > 0 (position 0 for an out-of-range index) + 1, or 0.
+int launch_query_extent(const int32_t* markers, const float* marker_mask, int64_t B, int64_t L, int64_t slots,
+                        int32_t* out, hipStream_t stream);
 
 // Packed rows from the extents: row_off[b] = sum of row_len[0, b) (B + 1
 // entries) and row_map[row_off[b] + l] = b * L + l for l < row_len[b], for
@@ -100,6 +108,10 @@ int launch_relative_index_table(int32_t* out, int n, int bucket_size, int max_po
 int launch_marker_rows(const int32_t* marker_indices, int32_t* rows_out, int64_t batch, int64_t seq_len,
                        int64_t markers_per_row, int32_t* error_flag, hipStream_t stream,
                        const int32_t* row_off = nullptr);
+// dst[i, :] = src[rows[i], :] for i < n (rows clamped to [0, src_rows)),
+// `cols` fp16 columns, rows of `cols` elements.
+int launch_gather_rows(const void* src, const int32_t* rows, int64_t n, int64_t src_rows, int64_t cols, void* dst,
+                       hipStream_t stream);
 int launch_head_output(const void* inner, const void* w2, const void* b2, const float* marker_mask, void* logits,
                        int64_t rows, int64_t width, hipStream_t stream);
 

@@ -62,6 +62,33 @@ int launch_marker_rows(const int32_t* marker_indices, int32_t* rows_out, int64_t
   return GD_OK;
 }
 
+namespace {
+// One thread per 16-byte piece: dst[i, 8c .. 8c + 7] = src[rows[i], ...].
+__global__ __launch_bounds__(256) void gather_rows_kernel(const half_t* __restrict__ src,
+                                                          const int32_t* __restrict__ rows, int64_t n,
+                                                          int64_t src_rows, int64_t pieces,
+                                                          half_t* __restrict__ dst) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n * pieces) return;
+  const int64_t i = t / pieces, c = t - i * pieces;
+  int64_t r = rows[i];
+  r = r < 0 ? 0 : (r >= src_rows ? src_rows - 1 : r);
+  *reinterpret_cast<half8_t*>(dst + (i * pieces + c) * 8) =
+      *reinterpret_cast<const half8_t*>(src + (r * pieces + c) * 8);
+}
+}  // namespace
+
+int launch_gather_rows(const void* src, const int32_t* rows, int64_t n, int64_t src_rows, int64_t cols, void* dst,
+                       hipStream_t stream) {
+  if (n <= 0) return GD_OK;
+  if (cols % 8 != 0 || src_rows <= 0) return fail(GD_ERR_SHAPE, "gather_rows: cols must be a multiple of 8");
+  const int64_t threads = n * (cols / 8);
+  hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
+                     static_cast<const half_t*>(src), rows, n, src_rows, cols / 8, static_cast<half_t*>(dst));
+  GD_LAUNCH_CHECK();
+  return GD_OK;
+}
+
 int launch_head_output(const void* inner, const void* w2, const void* b2, const float* marker_mask, void* logits,
                        int64_t rows, int64_t width, hipStream_t stream) {
   if (rows == 0) return GD_OK;

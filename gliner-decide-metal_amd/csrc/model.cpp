@@ -266,6 +266,7 @@ int Classifier::reserve(int64_t B, int64_t L, int64_t Hh, int64_t O) {
   // schedule slots: at most B * H * ceil(L / 128) items (<= nt * H / 16) plus a round
   const int64_t sched_cap = nt * std::max<int64_t>(cfg_.num_attention_heads, 16) / 16 + 1024;
   GD_RETURN_IF_ERROR(A((size_t)sched_cap * 4, &ws_.sched));
+  GD_RETURN_IF_ERROR(A((size_t)nt * 4, &ws_.q_len));  // B <= B * L
   ws_bytes_ = device_bytes_ - before;
   ws_tokens_ = nt;
   ws_markers_ = nm;
@@ -275,7 +276,7 @@ int Classifier::reserve(int64_t B, int64_t L, int64_t Hh, int64_t O) {
 
 // One encoder layer (DeBERTa.swift:296-428).
 int Classifier::layer_forward(int li, const void* mask, int64_t B, int64_t L, hipStream_t stream, StageHook* hook,
-                              const Rows& rows) {
+                              const Rows& rows, const int32_t* q_len, int64_t marker_count) {
   const Layer& Ly = layers_[li];
   const int64_t C = cfg_.hidden_size, F = cfg_.intermediate_size, H = cfg_.num_attention_heads, D = C / H;
   const int64_t T = rows.tokens >= 0 ? rows.tokens : B * L;
@@ -320,31 +321,41 @@ int Classifier::layer_forward(int li, const void* mask, int64_t B, int64_t L, hi
   a.ldo = C;
   a.row_len = rows.len;
   a.row_off = rows.off;
-  a.sched = rows.sched;
-  a.n_sched = rows.n_sched;
+  a.q_len = q_len;
+  a.sched = q_len ? nullptr : rows.sched;  // the schedule's costs assume every query
+  a.n_sched = q_len ? 0 : rows.n_sched;
   GD_RETURN_IF_ERROR(launch_deberta_attention(a, stream));
   if (hook) {
     std::snprintf(name, sizeof name, "layer_%d_attention", li);
     hook->end(name, stream);
     hook->begin(stream);
   }
+  // Rows leaving the layer: all T in place in ws_.hidden, or the marker rows
+  // compact in ws_.qkv (free once the attention has read Q, K and V): the
+  // output projection gathers their context rows, the residual their hidden
+  // rows; every later step is row-wise.
+  const bool compact = marker_count >= 0;
+  const int64_t R = compact ? marker_count : T;
+  void* hid = compact ? ws_.qkv : ws_.hidden;
+  const int32_t* gather = compact ? static_cast<const int32_t*>(ws_.marker_rows) : nullptr;
   // output projection + residual LayerNorm (:412-418)
+  GD_RETURN_IF_ERROR(launch_linear(ws_.ctx, Ly.out_w, Ly.out_b, ws_.tmp, R, C, C, C, C, gather, compact ? T : 0,
+                                   GD_EPI_BIAS, stream));
+  if (compact) GD_RETURN_IF_ERROR(launch_gather_rows(ws_.hidden, gather, R, T, C, hid, stream));
   GD_RETURN_IF_ERROR(
-      launch_linear(ws_.ctx, Ly.out_w, Ly.out_b, ws_.tmp, T, C, C, C, C, nullptr, 0, GD_EPI_BIAS, stream));
-  GD_RETURN_IF_ERROR(
-      launch_residual_layer_norm(ws_.tmp, ws_.hidden, Ly.ln1_g, Ly.ln1_b, ws_.hidden, T, C, eps, ln_flags, stream));
+      launch_residual_layer_norm(ws_.tmp, hid, Ly.ln1_g, Ly.ln1_b, hid, R, C, eps, ln_flags, stream));
   if (hook) {
     std::snprintf(name, sizeof name, "layer_%d_attention_output", li);
     hook->end(name, stream);
     hook->begin(stream);
   }
   // feed-forward + residual LayerNorm (:420-427)
-  GD_RETURN_IF_ERROR(launch_linear(ws_.hidden, Ly.inter_w, Ly.inter_b, ws_.ffn, T, F, C, C, F, nullptr, 0,
-                                   GD_EPI_BIAS_GELU, stream));
   GD_RETURN_IF_ERROR(
-      launch_linear(ws_.ffn, Ly.ffn_w, Ly.ffn_b, ws_.tmp, T, C, F, F, C, nullptr, 0, GD_EPI_BIAS, stream));
+      launch_linear(hid, Ly.inter_w, Ly.inter_b, ws_.ffn, R, F, C, C, F, nullptr, 0, GD_EPI_BIAS_GELU, stream));
   GD_RETURN_IF_ERROR(
-      launch_residual_layer_norm(ws_.tmp, ws_.hidden, Ly.ln2_g, Ly.ln2_b, ws_.hidden, T, C, eps, ln_flags, stream));
+      launch_linear(ws_.ffn, Ly.ffn_w, Ly.ffn_b, ws_.tmp, R, C, F, F, C, nullptr, 0, GD_EPI_BIAS, stream));
+  GD_RETURN_IF_ERROR(
+      launch_residual_layer_norm(ws_.tmp, hid, Ly.ln2_g, Ly.ln2_b, hid, R, C, eps, ln_flags, stream));
   if (hook) {
     std::snprintf(name, sizeof name, "layer_%d_feed_forward", li);
     hook->end(name, stream);
@@ -398,14 +409,30 @@ int Classifier::forward(const int32_t* ids, const void* mask, const int32_t* mar
     }
   }
   const int64_t T = packed ? packed_tokens : B * L;
-  GD_RETURN_IF_ERROR(encode_into_workspace(ids, mask, B, L, cfg_.num_hidden_layers, stream, hook, rows));
-  // classifier (:430-444)
-  if (hook) hook->begin(stream);
+  // The classifier reads the last layer's marker rows only: that layer runs
+  // its queries up to each row's last marker and everything after the
+  // attention on the M marker rows (unless GD_FULL_ROWS, or M > the
+  // workspace's rows).  The logits are those of the full computation.
+  const int N = cfg_.num_hidden_layers;
+  const bool prune = rows.len != nullptr && !(flags_ & GD_FULL_ROWS) && N > 0 && M > 0 && M <= ws_tokens_;
   GD_RETURN_IF_ERROR(launch_marker_rows(markers, static_cast<int32_t*>(ws_.marker_rows), B, L, Hh * O, err_flag_,
                                         stream, rows.off));
-  GD_RETURN_IF_ERROR(launch_linear(ws_.hidden, cls0_w_, cls0_b_, ws_.inner, M, CH, C, C, CH,
-                                   static_cast<const int32_t*>(ws_.marker_rows), T > 0 ? T : 1, GD_EPI_BIAS_RELU,
-                                   stream));
+  if (prune)
+    GD_RETURN_IF_ERROR(
+        launch_query_extent(markers, marker_mask, B, L, Hh * O, static_cast<int32_t*>(ws_.q_len), stream));
+  GD_RETURN_IF_ERROR(encode_into_workspace(ids, mask, B, L, prune ? N - 1 : N, stream, hook, rows));
+  if (prune)
+    GD_RETURN_IF_ERROR(
+        layer_forward(N - 1, mask, B, L, stream, hook, rows, static_cast<const int32_t*>(ws_.q_len), M));
+  // classifier (:430-444)
+  if (hook) hook->begin(stream);
+  if (prune)
+    GD_RETURN_IF_ERROR(launch_linear(ws_.qkv, cls0_w_, cls0_b_, ws_.inner, M, CH, C, C, CH, nullptr, 0,
+                                     GD_EPI_BIAS_RELU, stream));
+  else
+    GD_RETURN_IF_ERROR(launch_linear(ws_.hidden, cls0_w_, cls0_b_, ws_.inner, M, CH, C, C, CH,
+                                     static_cast<const int32_t*>(ws_.marker_rows), T > 0 ? T : 1, GD_EPI_BIAS_RELU,
+                                     stream));
   GD_RETURN_IF_ERROR(launch_head_output(ws_.inner, cls2_w_, cls2_b_, marker_mask, logits, M, CH, stream));
   if (hook) hook->end("classifier", stream);
   return GD_OK;

@@ -60,6 +60,7 @@ class Classifier {
     void* row_off = nullptr;  // int32 [B + 1]: packed rows: first token row of each batch row
     void* row_map = nullptr;  // int32 [T]: packed rows: token index b * L + l of each packed row
     void* sched = nullptr;    // int32 [sched_cap]: attention item schedule under row extents
+    void* q_len = nullptr;    // int32 [B]: last marker position + 1 per batch row (classify's last layer)
     void *ids = nullptr, *mask = nullptr, *markers = nullptr, *marker_mask = nullptr, *logits = nullptr;
   };
   using ShapeKey = std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t>;  // B, L, Hh, O, packed tokens
@@ -83,8 +84,12 @@ class Classifier {
     const int32_t* sched = nullptr;
     int n_sched = 0;
   };
+  // marker_count >= 0: only the marker rows ws_.marker_rows[0, marker_count)
+  // leave the layer, compact (row i = marker slot i) in ws_.qkv; attention
+  // queries stop at q_len[b] (the classifier reads nothing else of the last
+  // layer).
   int layer_forward(int li, const void* mask, int64_t B, int64_t L, hipStream_t stream, StageHook* hook,
-                    const Rows& rows);
+                    const Rows& rows, const int32_t* q_len = nullptr, int64_t marker_count = -1);
   int encode_into_workspace(const int32_t* ids, const void* mask, int64_t B, int64_t L, int num_layers,
                             hipStream_t stream, StageHook* hook, const Rows& rows);
   // packed_exact = false: packed_tokens is a capacity >= the extents' sum.
