@@ -709,6 +709,13 @@ int launch_linear(const void* a, const void* w, const void* bias, void* c, int64
     return launch_lds_tile<256, 128, 4, 64, 3>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
   }
   if (M >= 1024) return launch_tile<128, 128, false>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
+  // Short M (classifier head, the last layer's marker rows, short buckets):
+  // 64 x 64 tiles of four waves, four 64-deep DMA stages in flight (64 KiB:
+  // two workgroups per CU).  The register-staged kernel keeps one K step in
+  // flight, which left a 160-row K = 4096 product waiting on global latency
+  // for 55 us.
+  if (N % 64 == 0 && K % 64 == 0)
+    return launch_lds_tile<64, 64, 2, 64, 4, 4>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
   return launch_tile<64, 128, false>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
 }
 

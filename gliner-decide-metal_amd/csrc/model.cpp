@@ -331,17 +331,22 @@ int Classifier::layer_forward(int li, const void* mask, int64_t B, int64_t L, hi
     hook->begin(stream);
   }
   // Rows leaving the layer: all T in place in ws_.hidden, or the marker rows
-  // compact in ws_.qkv (free once the attention has read Q, K and V): the
-  // output projection gathers their context rows, the residual their hidden
-  // rows; every later step is row-wise.
+  // compact in ws_.qkv (free once the attention has read Q, K and V): their
+  // context rows (gathered into ws_.ffn, free until the FFN) go through the
+  // output projection, their hidden rows are gathered for the residual;
+  // every later step is row-wise.
   const bool compact = marker_count >= 0;
   const int64_t R = compact ? marker_count : T;
   void* hid = compact ? ws_.qkv : ws_.hidden;
-  const int32_t* gather = compact ? static_cast<const int32_t*>(ws_.marker_rows) : nullptr;
+  void* ctx = compact ? ws_.ffn : ws_.ctx;
+  if (compact) {
+    const int32_t* rows_m = static_cast<const int32_t*>(ws_.marker_rows);
+    GD_RETURN_IF_ERROR(launch_gather_rows(ws_.ctx, rows_m, R, T, C, ctx, stream));
+    GD_RETURN_IF_ERROR(launch_gather_rows(ws_.hidden, rows_m, R, T, C, hid, stream));
+  }
   // output projection + residual LayerNorm (:412-418)
-  GD_RETURN_IF_ERROR(launch_linear(ws_.ctx, Ly.out_w, Ly.out_b, ws_.tmp, R, C, C, C, C, gather, compact ? T : 0,
-                                   GD_EPI_BIAS, stream));
-  if (compact) GD_RETURN_IF_ERROR(launch_gather_rows(ws_.hidden, gather, R, T, C, hid, stream));
+  GD_RETURN_IF_ERROR(
+      launch_linear(ctx, Ly.out_w, Ly.out_b, ws_.tmp, R, C, C, C, C, nullptr, 0, GD_EPI_BIAS, stream));
   GD_RETURN_IF_ERROR(
       launch_residual_layer_norm(ws_.tmp, hid, Ly.ln1_g, Ly.ln1_b, hid, R, C, eps, ln_flags, stream));
   if (hook) {

@@ -136,6 +136,7 @@ def test_embedding_layer_norm():
 # linear (DeBERTa.swift:60-92, 421, 437)
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("m,n,k", [(1, 128, 64), (65, 256, 128), (300, 1024, 1024), (1000, 384, 192),
+                                   (160, 1024, 4096), (160, 4096, 1024), (37, 2048, 1024),
                                    (4096, 1024, 256), (8192, 3072, 1024),
                                    (4896, 4096, 256), (5500, 3072, 256)])  # split: whole rounds + 128x128 rest
 @pytest.mark.parametrize("epi", ["bias", "gelu", "relu", "none"])
@@ -177,6 +178,25 @@ def check_linear(out, x, w, b, epi):
     # the common case is exact agreement with the once-rounded reference value
     if epi in ("none", "bias"):
         assert np.mean(out != O.f16(y)) < 5e-3
+
+
+@pytest.mark.parametrize("epi", ["bias", "gelu"])
+def test_linear_rows_do_not_depend_on_m(epi):
+    """Every GEMM kernel accumulates an element over the same K slices in the
+    same order and rounds it the same way: the first rows of a 4096-row
+    product (256-row tiles) equal, bit for bit, the same rows computed alone
+    (160 rows: the short-M tiles; 1500: the register-staged 128-row tiles)."""
+    r = np.random.default_rng(21)
+    x = r.standard_normal((4096, 1024)).astype(np.float16)
+    w = (r.standard_normal((4096, 1024)) / 32).astype(np.float16)
+    b = r.standard_normal(4096).astype(np.float16)
+    def bits(t):
+        torch.cuda.synchronize()
+        return t.cpu().numpy().view(np.uint16)
+
+    full = bits(fk().linear(dev(x), dev(w), dev(b), epilogue=epi))
+    for m in (160, 1500):
+        np.testing.assert_array_equal(bits(fk().linear(dev(x[:m]), dev(w), dev(b), epilogue=epi)), full[:m])
 
 
 def test_linear_row_gather():
