@@ -694,18 +694,25 @@ int launch_linear(const void* a, const void* w, const void* bias, void* c, int64
     // finishes first: rounds of one tile per CU, each costing the tile's
     // measured time relative to a 256 x 128 tile (1.9, 1.35, 1; K = 1024 and
     // 4096 alike).  Ties keep the larger tile.
-    const int64_t tiles_m = (M + 255) / 256;
     const int64_t cus = gemm_cu_count();
-    auto rounds = [&](int bn) { return (double)((tiles_m * (N / bn) + cus - 1) / cus); };
-    int bn = 128;
-    double best = rounds(128);
-    if (N % 192 == 0 && rounds(192) * 1.35 <= best) {
-      bn = 192;
-      best = rounds(192) * 1.35;
+    auto rounds = [&](int bm, int bn) { return (double)((((M + bm - 1) / bm) * (N / bn) + cus - 1) / cus); };
+    int bm = 256, bn = 128;
+    double best = rounds(256, 128);
+    // 192 x 128 tiles (three stages, 120 KiB) fill a round that 256-row
+    // tiles leave part idle (out-proj and FFN-down on ~4,900 packed rows: 208
+    // tiles against 160), at about 0.8 of a 256 x 128 tile's time.
+    if (rounds(192, 128) * 0.8 < best) {
+      bm = 192;
+      best = rounds(192, 128) * 0.8;
     }
-    if (N % 256 == 0 && rounds(256) * 1.9 <= best) bn = 256;
+    if (N % 192 == 0 && rounds(256, 192) * 1.35 <= best) {
+      bm = 256, bn = 192;
+      best = rounds(256, 192) * 1.35;
+    }
+    if (N % 256 == 0 && rounds(256, 256) * 1.9 <= best) bm = 256, bn = 256;
     if (bn == 256) return launch_lds_tile<256, 256, 2, 64, 2>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
     if (bn == 192) return launch_lds_tile<256, 192, 4, 64, 2>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
+    if (bm == 192) return launch_lds_tile<192, 128, 2, 64, 3>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
     return launch_lds_tile<256, 128, 4, 64, 3>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
   }
   if (M >= 1024) return launch_tile<128, 128, false>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);

@@ -180,16 +180,17 @@ def check_linear(out, x, w, b, epi):
         assert np.mean(out != O.f16(y)) < 5e-3
 
 
-@pytest.mark.parametrize("epi", ["bias", "gelu"])
-def test_linear_rows_do_not_depend_on_m(epi):
+@pytest.mark.parametrize("epi,n", [("bias", 4096), ("gelu", 4096), ("bias", 1024)])
+def test_linear_rows_do_not_depend_on_m(epi, n):
     """Every GEMM kernel accumulates an element over the same K slices in the
     same order and rounds it the same way: the first rows of a 4096-row
-    product (256-row tiles) equal, bit for bit, the same rows computed alone
-    (160 rows: the short-M tiles; 1500: the register-staged 128-row tiles)."""
+    product (256 x 256 tiles at N = 4096, 192 x 128 at N = 1024) equal, bit
+    for bit, the same rows computed alone (160 rows: the short-M tiles;
+    1500: the register-staged 128-row tiles)."""
     r = np.random.default_rng(21)
     x = r.standard_normal((4096, 1024)).astype(np.float16)
-    w = (r.standard_normal((4096, 1024)) / 32).astype(np.float16)
-    b = r.standard_normal(4096).astype(np.float16)
+    w = (r.standard_normal((n, 1024)) / 32).astype(np.float16)
+    b = r.standard_normal(n).astype(np.float16)
     def bits(t):
         torch.cuda.synchronize()
         return t.cpu().numpy().view(np.uint16)
