@@ -60,6 +60,29 @@ def parse():
 # ---------------------------------------------------------------------------
 # live kernel timing
 # ---------------------------------------------------------------------------
+def gemm_tile(M, N, cus=256):
+    """The tile launch_linear picks for M >= 2048 rows (gemm.hip): whole
+    rounds of 256x256 plus a 128x128 remainder, or the fewest rounds of
+    tiles weighted by their relative cost."""
+    if N % 256 == 0:
+        per_round = cus // (N // 256)
+        full = M // (per_round * 256) * (per_round * 256) if per_round else 0
+        rest = M - full
+        if full > 0 and rest > 0 and (rest + 127) // 128 * (N // 128) <= cus:
+            return "256,256 + 128,128"
+
+    def rounds(bm, bn):
+        return -(-(-(-M // bm) * (N // bn)) // cus)
+    tile, best = "256,128", rounds(256, 128)
+    if rounds(192, 128) * 0.8 < best:
+        tile, best = "192,128", rounds(192, 128) * 0.8
+    if N % 192 == 0 and rounds(256, 192) * 1.35 <= best:
+        tile, best = "256,192", rounds(256, 192) * 1.35
+    if N % 256 == 0 and rounds(256, 256) * 1.9 <= best:
+        tile = "256,256"
+    return tile
+
+
 def time_launches(fn, sets, iters):
     """Average duration (us) of fn(set) over `iters` launches cycling through
     the buffer sets, between two events on the launch stream."""
@@ -188,9 +211,7 @@ def measure_kernels(model_cfg, iters, only=None):
 
         us = time_launches(lin, [0], iters)
         flops = 2 * T * n * k
-        t256 = (T + 255) // 256 * (n // 256)  # the library's tile choice for T >= 2048
-        tile = "256,256" if n % 256 == 0 and (t256 % 256 == 0 or t256 >= 512) else "256,128"
-        out[name] = dict(kernel=f"gemm_nt_lds_kernel<{tile}>", shape=[T, n, k], us=us, flops=flops,
+        out[name] = dict(kernel=f"gemm_nt_lds_kernel<{gemm_tile(T, n)}>", shape=[T, n, k], us=us, flops=flops,
                          tflops=flops / us / 1e6, bound="mfma", launches_per_step=24,
                          bytes=(T * k + n * k + T * n) * 2)
         del a, w, c
