@@ -242,8 +242,11 @@ typedef struct gd_classifier gd_classifier;
  * attention_mask > 0) + 1 and (last position a marker slot with
  * marker_mask > 0 reads) + 1.  Positions past the extent are masked keys and
  * feed no position before it, so the logits are the same; their hidden
- * states are not computed.  GD_FULL_ROWS computes every position, as the
- * reference's graph does (encode and layer_forward always do). */
+ * states are not computed.  Likewise the last layer, whose only reader is
+ * the classifier, computes its attention queries up to each row's last
+ * marker and the rest of the layer on the marker rows alone (the logits
+ * are bit-identical).  GD_FULL_ROWS computes every position of every layer,
+ * as the reference's graph does (encode and layer_forward always do). */
 #define GD_FULL_ROWS 8u
 
 /* Loads and checks the weights (key names and shapes of
