@@ -715,14 +715,18 @@ int launch_linear(const void* a, const void* w, const void* bias, void* c, int64
     if (bm == 192) return launch_lds_tile<192, 128, 2, 64, 3>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
     return launch_lds_tile<256, 128, 4, 64, 3>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
   }
-  if (M >= 1024) return launch_tile<128, 128, false>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
   // Short M (classifier head, the last layer's marker rows, short buckets):
-  // 64 x 64 tiles of four waves, four 64-deep DMA stages in flight (64 KiB:
-  // two workgroups per CU).  The register-staged kernel keeps one K step in
-  // flight, which left a 160-row K = 4096 product waiting on global latency
-  // for 55 us.
-  if (N % 64 == 0 && K % 64 == 0)
+  // DMA-pipelined tiles -- 128 x 128 (two stages) when they fill a round,
+  // else 64 x 64 tiles of four waves with four 64-deep stages in flight (64
+  // KiB: two workgroups per CU).  The register-staged kernel keeps one K step
+  // in flight, which left a 160-row K = 4096 product waiting on global
+  // latency for 55 us.
+  if (N % 64 == 0 && K % 64 == 0) {
+    if (N % 128 == 0 && (int64_t)((M + 127) / 128) * (N / 128) >= gemm_cu_count())
+      return launch_lds_tile<128, 128, 2, 64, 2>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
     return launch_lds_tile<64, 64, 2, 64, 4, 4>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
+  }
+  if (M >= 1024) return launch_tile<128, 128, false>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
   return launch_tile<64, 128, false>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
 }
 

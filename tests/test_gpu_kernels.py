@@ -185,8 +185,8 @@ def test_linear_rows_do_not_depend_on_m(epi, n):
     """Every GEMM kernel accumulates an element over the same K slices in the
     same order and rounds it the same way: the first rows of a 4096-row
     product (256 x 256 tiles at N = 4096, 192 x 128 at N = 1024) equal, bit
-    for bit, the same rows computed alone (160 rows: the short-M tiles;
-    1500: the register-staged 128-row tiles)."""
+    for bit, the same rows computed alone (160 rows: the 64 x 64 tiles;
+    1500: 128 x 128 tiles at N = 4096, 64 x 64 at N = 1024)."""
     r = np.random.default_rng(21)
     x = r.standard_normal((4096, 1024)).astype(np.float16)
     w = (r.standard_normal((n, 1024)) / 32).astype(np.float16)
