@@ -110,6 +110,35 @@ def _small_pair(seed=13, **flags):
     return GLiNERDecideClassifier(w, pc, **flags), GLiNERDecideClassifier(w, pc, full_rows=True), w, pc
 
 
+def test_compact_last_layer_edges():
+    """The last layer on the marker rows only: a row whose marker slots are
+    all masked (no query computed; its logits are all -10000) and more marker
+    slots than tokens (B*Hh*O = 240 > B*L = 128, after a larger batch grew the
+    workspace).  Padded and packed, the logits equal GD_FULL_ROWS bit for
+    bit."""
+    from gliner_decide import DecisionInput
+    fast, full, _, _ = _small_pair(seed=23)
+    big = _extent_batch(128, 5)
+    fast.classify(DecisionInput(*big))  # workspace for 768 tokens
+    r = np.random.default_rng(31)
+    B, L, Hh, O = 4, 32, 3, 20
+    ids = r.integers(1000, 3000, size=(B, L)).astype(np.int32)
+    lengths = np.array([32, 20, 9, 25])
+    mask = (np.arange(L)[None] < lengths[:, None]).astype(np.float16)
+    ids[mask == 0] = 0
+    mi = r.integers(0, L, size=(B, Hh, O)).astype(np.int32)
+    mm = (r.random((B, Hh, O)) < 0.7).astype(np.float32)
+    mm[2] = 0  # every slot of row 2 masked
+    inp = DecisionInput(ids, mask, mi, mm)
+    want = full.classify_device(*inp.to_device()).float().cpu().numpy()
+    assert np.all(want[2] == -10000.0)
+    padded = fast.classify_device(*inp.to_device()).float().cpu().numpy()
+    packed = fast.classify(inp).logits.float().cpu().numpy()
+    np.testing.assert_array_equal(padded, want)
+    np.testing.assert_array_equal(packed, want)
+    fast.check_device_errors()
+
+
 @pytest.mark.parametrize("L", [128, 256, 512])
 def test_row_extents_leave_logits_unchanged(L):
     """classify stops each row's attention at its extent (last unmasked or
