@@ -132,3 +132,47 @@ def test_row_extents_definition():
                     e = max(e, p + 1)
             want.append(e)
         assert row_extents(mask, mi, mm).tolist() == want
+
+
+def test_prepare_weights_filters_and_casts(tmp_path):
+    """Tools/prepare_model.py:82-113: encoder.* and classifier.* kept, floats
+    cast to fp16 (round to nearest even), integers kept, other heads dropped,
+    required tensors enforced, metadata written; bf16 sources read too."""
+    import json
+    import struct
+
+    import torch
+    from safetensors.torch import save_file
+    from gliner_decide.prepare import REQUIRED, prepare_weights
+    r = np.random.default_rng(0)
+    src = {k: torch.from_numpy(r.standard_normal((4, 8)).astype(np.float32)) for k in REQUIRED}
+    src["encoder.encoder.layer.0.output.dense.bias"] = torch.tensor([1 + 2 ** -11, 1 + 3 * 2 ** -11])
+    src["encoder.embeddings.position_ids"] = torch.arange(5, dtype=torch.int64)
+    src["span_rep.project.weight"] = torch.ones(3, 3)
+    src["count_embed.weight"] = torch.ones(2)
+    save_file(src, str(tmp_path / "model.safetensors"))
+    (tmp_path / "config.json").write_text('{"model_type": "deberta-v2"}')
+    out = prepare_weights(tmp_path / "model.safetensors", tmp_path / "out", tmp_path / "config.json")
+    from safetensors.numpy import load_file
+    got = load_file(str(out))
+    assert set(got) == set(REQUIRED) | {"encoder.encoder.layer.0.output.dense.bias", "encoder.embeddings.position_ids"}
+    assert got["classifier.0.weight"].dtype == np.float16 and got["encoder.embeddings.position_ids"].dtype == np.int64
+    np.testing.assert_array_equal(got["classifier.0.weight"], src["classifier.0.weight"].numpy().astype(np.float16))
+    # ties round to even: 1 + 2^-11 -> 1, 1 + 3 * 2^-11 -> 1 + 2^-9
+    assert got["encoder.encoder.layer.0.output.dense.bias"].tolist() == [1.0, 1 + 2 ** -9]
+    n = struct.unpack("<Q", out.read_bytes()[:8])[0]
+    meta = json.loads(out.read_bytes()[8:8 + n])["__metadata__"]
+    assert meta == {"source_model": "fastino/GLiNER2.5-Decide",
+                    "source_revision": "65624f1a0265b3f612bae66a2685a06b94a68a9d",
+                    "precision": "float16", "scope": "encoder+classification-only"}
+    assert (tmp_path / "out" / "encoder-config.json").read_text() == '{"model_type": "deberta-v2"}'
+    # bf16 source
+    save_file({k: v.to(torch.bfloat16) for k, v in src.items() if v.is_floating_point()},
+              str(tmp_path / "bf16.safetensors"))
+    got16 = load_file(str(prepare_weights(tmp_path / "bf16.safetensors", tmp_path / "o2")))
+    np.testing.assert_array_equal(got16["classifier.2.weight"],
+                                  src["classifier.2.weight"].to(torch.bfloat16).float().numpy().astype(np.float16))
+    del src["classifier.2.weight"]
+    save_file(src, str(tmp_path / "partial.safetensors"))
+    with pytest.raises(RuntimeError, match="missing required weights: \\['classifier.2.weight'\\]"):
+        prepare_weights(tmp_path / "partial.safetensors", tmp_path / "o3")
