@@ -13,8 +13,9 @@
  * (thread-local).  Text arguments are UTF-8 byte ranges (not NUL-terminated);
  * invalid UTF-8 is GD_ERR_INVALID_ARGUMENT.  Output arrays are caller-owned
  * host memory; when one is too small the call returns GD_ERR_SHAPE and still
- * reports the size it needs.  A handle may be used from several threads; its
- * calls are serialised.
+ * reports the size it needs.  A handle may be used from several threads:
+ * the calls that use its entry cache (append_tokenized, make_input,
+ * clear_cache) take its lock; the others only read it.
  */
 #ifndef GLINER_DECIDE_FRONTEND_H_
 #define GLINER_DECIDE_FRONTEND_H_
