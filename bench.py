@@ -438,6 +438,19 @@ def main():
         padded()
     padded_s = timed(padded, args.steps)
     log(f"e2e padded: {padded_s * 1000 / args.steps:.3f} ms/step, {B * args.steps / padded_s:.1f} rows/s")
+    # The reference's amount of work: every position of every layer (GD_FULL_ROWS);
+    # the logits must equal the row-extent / marker-row forward's bit for bit.
+    full = GLiNERDecideClassifier(weights, cfg, use_compiled_graph=args.compiled, full_rows=True)
+    full.reserve(B, L, Hh, O_)
+    full_logits = torch.empty_like(logits)
+    full_step = lambda: full.classify_device(ids, mask, markers, mmask, full_logits)  # noqa: E731
+    for _ in range(args.warmup):
+        full_step()
+    full_s = timed(full_step, args.steps)
+    assert torch.equal(full_logits, logits), "full-row logits differ from the row-extent forward's"
+    log(f"e2e full rows: {full_s * 1000 / args.steps:.3f} ms/step, {B * args.steps / full_s:.1f} rows/s")
+    full.close()
+    del full
 
     kernels = measure_kernels(cfg, args.kernel_iters)
     for k, v in kernels.items():
@@ -482,6 +495,7 @@ def main():
         "relbias_softmax_frac_hbm": round(kernels["relbias_softmax"]["gbs"] / HBM_PEAK_GBS, 4),
         "bucket_mix_rows_s": mix,
         "padded_rows_s": round(B * args.steps / padded_s, 2),
+        "full_rows_s": round(B * args.steps / full_s, 2),
         "relative_bias_gbs": round(kernels["relative_bias"]["gbs"], 1),
         "relative_bias_frac_hbm": round(kernels["relative_bias"]["gbs"] / HBM_PEAK_GBS, 4),
     }
