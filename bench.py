@@ -432,8 +432,10 @@ def main():
     ms = elapsed * 1000 / args.steps
     rows_s = B * args.steps / elapsed
     assert torch.isfinite(logits.float()).all()
+    packed_logits = logits.clone()  # the headline forward's output
     log(f"e2e: {ms:.3f} ms/step, {rows_s:.1f} rows/s (packed rows)")
-    padded = lambda: model.classify_device(ids, mask, markers, mmask, logits)  # noqa: E731
+    padded_logits = torch.empty_like(logits)
+    padded = lambda: model.classify_device(ids, mask, markers, mmask, padded_logits)  # noqa: E731
     for _ in range(args.warmup):
         padded()
     padded_s = timed(padded, args.steps)
@@ -447,7 +449,8 @@ def main():
     for _ in range(args.warmup):
         full_step()
     full_s = timed(full_step, args.steps)
-    assert torch.equal(full_logits, logits), "full-row logits differ from the row-extent forward's"
+    assert torch.equal(full_logits, packed_logits), "full-row logits differ from the packed (headline) forward's"
+    assert torch.equal(full_logits, padded_logits), "full-row logits differ from the padded forward's"
     log(f"e2e full rows: {full_s * 1000 / args.steps:.3f} ms/step, {B * args.steps / full_s:.1f} rows/s")
     full.close()
     del full

@@ -4,6 +4,7 @@
 #include <cmath>
 #include <cstring>
 #include <new>
+#include <stdexcept>
 
 #include "gd_common.hpp"
 #include "gd_kernels.hpp"
@@ -231,6 +232,9 @@ int gd_weight_store_add(gd_weight_store* store, const char* key, const void* hos
     return store->impl.add(key, host_data, dtype, shape, ndim);
   } catch (const std::bad_alloc&) {
     return fail(GD_ERR_OUT_OF_MEMORY, "host allocation failed");
+  } catch (const std::exception& e) {
+    set_error("weight store: %s", e.what());
+    return GD_ERR_INVALID_ARGUMENT;
   }
 }
 
@@ -241,11 +245,31 @@ int gd_weight_store_load_safetensors(gd_weight_store* store, const char* path) {
     return store->impl.load_safetensors(path);
   } catch (const std::bad_alloc&) {
     return fail(GD_ERR_OUT_OF_MEMORY, "host allocation failed");
+  } catch (const std::exception& e) {
+    set_error("%s: %s", path, e.what());
+    return GD_ERR_IO;
   }
 }
 
 int64_t gd_weight_store_count(const gd_weight_store* store) {
   return store ? (int64_t)store->impl.tensors.size() : 0;
+}
+
+int gd_weight_store_get(const gd_weight_store* store, const char* key, int32_t* dtype, int64_t* shape,
+                        int32_t* ndim, const void** host_data, int64_t* nbytes) {
+  clear_error();
+  GD_CHECK_ARG(store && key && dtype && shape && ndim && host_data && nbytes, "null argument");
+  const gd::HostTensor* t = store->impl.find(key);
+  if (!t) {
+    set_error("Missing model weight: %s", key);
+    return GD_ERR_MISSING_WEIGHT;
+  }
+  *dtype = t->dtype;
+  *ndim = (int32_t)t->shape.size();
+  for (size_t i = 0; i < t->shape.size() && i < 8; ++i) shape[i] = t->shape[i];
+  *host_data = t->data.data();
+  *nbytes = (int64_t)t->data.size();
+  return GD_OK;
 }
 
 int gd_classifier_create(gd_classifier** out, const gd_weight_store* store, const gd_config* config, uint32_t flags,

@@ -55,6 +55,16 @@ int64_t HostTensor::numel() const {
   return n;
 }
 
+// Bytes of a tensor of `shape` and element size `es`, or -1 when a
+// dimension is negative or the product overflows int64.
+static int64_t checked_bytes(const std::vector<int64_t>& shape, int64_t es) {
+  int64_t n = es;
+  for (int64_t d : shape) {
+    if (d < 0 || __builtin_mul_overflow(n, d, &n)) return -1;
+  }
+  return n;
+}
+
 std::string HostTensor::shape_string() const {
   std::ostringstream os;
   os << "[";
@@ -117,13 +127,21 @@ class JsonCursor {
     ++i_;
     return true;
   }
+  // A decimal integer in int64 range (anything else marks the header bad).
   bool integer(int64_t& v) {
     ws();
     size_t j = i_;
-    if (j < s_.size() && s_[j] == '-') ++j;
+    const bool neg = j < s_.size() && s_[j] == '-';
+    if (neg) ++j;
     if (j >= s_.size() || s_[j] < '0' || s_[j] > '9') return bad();
-    while (j < s_.size() && s_[j] >= '0' && s_[j] <= '9') ++j;
-    v = std::stoll(s_.substr(i_, j - i_));
+    int64_t acc = 0;
+    while (j < s_.size() && s_[j] >= '0' && s_[j] <= '9') {
+      const int digit = s_[j] - '0';
+      if (__builtin_mul_overflow(acc, (int64_t)10, &acc) || __builtin_add_overflow(acc, (int64_t)digit, &acc))
+        return bad();
+      ++j;
+    }
+    v = neg ? -acc : acc;
     i_ = j;
     return true;
   }
@@ -191,13 +209,11 @@ int WeightStore::add(const std::string& key, const void* data, int dtype, const 
   HostTensor t;
   t.dtype = dtype;
   t.shape.assign(shape, shape + ndim);
-  for (int64_t d : t.shape) {
-    if (d < 0) {
-      set_error("negative dimension for %s", key.c_str());
-      return GD_ERR_INVALID_ARGUMENT;
-    }
+  const int64_t bytes = checked_bytes(t.shape, es);
+  if (bytes < 0) {
+    set_error("negative or overflowing dimensions for %s", key.c_str());
+    return GD_ERR_INVALID_ARGUMENT;
   }
-  const int64_t bytes = t.numel() * es;
   if (bytes > 0 && !data) {
     set_error("null data for %s", key.c_str());
     return GD_ERR_INVALID_ARGUMENT;
@@ -291,8 +307,12 @@ int WeightStore::load_safetensors(const std::string& path) {
     HostTensor t;
     t.dtype = e.dtype;
     t.shape = e.shape;
-    const int64_t bytes = t.numel() * dtype_size(e.dtype);
-    if (e.dtype < 0 || e.begin < 0 || e.end - e.begin != bytes || data_start + e.end > file_size) {
+    // Every check runs before the resize: a negative dimension, an end
+    // before the begin, a size that overflows or a range past the file's end
+    // are header errors.
+    const int64_t bytes = e.dtype < 0 || e.shape.size() > 8 ? -1 : checked_bytes(e.shape, dtype_size(e.dtype));
+    if (bytes < 0 || e.begin < 0 || e.end < e.begin || e.end - e.begin != bytes ||
+        e.end > file_size - data_start) {
       set_error("%s: bad data offsets for %s", path.c_str(), e.key.c_str());
       return GD_ERR_IO;
     }

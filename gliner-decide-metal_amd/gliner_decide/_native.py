@@ -110,6 +110,8 @@ _SIGNATURES = {
     "gd_weight_store_add": (C.c_int, [vp, C.c_char_p, vp, i32, C.POINTER(i64), i32]),
     "gd_weight_store_load_safetensors": (C.c_int, [vp, C.c_char_p]),
     "gd_weight_store_count": (i64, [vp]),
+    "gd_weight_store_get": (C.c_int, [vp, C.c_char_p, C.POINTER(i32), C.POINTER(i64), C.POINTER(i32),
+                                      C.POINTER(vp), C.POINTER(i64)]),
     "gd_classifier_create": (C.c_int, [C.POINTER(vp), vp, C.POINTER(GdConfig), u32, vp]),
     "gd_classifier_destroy": (None, [vp]),
     "gd_classifier_reserve": (C.c_int, [vp, i64, i64, i64, i64]),

@@ -76,7 +76,7 @@ def decode(logits, row: int, tasks) -> list:
     for head, task in enumerate(tasks):
         probs = [float(arr[row, head, i]) for i in range(len(task.labels))]
         if task.multi_label:
-            probs = [1.0 / (1.0 + math.exp(-x)) for x in probs]
+            probs = [_sigmoid(x) for x in probs]
             selected = [i for i, p in enumerate(probs) if p >= 0.5]
             if not selected:
                 selected = [_first_argmax(probs)]
@@ -89,6 +89,13 @@ def decode(logits, row: int, tasks) -> list:
             best = _first_argmax(probs)
             out.append(Prediction(task.name, [task.labels[best]], probs))
     return out
+
+
+def _sigmoid(x: float) -> float:
+    """1 / (1 + exp(-x)) with IEEE overflow: Swift's Double exp returns +inf
+    below x = -709.78 (probability 0), where math.exp raises."""
+    e = math.exp(-x) if -x < 709.78 else math.inf
+    return 1.0 / (1.0 + e)
 
 
 def _first_argmax(values) -> int:

@@ -16,6 +16,7 @@ from . import _native as N
 
 _NP_TO_GD = {np.dtype(np.float16): N.GD_F16, np.dtype(np.float32): N.GD_F32, np.dtype(np.int32): N.GD_I32,
              np.dtype(np.int64): N.GD_I64}
+_GD_TO_NP = {v: k for k, v in _NP_TO_GD.items()}
 
 
 class WeightStore:
@@ -40,6 +41,17 @@ class WeightStore:
 
     def load_safetensors(self, path: str | Path) -> None:
         N.check(self._lib.gd_weight_store_load_safetensors(self._h, str(path).encode()))
+
+    def array(self, key: str) -> np.ndarray:
+        """A copy of the stored tensor `key` (the lookup of WeightStore.array,
+        Weights.swift:35-57); BF16 entries come back as raw uint16."""
+        dtype, ndim, data, nbytes = C.c_int32(), C.c_int32(), C.c_void_p(), C.c_int64()
+        shape = (C.c_int64 * 8)()
+        N.check(self._lib.gd_weight_store_get(self._h, key.encode(), C.byref(dtype), shape, C.byref(ndim),
+                                              C.byref(data), C.byref(nbytes)))
+        np_dtype = _GD_TO_NP.get(dtype.value, np.dtype(np.uint16))
+        raw = C.string_at(data, nbytes.value) if nbytes.value else b""
+        return np.frombuffer(raw, dtype=np_dtype).reshape(tuple(shape[: ndim.value])).copy()
 
     def __len__(self) -> int:
         return int(self._lib.gd_weight_store_count(self._h))

@@ -227,6 +227,13 @@ int gd_weight_store_add(gd_weight_store* store, const char* key, const void* hos
 /* Loads every tensor of a safetensors file (MLX loadArrays, Weights.swift:26-28). */
 int gd_weight_store_load_safetensors(gd_weight_store* store, const char* path);
 int64_t gd_weight_store_count(const gd_weight_store* store);
+/* Looks up `key` (WeightStore.array's lookup, Weights.swift:35-57, without
+ * the shape/dtype checks): writes its dtype (gd_dtype), rank (<= 8) and
+ * shape (shape[0..ndim)), and a pointer to the store's host bytes, valid
+ * until the store is destroyed or the key is replaced.  GD_ERR_MISSING_WEIGHT
+ * when absent. */
+int gd_weight_store_get(const gd_weight_store* store, const char* key, int32_t* dtype, int64_t* shape,
+                        int32_t* ndim, const void** host_data, int64_t* nbytes);
 
 /* ------------------------------------------------------------------------ *
  * Classifier context -- GLiNERDecideClassifier (DeBERTa.swift:156-447)

@@ -119,6 +119,25 @@ def test_safetensors_roundtrip(tmp_path):
     save_file(w, str(path), metadata={"precision": "float16", "scope": "encoder+classification-only"})
     store = WeightStore(url=path)
     assert len(store) == len(w)
+    # every tensor reads back with its shape, dtype and bytes (a wrong data
+    # offset, header base or dtype mapping would show here)
+    for key, arr in w.items():
+        got = store.array(key)
+        assert got.dtype == arr.dtype and got.shape == arr.shape, key
+        np.testing.assert_array_equal(got.view(np.uint16), arr.view(np.uint16), err_msg=key)
+    # mixed dtypes and ranks: offsets of later tensors depend on the sizes of earlier ones
+    mixed = {"a": np.arange(6, dtype=np.float32).reshape(2, 3), "b": np.array([7, -9], np.int64),
+             "c": np.arange(5, dtype=np.int32), "d": np.float16(1.5) * np.ones((3, 1, 2), np.float16),
+             "s": np.array(3.25, np.float32)}
+    save_file(mixed, str(tmp_path / "m.safetensors"))
+    ms = WeightStore(url=tmp_path / "m.safetensors")
+    for key, arr in mixed.items():
+        got = ms.array(key)
+        assert got.dtype == arr.dtype and got.shape == arr.shape, key
+        np.testing.assert_array_equal(got, arr)
+    with pytest.raises(N.GlinerDecideError) as e:
+        ms.array("missing")
+    assert e.value.status == N.GD_ERR_MISSING_WEIGHT
     bad = tmp_path / "bad.safetensors"
     bad.write_bytes(b"\x10\x00\x00\x00\x00\x00\x00\x00{not json")
     with pytest.raises(N.GlinerDecideError) as e:
@@ -126,3 +145,42 @@ def test_safetensors_roundtrip(tmp_path):
     assert e.value.status == N.GD_ERR_IO
     with pytest.raises(N.GlinerDecideError):
         WeightStore(url=tmp_path / "nope.safetensors")
+
+
+def _raw_safetensors(path, header: bytes, payload: bytes = b"\0" * 16):
+    import struct
+    path.write_bytes(struct.pack("<Q", len(header)) + header + payload)
+    return path
+
+
+@pytest.mark.parametrize("header", [
+    # negative dimension with end < begin: both sides of the size check are -2
+    b'{"x": {"dtype": "F16", "shape": [-1], "data_offsets": [2, 0]}}',
+    # an integer beyond int64
+    b'{"x": {"dtype": "F16", "shape": [99999999999999999999999], "data_offsets": [0, 2]}}',
+    # a size that overflows int64 while every dimension fits
+    b'{"x": {"dtype": "F16", "shape": [4294967296, 4294967296], "data_offsets": [0, 0]}}',
+    # a range past the end of the file
+    b'{"x": {"dtype": "F16", "shape": [64], "data_offsets": [0, 128]}}',
+    # end before begin with a matching (negative) size is still rejected
+    b'{"x": {"dtype": "F16", "shape": [], "data_offsets": [4, 2]}}',
+])
+def test_safetensors_malformed_headers_return_io_error(tmp_path, header):
+    """Crafted headers are rejected with GD_ERR_IO; the process survives."""
+    from gliner_decide.weights import WeightStore
+    with pytest.raises(N.GlinerDecideError) as e:
+        WeightStore(url=_raw_safetensors(tmp_path / "h.safetensors", header))
+    assert e.value.status == N.GD_ERR_IO
+
+
+def test_weight_store_add_rejects_overflowing_shape():
+    from gliner_decide.weights import WeightStore
+    import ctypes as C
+    store = WeightStore()
+    shape = (C.c_int64 * 2)(1 << 40, 1 << 40)
+    buf = np.zeros(4, np.float16)
+    assert N.lib().gd_weight_store_add(store.handle, b"x", buf.ctypes.data_as(C.c_void_p), N.GD_F16, shape, 2) \
+        == N.GD_ERR_INVALID_ARGUMENT
+    shape = (C.c_int64 * 1)(-3)
+    assert N.lib().gd_weight_store_add(store.handle, b"x", buf.ctypes.data_as(C.c_void_p), N.GD_F16, shape, 1) \
+        == N.GD_ERR_INVALID_ARGUMENT

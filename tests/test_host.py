@@ -176,3 +176,15 @@ def test_prepare_weights_filters_and_casts(tmp_path):
     save_file(src, str(tmp_path / "partial.safetensors"))
     with pytest.raises(RuntimeError, match="missing required weights: \\['classifier.2.weight'\\]"):
         prepare_weights(tmp_path / "partial.safetensors", tmp_path / "o3")
+
+
+def test_decode_multi_label_extreme_logits():
+    """fp16 logits reach -65504: the sigmoid is 0 there (IEEE exp overflow to
+    +inf, as Swift's Double exp), not an exception; the argmax fallback still
+    picks the largest."""
+    logits = np.array([[[-800.0, 3.0, -65504.0]], [[-65504.0, -900.0, -1000.0]]], np.float32)
+    tasks = [DecisionTask("m", ("a", "b", "c"), True)]
+    p0 = decode(logits, 0, tasks)[0]
+    assert p0.labels == ["b"] and p0.probabilities[0] == 0.0 and p0.probabilities[2] == 0.0
+    p1 = decode(logits, 1, tasks)[0]
+    assert p1.probabilities == [0.0, 0.0, 0.0] and p1.labels == ["a"]  # first of equal maxima
