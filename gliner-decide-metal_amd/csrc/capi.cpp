@@ -113,44 +113,21 @@ int gd_linear(const void* a, const void* w, const void* bias, void* c, int64_t m
                        as_stream(stream));
 }
 
-int gd_relative_bias(const void* q, const void* k, const void* pos_key, const void* pos_query,
-                     const int32_t* c2p_indices, const int32_t* p2c_indices, const void* key_mask, float scale,
-                     int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim, int64_t positions, void* out,
-                     void* stream) {
-  clear_error();
-  GD_CHECK_ARG(q && k && pos_key && pos_query && c2p_indices && p2c_indices && key_mask && out,
-               "null tensor pointer");
-  GD_CHECK_SHAPE(batch >= 0 && heads > 0 && seq_len > 0 && head_dim > 0 && positions > 0,
-                 "dimensions must be positive");
-  GD_CHECK_SHAPE(head_dim <= 4096, "head_dim too large");
-  GD_CHECK_SHAPE(batch * heads * seq_len <= 0x7fffffff, "too many rows");
-  return launch_relative_bias_general(q, k, pos_key, pos_query, c2p_indices, p2c_indices, key_mask, scale, batch,
-                                      heads, seq_len, head_dim, positions, out, nullptr, as_stream(stream));
-}
+namespace {
 
-int gd_fused_attention(const void* q, const void* k, const void* v, const void* pos_key, const void* pos_query,
-                       const int32_t* c2p_indices, const int32_t* p2c_indices, const void* key_mask, float scale,
-                       int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim, int64_t positions, void* out,
-                       void* stream) {
-  clear_error();
-  GD_CHECK_ARG(q && k && v && pos_key && pos_query && c2p_indices && p2c_indices && key_mask && out,
-               "null tensor pointer");
-  GD_CHECK_SHAPE(batch >= 0 && heads > 0 && seq_len > 0 && head_dim > 0 && positions > 0,
-                 "dimensions must be positive");
-  GD_CHECK_SHAPE((head_dim + seq_len) * 4 <= 64 * 1024, "seq_len + head_dim exceed the kernel's LDS budget");
-  GD_CHECK_SHAPE(batch * heads * seq_len <= 0x7fffffff, "too many rows");
-  return launch_fused_attention_general(q, k, v, pos_key, pos_query, c2p_indices, p2c_indices, key_mask, scale, batch,
-                                        heads, seq_len, head_dim, positions, out, nullptr, as_stream(stream));
-}
-
-int gd_deberta_attention(gd_bhld q, gd_bhld k, gd_bhld v, gd_table pos_key, gd_table pos_query, const void* mask,
-                         int32_t mask_kind, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
-                         int64_t positions, int32_t bucket_size, int32_t output, void* out, int64_t ldo,
-                         void* stream) {
-  clear_error();
+// Checks a closed-form-index attention call and launches it (shared by
+// gd_deberta_attention and the closed-form paths of gd_relative_bias /
+// gd_fused_attention).
+int deberta_attention_checked(gd_bhld q, gd_bhld k, gd_bhld v, gd_table pos_key, gd_table pos_query,
+                              const void* mask, int32_t mask_kind, int64_t batch, int64_t heads, int64_t seq_len,
+                              int64_t head_dim, int64_t positions, int32_t bucket_size, int32_t output, int score,
+                              float scale_rel, void* out, int64_t ldo, hipStream_t stream) {
   GD_CHECK_ARG(q.data && k.data && pos_key.data && pos_query.data && mask && out, "null tensor pointer");
   GD_CHECK_ARG(output == GD_ATTN_OUT_PROBS || output == GD_ATTN_OUT_CONTEXT || output == GD_ATTN_OUT_BIAS,
                "unknown output kind %d", output);
+  GD_CHECK_ARG(score >= kScoreDefault && score <= kScoreFused, "unknown score chain %d", score);
+  GD_CHECK_ARG(output != GD_ATTN_OUT_BIAS || score == kScoreDefault || score == kScoreKernelBias,
+               "the bias output exists for the default and the kernel-bias score chains only");
   GD_CHECK_ARG(output != GD_ATTN_OUT_CONTEXT || v.data, "context output needs v");
   GD_CHECK_ARG(mask_kind == GD_MASK_ATTENTION || mask_kind == GD_MASK_ADDITIVE, "unknown mask kind %d", mask_kind);
   GD_CHECK_SHAPE(head_dim == 64, "head_dim must be 64 (got %lld)", (long long)head_dim);
@@ -201,9 +178,78 @@ int gd_deberta_attention(gd_bhld q, gd_bhld k, gd_bhld v, gd_table pos_key, gd_t
   a.scale_qk = 1.0f / std::sqrt((float)(3 * head_dim));
   a.scale16 = (float)(_Float16)std::sqrt((float)(3 * head_dim));
   a.output = output;
+  a.score = score;
+  a.scale_rel = scale_rel;
   a.out = out;
   a.ldo = ldo;
-  return launch_deberta_attention(a, as_stream(stream));
+  return launch_deberta_attention(a, stream);
+}
+
+}  // namespace
+
+int gd_relative_bias(const void* q, const void* k, const void* pos_key, const void* pos_query,
+                     const int32_t* c2p_indices, const int32_t* p2c_indices, const void* key_mask, float scale,
+                     int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim, int64_t positions, void* out,
+                     void* stream) {
+  clear_error();
+  GD_CHECK_ARG(q && k && pos_key && pos_query && key_mask && out, "null tensor pointer");
+  GD_CHECK_ARG((c2p_indices == nullptr) == (p2c_indices == nullptr),
+               "give both index tensors, or neither for the closed-form indices");
+  GD_CHECK_SHAPE(batch >= 0 && heads > 0 && seq_len > 0 && head_dim > 0 && positions > 0,
+                 "dimensions must be positive");
+  if (c2p_indices == nullptr) {
+    // Closed-form indices (the ones the classifier builds, DeBERTa.swift:498-519):
+    // the MFMA attention kernel's kernel-bias chain with the bias output.
+    const int64_t HLD = heads * seq_len * head_dim, LD = seq_len * head_dim;
+    return deberta_attention_checked(gd_bhld{q, HLD, LD, head_dim}, gd_bhld{k, HLD, LD, head_dim}, gd_bhld{},
+                                     gd_table{pos_key, positions * head_dim, head_dim},
+                                     gd_table{pos_query, positions * head_dim, head_dim}, key_mask, GD_MASK_ADDITIVE,
+                                     batch, heads, seq_len, head_dim, positions, 256, GD_ATTN_OUT_BIAS,
+                                     kScoreKernelBias, scale, out, seq_len, as_stream(stream));
+  }
+  GD_CHECK_SHAPE(head_dim <= 4096, "head_dim too large");
+  GD_CHECK_SHAPE(batch * heads * seq_len <= 0x7fffffff, "too many rows");
+  return launch_relative_bias_general(q, k, pos_key, pos_query, c2p_indices, p2c_indices, key_mask, scale, batch,
+                                      heads, seq_len, head_dim, positions, out, nullptr, as_stream(stream));
+}
+
+int gd_fused_attention(const void* q, const void* k, const void* v, const void* pos_key, const void* pos_query,
+                       const int32_t* c2p_indices, const int32_t* p2c_indices, const void* key_mask, float scale,
+                       int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim, int64_t positions, void* out,
+                       void* stream) {
+  clear_error();
+  GD_CHECK_ARG(q && k && v && pos_key && pos_query && key_mask && out, "null tensor pointer");
+  GD_CHECK_ARG((c2p_indices == nullptr) == (p2c_indices == nullptr),
+               "give both index tensors, or neither for the closed-form indices");
+  GD_CHECK_SHAPE(batch >= 0 && heads > 0 && seq_len > 0 && head_dim > 0 && positions > 0,
+                 "dimensions must be positive");
+  if (c2p_indices == nullptr) {
+    // Closed-form indices: the MFMA attention kernel's fused chain; its
+    // context rows [B, L, H*D] are the [B, L, H, D] output.
+    const int64_t HLD = heads * seq_len * head_dim, LD = seq_len * head_dim;
+    return deberta_attention_checked(gd_bhld{q, HLD, LD, head_dim}, gd_bhld{k, HLD, LD, head_dim},
+                                     gd_bhld{v, HLD, LD, head_dim}, gd_table{pos_key, positions * head_dim, head_dim},
+                                     gd_table{pos_query, positions * head_dim, head_dim}, key_mask, GD_MASK_ADDITIVE,
+                                     batch, heads, seq_len, head_dim, positions, 256, GD_ATTN_OUT_CONTEXT,
+                                     kScoreFused, scale, out, heads * head_dim, as_stream(stream));
+  }
+  GD_CHECK_SHAPE((head_dim + seq_len) * 4 <= 64 * 1024, "seq_len + head_dim exceed the kernel's LDS budget");
+  GD_CHECK_SHAPE(batch * heads * seq_len <= 0x7fffffff, "too many rows");
+  return launch_fused_attention_general(q, k, v, pos_key, pos_query, c2p_indices, p2c_indices, key_mask, scale, batch,
+                                        heads, seq_len, head_dim, positions, out, nullptr, as_stream(stream));
+}
+
+int gd_deberta_attention(gd_bhld q, gd_bhld k, gd_bhld v, gd_table pos_key, gd_table pos_query, const void* mask,
+                         int32_t mask_kind, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+                         int64_t positions, int32_t bucket_size, int32_t output, void* out, int64_t ldo,
+                         void* stream) {
+  clear_error();
+  const int32_t kind = output & 0xff, score = (output >> 8) & 0xff;
+  GD_CHECK_ARG((output & ~0xffff) == 0, "unknown output bits 0x%x", output);
+  // the Metal kernels' scale: 1 / sqrt(3 D) in fp32 (DeBERTa.swift:347,366)
+  const float scale_rel = head_dim > 0 ? 1.0f / std::sqrt((float)(3 * head_dim)) : 0.f;
+  return deberta_attention_checked(q, k, v, pos_key, pos_query, mask, mask_kind, batch, heads, seq_len, head_dim,
+                                   positions, bucket_size, kind, score, scale_rel, out, ldo, as_stream(stream));
 }
 
 int gd_relative_index_table(int32_t* out, int32_t n, int32_t bucket_size, int32_t max_position, void* stream) {
@@ -276,7 +322,8 @@ int gd_classifier_create(gd_classifier** out, const gd_weight_store* store, cons
                          void* stream) {
   clear_error();
   GD_CHECK_ARG(out && store, "null output or store");
-  GD_CHECK_ARG((flags & ~(GD_USE_FUSED_KERNELS | GD_USE_COMPILED_GRAPH | GD_USE_GENERIC_ATTENTION | GD_FULL_ROWS)) == 0,
+  GD_CHECK_ARG((flags & ~(GD_USE_FUSED_KERNELS | GD_USE_COMPILED_GRAPH | GD_USE_GENERIC_ATTENTION | GD_FULL_ROWS |
+                          GD_USE_CUSTOM_RELATIVE_KERNEL | GD_USE_FUSED_ATTENTION_KERNEL)) == 0,
                "unknown flags 0x%x", flags);
   gd_config cfg;
   if (config) {

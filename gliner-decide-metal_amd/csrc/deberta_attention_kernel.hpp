@@ -1,0 +1,931 @@
+// Disentangled attention of the DeBERTa-v3 encoder (the hot path).
+//
+// Reference: DeBERTa.swift:322-395 (relative bias from the fp16 c2pRaw/p2cRaw
+// gathers, additive key mask, SDPA) with the index math of :498-551.
+//
+// One work item = (batch b, head h, 128 queries), run by a workgroup of 8
+// waves, wave w owning queries q0 + 16w .. q0 + 16w + 15.  The LDS holds one
+// workgroup per CU; up to L = 256 the grid has one workgroup per CU, each
+// looping over items and fetching the next item's first stage while it
+// finishes the current one.  Keys stream through LDS in chunks of 64.  For
+// a chunk, every relative index the workgroup can need, idx(q - k) for its
+// 128 queries and the chunk's 64 keys, lies in one window of at most 191
+// consecutive rows of the relative tables (idx is monotone in q - k), so the
+// stage of a chunk is
+//     K rows        64 x 128 B
+//     posK window  192 x 128 B   (relative keys, for c2p)
+//     posQ window  192 x 128 B   (relative queries, for p2c)
+// fetched with global_load_lds_dwordx4 (16 B per lane straight into LDS; the
+// XOR swizzle of the 128-byte rows is applied on the global side) into one of
+// two buffers while the other chunk is computed.  Inside a chunk nothing
+// touches global memory:
+//   c2p  per wave: C2P^T = posK[window] . Q^T over <= 80 positions (5 MFMA
+//        column tiles, v_mfma_f32_16x16x32_f16), rounded to fp16 (the
+//        reference's c2pRaw) into a per-wave LDS tile;
+//   per 16-key tile: S^T = K Q^T (2 MFMAs) and P2C = K . posQ[window]^T over
+//        <= 31 positions (4 MFMAs), fp16 into a per-wave LDS tile; each score
+//        gathers its two terms by idx and applies the reference rounding
+//        chain fp16(fp16(c2p + p2c) / fp16(sqrt(3D))).
+// Scores stay in registers (a lane owns one query column and 4 keys per
+// tile), the softmax reduces in registers plus two cross-lane steps, and the
+// outputs leave through LDS as 16-byte row segments: P rows (probabilities),
+// the SDPA additive mask (bias), or the context P.V (V^T chunks in LDS, P as
+// the MFMA A operand split into fp16 hi + lo parts).
+//
+// This header holds the kernel template; deberta_attention.hip holds the
+// per-forward helper kernels (row extents, item schedule, packed rows) and
+// the relative index table, and each attention_sm_*.hip instantiates one
+// score mode.
+#pragma once
+
+#include <atomic>
+#include <climits>
+#include <cmath>
+#include <mutex>
+#include <type_traits>
+#include "gd_common.hpp"
+#include "gd_kernels.hpp"
+
+namespace gd {
+
+// Compute units of the current device (cached per device).
+int device_cu_count();
+
+namespace {
+
+constexpr int kThreads = 512;
+constexpr int kWaves = 8;
+constexpr int kQT = 128;           // queries per workgroup
+constexpr int kKC = 64;            // keys per chunk
+constexpr int kD = 64;             // head dim
+constexpr int kWin = 192;          // relative-table rows per chunk window (>= 191)
+constexpr int kMid = 128;          // |q - k| <= kMid: idx(q - k) = q - k + 256 (bucket size 256)
+constexpr int kC2PCols = 80;       // per-wave c2p window (<= 79 positions)
+constexpr int kC2PStride = kC2PCols + 4;  // 168-byte rows keep the 8-byte stores aligned
+// Per-wave p2c tile (16 keys x 32 window positions), stored skewed: value
+// (key row kr, position p) at (kr + p) * kP2CSkew + kr.  A score's four keys
+// 4g .. 4g+3 in the linear zone share kr + p = 15 + lc, so its four p2c terms
+// are one aligned 8-byte read; rows of 24 halfs make those reads
+// conflict-free across the wave.
+constexpr int kP2CSkew = 24;
+constexpr int kP2CRows = 47;       // kr + p <= 15 + 31
+constexpr int kVRowsA = 448;       // V rows held by one stage buffer (448 x 128 B = 56 KiB)
+
+// LDS map (halfs).  The stage buffers are reused for the V^T chunks and the
+// output staging once the score loop is done.
+constexpr int kStageK = kKC * kD;                 // 4096
+constexpr int kStageWin = kWin * kD;              // 12288
+constexpr int kStage = kStageK + 2 * kStageWin;   // 28672 halfs = 56 KiB
+// The kernel-bias and fused chains keep c2p and p2c in fp32 (the Metal
+// kernels never round them): per wave and key tile, c2p [16 queries][33]
+// over the tile's 32 positions (33-float rows spread a wave's gathers over
+// the banks) and p2c skewed as above in rows of 16 floats whose 16-byte block
+// index is XORed with bits 2..3 of the row (a linear-zone read of four p2c
+// terms is one conflict-free 16-byte read).
+constexpr int kC2PF32Stride = 33;
+constexpr int kScratchWave16 = 16 * kC2PStride + kP2CRows * kP2CSkew;       // halfs
+constexpr int kScratchWave32 = (16 * kC2PF32Stride + kP2CRows * 16) * 2;    // halfs
+constexpr int kScratchWave = kScratchWave16 > kScratchWave32 ? kScratchWave16 : kScratchWave32;
+static_assert(16 * 72 <= kScratchWave, "context staging fits a wave's scratch");
+static_assert((16 * kC2PF32Stride * 4) % 16 == 0 && (kScratchWave * 2) % 16 == 0, "fp32 p2c tile alignment");
+
+// The relative index table holds idx(r) for every r in [-kRelSpan, kRelSpan]
+// (bucket size 256, 512 positions) at entry r + kRelSpan.
+constexpr int kRelSpan = 511;
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) half_t lds_half_t;
+typedef short short4_t __attribute__((ext_vector_type(4)));
+
+
+// 16-byte direct-to-LDS load (global_load_lds_dwordx4: lane l's 16 bytes land
+// at M0 + 16 l), issued as inline assembly.  The compiler cannot tell which
+// LDS buffer the builtin form writes once stage pointers are merged across
+// the unrolled chunks, so it would drain every load in flight (vmcnt(0))
+// before each later LDS read and serialise the stage pipeline; here the
+// pipeline orders these loads itself (vmcnt(0) + barrier before a stage is
+// read).  M0 is not used by anything else in this kernel.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void load_lds16(const half_t* g, lds_half_t* lds_block) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_block);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
+}
+// The same with a wave-uniform base address and a 32-bit byte offset per lane.
+__device__ __forceinline__ void load_lds16(const half_t* sbase, uint32_t voff, lds_half_t* lds_block) {
+  // (readfirstlane returns int: each half goes through uint32_t so that the
+  // low half is not sign-extended into the high one)
+  const uint64_t a = (uint64_t)(uintptr_t)sbase;
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
+  sbase = (const half_t*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_block);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(m0)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// 128-byte rows; the 16-byte chunk index is XORed with bits 1..3 of the row.
+// gfx950's LDS serves a ds_read_b128 16 lanes at a time over 64 banks
+// (256 B): 16 consecutive rows at the same logical chunk then land on 16
+// distinct (row parity, chunk) bank groups -- conflict-free.
+__device__ __forceinline__ int swz(int row, int chunk) { return row * kD + ((chunk ^ ((row >> 1) & 7)) << 3); }
+
+// Workgroups loop over items up to L = 256 (16 key tiles).
+template <int MAXT>
+constexpr bool attention_persistent() {
+  return MAXT <= 16;
+}
+
+// SM selects the score chain (AttentionScore): the bias term (the default
+// graph's fp16 chain, or the Metal kernels' fp32 c2p + p2c) and how it meets
+// q.k (SDPA with an additive mask, the explicit fp16 chain, or the fused
+// kernel's single fp32 sum).
+template <int MAXT, int OUT, int SM>
+__global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
+    const half_t* __restrict__ Q, const half_t* __restrict__ K, const half_t* __restrict__ V, int qsb, int qsh,
+    int qsl, int ksb, int ksh, int ksl, int vsb, int vsh, int vsl, const half_t* __restrict__ PK,
+    const half_t* __restrict__ PQ, int pksh, int pksp, int pqsh, int pqsp, const half_t* __restrict__ mask,
+    int mask_kind, const int* __restrict__ row_len, const int* __restrict__ row_off, const int* __restrict__ q_len,
+    const int* __restrict__ sched,
+    int n_sched, int B, int H, int L, int P, int bucket_size, float scale_qk, float scale16, float scale_rel,
+    const int16_t* __restrict__ rel_idx, half_t* __restrict__ out, int ldo) {
+  // fp32 c2p / p2c per key tile (the Metal kernels' arithmetic)
+  constexpr bool B32 = SM == kScoreKernelBias || SM == kScoreKernelBiasExplicit || SM == kScoreFused;
+  // explicit-score chain: fp16 content score, fp16 P (DeBERTa.swift:397-409)
+  constexpr bool GENC = SM == kScoreExplicit || SM == kScoreKernelBiasExplicit;
+  // Two stage buffers and the per-wave scratch.  The stage DMA is inline
+  // assembly the compiler does not track, so its reads of a stage never wait
+  // for the next stage's loads in flight; the kernel orders them itself
+  // (vmcnt + barrier before a stage is read).
+  __shared__ __attribute__((aligned(1024))) half_t stages[2 * kStage];  // stage buffers 0 and 1
+  __shared__ __attribute__((aligned(1024))) half_t scratch_lds[kWaves * kScratchWave];
+  __shared__ int16_t idx_tab[2 * 16 * MAXT];
+  __shared__ __attribute__((aligned(16))) float mask_add[16 * MAXT];
+
+  // The stage buffers as LDS pointers: the DMA and the transposing reads
+  // address them through these (no generic-to-LDS casts of computed pointers).
+  lds_half_t* const stages3 = (lds_half_t*)(lds_void_t*)stages;
+  constexpr bool kPersistent = attention_persistent<MAXT>();
+  const int ntq = (L + kQT - 1) / kQT;
+  const int nblk = B * H * ntq;
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  // Wave-uniform values live in scalar registers: branches on them are scalar
+  // and their address arithmetic runs once per wave, not per lane.
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int lc = lane & 15;  // MFMA output column: the lane's query
+  const int g = lane >> 4;   // lane group
+  const float inv_scale16 = 1.0f / scale16;  // correctly rounded fp32 reciprocal
+  half_t* c2p_w = scratch_lds + wave * kScratchWave;
+  half_t* p2c_w = c2p_w + 16 * kC2PStride;
+  float* const c2pf = reinterpret_cast<float*>(c2p_w);  // fp32 chains
+  float* const p2cf = c2pf + 16 * kC2PF32Stride;
+
+  // ---- stage loads: lane l of 1 KiB block `blk` writes physical chunk l%8 of
+  // row 8*blk + l/8, so it fetches the logical chunk that swz() puts there.
+  // Every block this wave loads has the parity of the wave index.  `wlo` is
+  // the relative-table row at window row 0.  The chunk's pairs have
+  // q - k in [bot, top = bot + 190], bot = q0 - kc - 63.  When bot or top lies
+  // in the linear zone [-128, 128], wlo is the linear extrapolation bot + 256:
+  // every index the chunk needs lies in [wlo, wlo + 190] (log buckets keep
+  // |bucket(r)| <= |r| and stay beyond the linear zone's ends), and every
+  // wave whose own pairs are all linear finds its rows at closed-form,
+  // 16-aligned offsets.  Otherwise wlo = idx(bot).  wlo is then clamped to
+  // [0, 512 - 192] so that every window row exists (the indices lie in
+  // [0, 511]); the clamp moves only windows with no all-linear wave (their
+  // bot lies in (64, 128] or below -256). ----
+  const int blk_row = lane >> 3;
+  const int blk_chunk = (lane & 7) ^ (((wave & 1) << 2) | (lane >> 4));
+  // byte offsets of this lane's 16-byte piece from a block's first table row
+  const uint32_t pk_lane = (uint32_t)((blk_row * pksp + blk_chunk * 8) * 2);
+  const uint32_t pq_lane = (uint32_t)((blk_row * pqsp + blk_chunk * 8) * 2);
+  auto window_lo = [&](int q0, int kc, auto&& idx_of) -> int {
+    const int bot = q0 - kc - (kKC - 1), top = bot + kQT + kKC - 2;
+    const bool lin = (bot >= -kMid && bot <= kMid) || (top >= -kMid && top <= kMid);
+    const int w = lin ? bot + bucket_size : idx_of(bot);
+    return w < 0 ? 0 : (w > 512 - kWin ? 512 - kWin : w);
+  };
+  // Stage of key chunk kc into buffer st: kStageOps DMA instructions per wave.
+  auto issue_stage = [&](lds_half_t* st, const half_t* Kb, const half_t* PKh, const half_t* PQh, int kc, int wlo,
+                         int klim) {
+    {  // K rows: 8 blocks of 8 rows, one per wave; rows from klim on repeat row klim - 1
+      int key = kc + wave * 8 + blk_row;
+      key = key < klim ? key : klim - 1;
+      load_lds16(Kb + (int64_t)key * ksl + blk_chunk * 8, st + wave * 512);
+    }
+#pragma unroll
+    for (int j = 0; j < kWin / 8 / kWaves; ++j) {  // 3 blocks per wave per table; rows wlo .. wlo + 191 exist
+      const int blk = wave + kWaves * j;
+      const int p0 = wlo + blk * 8;  // uniform
+      load_lds16(PKh + (int64_t)p0 * pksp, pk_lane, st + kStageK + blk * 512);
+      load_lds16(PQh + (int64_t)p0 * pqsp, pq_lane, st + kStageK + kStageWin + blk * 512);
+    }
+  };
+  constexpr int kStageOps = 1 + 2 * (kWin / 8 / kWaves);
+  auto rel_arith = [&](int r) -> int {  // idx(r) computed: no memory wait in front of a DMA
+    return relative_index(r < -(L - 1) ? -(L - 1) : r, 256, 512);
+  };
+
+  // ---- work items: (b, h, 128-query tile).  Up to L = 256 the grid holds
+  // at most one workgroup per CU (the LDS allows no more) and workgroup w
+  // takes items w, w + gridDim.x, ...; beyond, the scores fill the registers
+  // and every workgroup takes one item.  Item ids map so that a (b, h)'s query tiles share an
+  // XCD.  Each item's first stage and per-thread set-up reads are issued
+  // while the previous item finishes (last chunk, softmax, P.V, stores), into
+  // the stage buffer that item no longer needs. ----
+  // `len` is the item's row extent: positions from len on take no part (keys
+  // past it are neither read nor weighted, queries past it are not computed);
+  // L without a row-extent array.  `klim` = max(len, 1) bounds row reads.
+  // `row0` is the token row of (b, 0) with packed rows (row_off[b]), else -1.
+  // `qlen` (<= len) bounds the queries computed and stored: q_len[b] when
+  // given (only the rows a later step reads), else len.
+  struct Item {
+    int b, h, qt, len, klim, row0, qlen;
+  };
+  // Q / K / V of (b, h): row 0 of the batch row's slice.
+  auto slice_base = [&](const half_t* X, const int b, const int h, const int row0, int sb, int sh, int sl) {
+    return X + (row0 >= 0 ? (int64_t)row0 * sl : (int64_t)b * sb) + (int64_t)h * sh;
+  };
+  // Remap: item w + j gridDim.x (workgroup w on XCD w % 8, round j) becomes
+  // local index l = w / 8 + j G (G = gridDim.x / 8) of XCD w % 8's contiguous
+  // share, so the two query tiles of a (b, h) (l = 2m, 2m + 1 at L = 256) run
+  // side by side on one XCD and share their K, V and table reads through its
+  // L2.  On odd rounds l is swapped with its partner (l ^ 1): a workgroup's
+  // successive items alternate between the pair's query tiles, which differ
+  // in cost under row extents (when G and the share are even, the pairs stay
+  // within a round).
+  const bool swap_rounds = ((nblk >> 3) & 1) == 0 && ((gridDim.x >> 3) & 1) == 0 && gridDim.x >= 8;
+  // With a schedule (row extents; built per forward by
+  // attention_schedule_kernel) item slot s holds bh * ntq + qt, or -1 for an
+  // empty slot, which runs as a query tile past every row's extent.
+  const int n_items = sched != nullptr ? n_sched : nblk;
+  auto decode = [&](int item) -> Item {
+    int bid = item;
+    bool empty = false;
+    if (sched != nullptr) {
+      bid = __builtin_amdgcn_readfirstlane(sched[item]);
+      empty = bid < 0;
+      bid = empty ? 0 : bid;
+    } else if ((nblk & 7) == 0) {
+      int l = bid >> 3;
+      if (swap_rounds) l ^= (l / (int)(gridDim.x >> 3)) & 1;
+      bid = (bid & 7) * (nblk >> 3) + l;
+    }
+    const int bh = bid / ntq;
+    const int b = __builtin_amdgcn_readfirstlane(bh / H);
+    int len = L;
+    if (row_len != nullptr) {
+      len = __builtin_amdgcn_readfirstlane(row_len[b]);
+      len = len < 0 ? 0 : (len > L ? L : len);
+    }
+    const int row0 = row_off != nullptr ? __builtin_amdgcn_readfirstlane(row_off[b]) : -1;
+    int qlen = len;
+    if (q_len != nullptr) {
+      qlen = __builtin_amdgcn_readfirstlane(q_len[b]);
+      qlen = qlen < 0 ? 0 : (qlen > len ? len : qlen);
+    }
+    return Item{b, __builtin_amdgcn_readfirstlane(bh % H), empty ? ntq : __builtin_amdgcn_readfirstlane(bid % ntq), len,
+                len > 0 ? len : 1, row0, qlen};
+  };
+  // Window start of chunk 0 per query tile (at most 4), lane qt of w0_tab.
+  const int w0_tab = window_lo(kQT * (lane & 3), 0, rel_arith);
+  auto stage0_of = [&](const Item& it, lds_half_t* st) {
+    issue_stage(st, slice_base(K, it.b, it.h, it.row0, ksb, ksh, ksl), PK + (int64_t)it.h * pksh,
+                PQ + (int64_t)it.h * pqsh, 0, __builtin_amdgcn_readlane(w0_tab, it.qt), it.klim);
+  };
+  // Per-thread set-up reads of an item: its key-mask entry, its lane of the
+  // window table and the Q fragments.  Window table (read with readlane):
+  // lane T < MAXT holds idx(qw - 16 T - 15), the first p2c position of key
+  // tile T; lane 32 + c holds idx(qw - 64 c - 63), the first c2p position of
+  // chunk c; lane 48 + c holds wlo of chunk c.
+  static_assert(2 * kThreads >= 2 * 16 * MAXT - 1 && kThreads >= 16 * MAXT, "one pass of set-up reads");
+  struct Setup {
+    half8_t qf0, qf1;  // Q[qw + lc][8g..] and [32 + 8g..] (B operand of K Q^T)
+    int win_tab;
+    half_t mval;
+  };
+  // The global loads are unconditional (clamped rows; values of rows past
+  // the sequence are never used) and the window indices come from the LDS
+  // index table.  An item's set-up reads are issued before its stage DMA: any
+  // vmcnt wait the compiler places among them (it does not count the DMA,
+  // which is inline assembly) then cannot wait for that DMA.
+  auto rel_lds = [&](int r) -> int {
+    r = r < -(L - 1) ? -(L - 1) : (r > L - 1 ? L - 1 : r);
+    return idx_tab[r + L - 1];
+  };
+  auto setup_of = [&](const Item& it) -> Setup {
+    Setup su;
+    const int q0 = it.qt * kQT, qw = q0 + 16 * wave;
+    su.mval = mask[(int64_t)it.b * L + (t < L ? t : L - 1)];
+    if (lane < 32)
+      su.win_tab = rel_lds(qw - 16 * lane - 15);
+    else if (lane < 48)
+      su.win_tab = rel_lds(qw - kKC * (lane - 32) - (kKC - 1));
+    else
+      su.win_tab = window_lo(q0, kKC * (lane - 48), rel_lds);
+    const int qr = qw + lc < it.klim ? qw + lc : it.klim - 1;
+    const half_t* qrow = slice_base(Q, it.b, it.h, it.row0, qsb, qsh, qsl) + (int64_t)qr * qsl;
+    su.qf0 = *reinterpret_cast<const half8_t*>(qrow + 8 * g);
+    su.qf1 = *reinterpret_cast<const half8_t*>(qrow + 32 + 8 * g);
+    return su;
+  };
+
+  int item = blockIdx.x;
+  Item cur = decode(item);
+  stage0_of(cur, stages3);
+  // The index table, the same for every item, is built once.
+  const int n_idx = 2 * L - 1;
+  const int16_t id0 = t < n_idx ? rel_idx[t - (L - 1) + kRelSpan] : (int16_t)0;
+  const int16_t id1 = t + kThreads < n_idx ? rel_idx[t + kThreads - (L - 1) + kRelSpan] : (int16_t)0;
+  if (t < n_idx) idx_tab[t] = id0;
+  if (t + kThreads < n_idx) idx_tab[t + kThreads] = id1;
+  stage_barrier();  // the index table is complete (setup_of reads it)
+  Setup cs = setup_of(cur);
+
+  for (;;) {
+    const int next = item + (int)gridDim.x;
+    const bool has_next = kPersistent && next < n_items;  // uniform
+    Item nit = cur;  // decoded once the chunk loop is done
+    bool next_staged = false, next_setup = false;
+    Setup ns;  // the next item's set-up reads, once issued
+
+    [&]() {
+      // Lane-derived values of the item body are computed afresh per item
+      // (an opaque copy of the lane index), not hoisted out of the item loop
+      // where they would hold registers through every chunk.
+      int lane_item = lane;
+      asm volatile("" : "+v"(lane_item));
+      const int lane = lane_item;
+      const int lc = lane & 15;
+      const int g = lane >> 4;
+      // Swizzled offsets of this lane's two 16-byte chunks (g and 4 + g) in
+      // row 16m + lc of a staged table: the XOR term depends on the row only
+      // through lc, so a 16-aligned tile row base is a plain (uniform) offset.
+      const int swz_lo = swz(lc, g);
+      const int swz_hi = swz(lc, 4 + g);
+      const int b = cur.b, h = cur.h;
+      const int q0 = cur.qt * kQT;
+      const int qw = q0 + 16 * wave;
+      // Key tiles and chunks of this item: up to its row extent.  An item
+      // whose queries all lie past the extent computes nothing; it runs one
+      // chunk step (its first stage is already in flight) and loads no V.
+      const bool live = q0 < cur.qlen;
+      const int nt = live ? (cur.len + 15) >> 4 : 0;
+      const int nchunks = live ? (nt + 3) >> 2 : 1;
+      const int klim = cur.klim;
+      const bool active = qw < cur.qlen;
+      const half_t* Kb = slice_base(K, b, h, cur.row0, ksb, ksh, ksl);
+      const half_t* PKh = PK + (int64_t)h * pksh;
+      const half_t* PQh = PQ + (int64_t)h * pqsh;
+      const half_t* Vb = slice_base(V, b, h, cur.row0, vsb, vsh, vsl);
+      const half8_t qf0 = cs.qf0, qf1 = cs.qf1;
+      const int win_tab = cs.win_tab;
+      auto win = [&](int j) -> int { return __builtin_amdgcn_readlane(win_tab, j); };
+      // The key mask of batch row b as an additive term: 0 for a valid key,
+      // -inf (probabilities) or -65504 (the SDPA mask output) for a masked
+      // one; made visible by chunk 0's barrier.
+      if (t < L) {
+        const float m = (float)cs.mval;
+        const bool valid = mask_kind == GD_MASK_ATTENTION ? (m > 0.f) : !(m < -60000.f);
+        mask_add[t] = valid ? 0.f : (OUT == GD_ATTN_OUT_BIAS ? -65504.f : -INFINITY);
+      }
+
+      // ---- V for the P.V pass: rows [row_lo, row_hi) of the (b, h) slice
+      // land row-major and swizzled like K at rows 0.. of an LDS buffer, by
+      // DMA (placement: after the chunk loop).  Rows past the sequence repeat
+      // row klim - 1; their probabilities are exactly 0. ----
+      const int v_rows = ((16 * nt + 31) >> 5) << 5;  // the P.V tile pairs reach this far
+      auto issue_v = [&](lds_half_t* dst, int row_lo, int row_hi) {
+        for (int blk = wave; 8 * blk < row_hi - row_lo; blk += kWaves) {  // uniform
+          int key = row_lo + 8 * blk + blk_row;
+          key = key < klim ? key : klim - 1;
+          load_lds16(Vb + (int64_t)key * vsl + blk_chunk * 8, dst + blk * 512);
+        }
+      };
+
+      float sc[MAXT][4];  // tiles at or past nt are set to -inf after the chunk loop
+
+#pragma unroll
+      for (int c = 0; c < MAXT / 4; ++c) {
+        if (c >= nchunks) break;  // uniform
+        wait_vmcnt<0>();
+        __syncthreads();  // stage c landed everywhere; every wave is done with stage c - 1
+        half_t* const st = stages + (c & 1) * kStage;
+        lds_half_t* const so = stages3 + ((c + 1) & 1) * kStage;  // free: every wave is done with stage c - 1
+        if (c + 1 < nchunks) {
+          issue_stage(so, Kb, PKh, PQh, (c + 1) * kKC, win(48 + c + 1), klim);
+        } else if constexpr (OUT == GD_ATTN_OUT_CONTEXT) {  // V rows into the free buffer
+          if (!(c & 1) || !has_next) issue_v(so, 0, v_rows < kVRowsA ? v_rows : kVRowsA);
+        }
+        const half_t* Ks = st;
+        const half_t* PKs = st + kStageK;
+        const half_t* PQs = st + kStageK + kStageWin;
+        const int kc = c * kKC;
+        const int wlo = win(48 + c);
+        // The chunk's work for this wave, in compile-time variants whose bodies
+        // have no branches, so the scheduler can overlap the tiles freely.  LIN
+        // (every (query, key) pair of this wave lies in the linear zone): every
+        // window offset is closed-form and 16-aligned and the gathers are
+        // contiguous.  Otherwise the window starts come from the lane table, the
+        // fixed 80 c2p and 32 p2c positions are computed (rows clamped to the
+        // window; the extra ones are never gathered) and every score gathers
+        // through the index table.  FULL: all 64 keys of the chunk exist.
+        auto chunk = [&](auto lin_c, auto full_c) {
+          constexpr bool LIN = decltype(lin_c)::value;
+          constexpr bool FULL = decltype(full_c)::value;  // LIN implies FULL
+          // c2p for this wave's 16 queries and the chunk's keys: positions
+          // [cw_lo, cw_lo + 80) = window rows [crow0, crow0 + 80)
+          const int cw_lo = LIN ? qw - kc - (kKC - 1) + bucket_size : win(32 + c);
+          const int crow0 = cw_lo - wlo;
+          // Off the linear zone a lane's window row r = crow0 + 16 tw + lc may run
+          // past the window; such rows hold positions this wave never gathers and
+          // are clamped to a row with the same r mod 16, so the swizzle term of
+          // the lane is the same for every tile.
+          const int crow_l = crow0 + lc;
+          const int crow_lim = kWin - 16 + (crow_l & 15);
+          const int csw_lo = (g ^ ((crow_l >> 1) & 7)) << 3, csw_hi = ((4 + g) ^ ((crow_l >> 1) & 7)) << 3;
+          if constexpr (!B32) {  // the fp32 chains compute c2p per key tile instead
+#pragma unroll
+          for (int tw = 0; tw < kC2PCols / 16; ++tw) {
+            {
+              half8_t a0, a1;
+              if constexpr (LIN) {  // crow0 = 16 wave
+                a0 = *reinterpret_cast<const half8_t*>(PKs + (crow0 + 16 * tw) * kD + swz_lo);
+                a1 = *reinterpret_cast<const half8_t*>(PKs + (crow0 + 16 * tw) * kD + swz_hi);
+              } else {
+                const int row = crow_l + 16 * tw < crow_lim ? crow_l + 16 * tw : crow_lim;
+                a0 = *reinterpret_cast<const half8_t*>(PKs + row * kD + csw_lo);
+                a1 = *reinterpret_cast<const half8_t*>(PKs + row * kD + csw_hi);
+              }
+              float4_t r = {0.f, 0.f, 0.f, 0.f};
+              r = mfma16x16x32(a0, qf0, r);
+              r = mfma16x16x32(a1, qf1, r);
+              half4_t hv;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) hv[i] = (half_t)r[i];
+              *reinterpret_cast<half4_t*>(c2p_w + lc * kC2PStride + 16 * tw + 4 * g) = hv;
+            }
+          }
+          }
+
+          // Per 16-key tile tt: S^T = K Q^T (scores) and P2C = K . posQ[window]^T
+          // over the <= 31 positions [pp_lo, pp_lo + 16 nj) the tile needs, stored
+          // skewed into p2c_w.  Tiles are software-pipelined: tile tt's gathers are
+          // issued before tile tt+1's MFMAs and p2c stores (the LDS executes a
+          // wave's accesses in order, so one p2c buffer suffices), and tile tt is
+          // combined while those are in flight.
+          int pp_lo[4];
+          float4_t s_t[4];
+          half8_t fk[2][2], fq[2][4];  // per tile parity: K rows (chunks g, 4+g), posQ rows (j = 0, 1)
+          // Operand fragments of tile tt (LDS reads only; issued a tile ahead).
+          auto prep_load = [&](int tt) {
+            const int k0 = kc + 16 * tt;
+            const int par = tt & 1;
+            pp_lo[tt] = LIN ? qw - k0 - 15 + bucket_size : win(4 * c + tt);
+            const int prow0 = pp_lo[tt] - wlo;
+            const int prow_l = prow0 + lc;  // clamped as the c2p rows
+            const int prow_lim = kWin - 16 + (prow_l & 15);
+            const int psw_lo = (g ^ ((prow_l >> 1) & 7)) << 3, psw_hi = ((4 + g) ^ ((prow_l >> 1) & 7)) << 3;
+            fk[par][0] = *reinterpret_cast<const half8_t*>(Ks + 16 * tt * kD + swz_lo);
+            fk[par][1] = *reinterpret_cast<const half8_t*>(Ks + 16 * tt * kD + swz_hi);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              {
+                if constexpr (LIN) {  // prow0 = 16 (wave - tt) + 48
+                  fq[par][2 * j] = *reinterpret_cast<const half8_t*>(PQs + (prow0 + 16 * j) * kD + swz_lo);
+                  fq[par][2 * j + 1] = *reinterpret_cast<const half8_t*>(PQs + (prow0 + 16 * j) * kD + swz_hi);
+                } else {
+                  const int row = prow_l + 16 * j < prow_lim ? prow_l + 16 * j : prow_lim;
+                  fq[par][2 * j] = *reinterpret_cast<const half8_t*>(PQs + row * kD + psw_lo);
+                  fq[par][2 * j + 1] = *reinterpret_cast<const half8_t*>(PQs + row * kD + psw_hi);
+                }
+              }
+            }
+          };
+          // Scores and p2c of tile tt from its fragments; p2c stored skewed.
+          auto prep_compute = [&](int tt) {
+            const int par = tt & 1;
+            float4_t sv = {0.f, 0.f, 0.f, 0.f};
+            sv = mfma16x16x32(fk[par][0], qf0, sv);
+            s_t[tt] = mfma16x16x32(fk[par][1], qf1, sv);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              {
+                float4_t r = {0.f, 0.f, 0.f, 0.f};
+                r = mfma16x16x32(fk[par][0], fq[par][2 * j], r);
+                r = mfma16x16x32(fk[par][1], fq[par][2 * j + 1], r);
+                // lane holds (kr = 4g + i, p = 16 j + lc)
+                if constexpr (B32) {
+#pragma unroll
+                  for (int i = 0; i < 4; ++i) {
+                    const int row = 4 * g + i + 16 * j + lc;
+                    p2cf[row * 16 + ((g ^ ((row >> 2) & 3)) << 2) + i] = r[i];
+                  }
+                } else {  // converted in pairs
+                  const half4_t rh = __builtin_convertvector(r, half4_t);
+#pragma unroll
+                  for (int i = 0; i < 4; ++i) p2c_w[(4 * g + i + 16 * j + lc) * kP2CSkew + 4 * g + i] = rh[i];
+                }
+              }
+            }
+            if constexpr (B32) {
+              // C2P^T = posK[the tile's 32 positions] . Q^T, the same window
+              // rows as the p2c fragments (every index of the tile lies in
+              // [pp_lo, pp_lo + 32)); lane holds (position 16 j + 4 g + i,
+              // query lc).
+              const int prow0 = pp_lo[tt] - wlo;
+              const int prow_l = prow0 + lc;
+              const int prow_lim = kWin - 16 + (prow_l & 15);
+              const int psw_lo = (g ^ ((prow_l >> 1) & 7)) << 3, psw_hi = ((4 + g) ^ ((prow_l >> 1) & 7)) << 3;
+#pragma unroll
+              for (int j = 0; j < 2; ++j) {
+                half8_t a0, a1;
+                if constexpr (LIN) {
+                  a0 = *reinterpret_cast<const half8_t*>(PKs + (prow0 + 16 * j) * kD + swz_lo);
+                  a1 = *reinterpret_cast<const half8_t*>(PKs + (prow0 + 16 * j) * kD + swz_hi);
+                } else {
+                  const int row = prow_l + 16 * j < prow_lim ? prow_l + 16 * j : prow_lim;
+                  a0 = *reinterpret_cast<const half8_t*>(PKs + row * kD + psw_lo);
+                  a1 = *reinterpret_cast<const half8_t*>(PKs + row * kD + psw_hi);
+                }
+                float4_t r = {0.f, 0.f, 0.f, 0.f};
+                r = mfma16x16x32(a0, qf0, r);
+                r = mfma16x16x32(a1, qf1, r);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) c2pf[lc * kC2PF32Stride + 16 * j + 4 * g + i] = r[i];
+              }
+            }
+          };
+          prep_load(0);
+          prep_compute(0);
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt) {
+            const int T = 4 * c + tt;
+            if constexpr (!FULL) {
+              if (T >= nt) break;  // uniform
+            }
+            const int k0 = 16 * T;
+            const bool next = tt + 1 < 4 && (FULL || T + 1 < nt);
+            if (next) prep_load(tt + 1);  // fragment reads overlap this tile's gathers
+            wave_lds_sync();  // tile tt's p2c stores (and the chunk's c2p) precede its gathers
+            // Gather the two terms of score (q = qw + lc, k = k0 + 4g + i) at
+            // idx(q - k).  In the linear zone idx = q - k + 256: the four c2p
+            // terms are consecutive (descending) in the lane's c2p row and the
+            // four p2c terms are one 8-byte read.
+            const float4_t madd = *reinterpret_cast<const float4_t*>(mask_add + k0 + 4 * g);
+            half4_t c2p, p2c;
+            float4_t c2p32, p2c32;
+            if constexpr (B32) {
+              if constexpr (LIN) {  // position idx - pp_lo = 15 + lc - 4 g - i
+                const float* cp = c2pf + lc * kC2PF32Stride + 15 + lc - 4 * g;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) c2p32[i] = cp[-i];
+                const int row = 15 + lc;
+                p2c32 = *reinterpret_cast<const float4_t*>(p2cf + row * 16 + ((g ^ ((row >> 2) & 3)) << 2));
+              } else {
+                const int r0 = qw + lc - k0 - 4 * g + L - 1;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                  const int pos = idx_tab[r0 - i] - pp_lo[tt];  // 0 <= pos < 32
+                  c2p32[i] = c2pf[lc * kC2PF32Stride + pos];
+                  const int row = 4 * g + i + pos;
+                  p2c32[i] = p2cf[row * 16 + ((g ^ ((row >> 2) & 3)) << 2) + i];
+                }
+              }
+            } else if constexpr (LIN) {
+              const half_t* cp = c2p_w + lc * kC2PStride + (qw - k0 + bucket_size - cw_lo) + lc - 4 * g;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) c2p[i] = cp[-i];
+              p2c = *reinterpret_cast<const half4_t*>(p2c_w + (15 + lc) * kP2CSkew + 4 * g);
+            } else {
+              const int r0 = qw + lc - k0 - 4 * g + L - 1;
+              const half_t* cb = c2p_w + lc * kC2PStride - cw_lo;
+              const half_t* pb = p2c_w + (4 * g - pp_lo[tt]) * kP2CSkew + 4 * g;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const int id = idx_tab[r0 - i];  // 0 <= id < 512
+                c2p[i] = cb[id];
+                p2c[i] = pb[__mul24(id, kP2CSkew) + i * (kP2CSkew + 1)];
+              }
+            }
+            wave_lds_sync();  // these gathers precede the next tile's p2c stores
+            if (next) prep_compute(tt + 1);
+            // fp16(c2p + p2c) is the fp16 add (two packed adds); the division by
+            // fp16(sqrt(3D)) is a multiply by its fp32 reciprocal, which rounds to
+            // the same fp16 value for every finite fp16 numerator (checked
+            // exhaustively).
+            // The fp32 chains: the relative-bias kernel's fp16((c2p + p2c) *
+            // scale) with masked keys := -65504 (FusedKernels.swift:113-119),
+            // or the fused kernel's (q.k + c2p + p2c) * scale (:47-56).
+            const half4_t sum16 = c2p + p2c;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              float v;
+              if constexpr (SM == kScoreFused) {
+                v = ((s_t[tt][i] + c2p32[i]) + p2c32[i]) * scale_rel + madd[i];
+              } else {
+                float bias16;
+                if constexpr (B32)
+                  bias16 = round_f16((c2p32[i] + p2c32[i]) * scale_rel);
+                else
+                  bias16 = round_f16((float)sum16[i] * inv_scale16);
+                if constexpr (OUT == GD_ATTN_OUT_BIAS) {
+                  if constexpr (B32)
+                    v = madd[i] != 0.f ? -65504.f : bias16;
+                  else
+                    v = round_f16(bias16 + madd[i]);
+                } else if constexpr (GENC) {
+                  // fp16(fp16(q.k) / fp16(sqrt(3D))) (the reciprocal multiply
+                  // rounds like the divide for every fp16 numerator), then the
+                  // fp16 add of the bias
+                  const float content = round_f16(round_f16(s_t[tt][i]) * inv_scale16);
+                  v = round_f16(content + bias16) + madd[i];
+                } else {
+                  v = fmaf(s_t[tt][i], scale_qk, bias16) + madd[i];
+                }
+              }
+              sc[T][i] = v;
+            }
+          }
+          wave_lds_sync();  // the last gathers precede the next chunk's c2p / p2c stores
+        };
+        if (active) {
+          const bool full = kc + kKC <= 16 * nt;
+          const bool lin = full && (qw - kc - (kKC - 1) >= -kMid) && (qw + 15 - kc <= kMid);
+          if (lin)
+            chunk(std::true_type{}, std::true_type{});
+          else if (full)
+            chunk(std::false_type{}, std::true_type{});
+          else
+            chunk(std::false_type{}, std::false_type{});
+        }
+      }
+      if (nt < MAXT) {  // key tiles past the sequence take no part in the softmax
+#pragma unroll
+        for (int T = 0; T < MAXT; ++T)
+          if (T >= nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sc[T][i] = -INFINITY;
+      }
+      // The stage buffers are free from here on, except for V rows in flight
+      // (context; waited for before the P.V pass) and the next item's stage.
+      stage_barrier();
+      // Chunk c used buffer c & 1; the next item's first stage goes to buffer
+      // 0 now.  V rows [0, kVRowsA) are in buffer 1, loaded during the last
+      // chunk when that chunk was in buffer 0 and now otherwise, except
+      // without a next item when the last chunk was in buffer 1 (then in
+      // buffer 0, loaded during that chunk); rows from kVRowsA on (no next
+      // item) go to the other buffer now.
+      const bool last_in_1 = ((nchunks - 1) & 1) != 0;
+      const bool v_in_0 = last_in_1 && !has_next;
+      lds_half_t* const v_lo = stages3 + (v_in_0 ? 0 : kStage);  // V rows [0, kVRowsA)
+      lds_half_t* const v_hi = stages3 + (v_in_0 ? kStage : 0);  // V rows [kVRowsA, v_rows)
+      if constexpr (OUT == GD_ATTN_OUT_CONTEXT) {
+        if (last_in_1 && has_next) issue_v(v_lo, 0, v_rows < kVRowsA ? v_rows : kVRowsA);
+        if (MAXT * 16 > kVRowsA && v_rows > kVRowsA) issue_v(v_hi, kVRowsA, v_rows);  // no next item here
+      }
+      if (has_next) {  // after every V row; the set-up reads before the stage DMA (see setup_of)
+        nit = decode(next);
+        ns = setup_of(nit);
+        next_setup = true;
+        stage0_of(nit, stages3);
+        next_staged = true;
+      }
+
+      float inv_sum = 0.f;
+      if (OUT != GD_ATTN_OUT_BIAS) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int T = 0; T < MAXT; ++T)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[T][i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mref = mx == -INFINITY ? 0.f : mx;
+        constexpr float kLog2e = 1.4426950408889634f;
+        // exp(s - m) = 2^(s log2e - m log2e) as one fma per score; the rounding
+        // of m log2e scales the whole row alike and cancels in the normalisation.
+        const float mref_l2 = mref * kLog2e;
+        float sum = 0.f;
+#pragma unroll
+        for (int T = 0; T < MAXT; ++T)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float e = __builtin_amdgcn_exp2f(fmaf(sc[T][i], kLog2e, -mref_l2));  // v_exp_f32; exp2(-inf) = 0
+            sc[T][i] = e;
+            sum += e;
+          }
+        sum += __shfl_xor(sum, 16, 64);
+        sum += __shfl_xor(sum, 32, 64);
+        inv_sum = sum > 0.f ? 1.0f / sum : 0.f;
+        // The context path scales O once at the end instead of every
+        // probability, except on the explicit chain, whose P.V multiplies the
+        // fp16 probabilities (DeBERTa.swift:407-408).
+        if (OUT == GD_ATTN_OUT_PROBS || GENC) {
+#pragma unroll
+          for (int T = 0; T < MAXT; ++T)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sc[T][i] *= inv_sum;
+        }
+      }
+      if (OUT == GD_ATTN_OUT_PROBS || OUT == GD_ATTN_OUT_BIAS) {
+        // Stage this wave's 16 rows x L in LDS (rows padded by 16 bytes so the
+        // 8-byte column stores of a wave hit distinct banks), then write
+        // 16-byte row segments.  At L <= 256 (where buffer 0 may hold the
+        // next item's stage) waves 0-3 stage in buffer 1, 4-7 in the scratch
+        // buffer; else waves 0-5 in the stage buffers, 6-7 in the scratch
+        // buffer.
+        const int rs = L + 8;
+        constexpr int kRowsWave = 16 * (16 * MAXT + 8);
+        static_assert(MAXT > 16 || (4 * kRowsWave <= kStage && 4 * kRowsWave <= kWaves * kScratchWave),
+                      "probability staging");
+        static_assert(3 * kRowsWave <= kStage && 2 * kRowsWave <= kWaves * kScratchWave, "probability staging");
+        half_t* rows;
+        if constexpr (MAXT <= 16)
+          rows = (wave < 4 ? stages + kStage : scratch_lds) + (wave & 3) * kRowsWave;
+        else
+          rows = wave < 6 ? stages + (wave / 3) * kStage + (wave % 3) * kRowsWave
+                          : scratch_lds + (wave - 6) * kRowsWave;
+        if (active) {
+#pragma unroll
+          for (int T = 0; T < MAXT; ++T)
+            if (T < nt) {
+              half4_t v;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) v[i] = (half_t)sc[T][i];
+              *reinterpret_cast<half4_t*>(rows + lc * rs + 16 * T + 4 * g) = v;
+            }
+          wave_lds_sync();
+          const int per_row = L / 8;  // 16-byte pieces per row
+          for (int pce = lane; pce < 16 * per_row; pce += 64) {
+            const int r = pce / per_row, cpos = pce - r * per_row;
+            *reinterpret_cast<half8_t*>(out + (((int64_t)b * H + h) * L + qw + r) * L + cpos * 8) =
+                *reinterpret_cast<const half8_t*>(rows + r * rs + cpos * 8);
+          }
+        }
+        return;
+      }
+
+      // ---- context: O = P V with V row-major in LDS, P (hi + lo) as the A operand ----
+      // The B operand (keys x d) is read with ds_read_b64_tr_b16: in each
+      // 16-lane group, source lane s names 4 consecutive halfs and output lane
+      // j receives element j % 4 of source lanes j / 4, 4 + j / 4, 8 + j / 4,
+      // 12 + j / 4.  Source lane lc of group g names V[r0 + lc / 4][16 dt +
+      // 4 (lc % 4) ..] with r0 = 16 T + 4 g, so lane (g, lc) receives
+      // V[16 T + 4 g + i][16 dt + lc], i = 0..3: the B fragment of the keys
+      // that pa holds for tile T (and, from r0 + 16, for tile T + 1).  The
+      // swizzle term (row >> 1) & 7 of those rows is (2 g + lc / 8) & 7 for
+      // every 16-aligned tile base.  The next item's stage (the last kStageOps
+      // DMA instructions, issued after the V rows) may stay in flight.
+      if (next_staged)
+        wait_vmcnt<kStageOps>();
+      else
+        wait_vmcnt<0>();
+      stage_barrier();  // every wave's V rows have landed
+      if (!active) return;
+      float4_t o[4];
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) o[dt] = (float4_t){0.f, 0.f, 0.f, 0.f};
+      typedef __attribute__((address_space(3))) short4_t lds_short4_t;
+      const int tr_sw = (2 * g + (lc >> 3)) & 7;
+      const int tr_lane = (4 * g + (lc >> 2)) * kD + 4 * (lc & 1);  // row and half offset of this source lane
+      const int tr_c = (lc >> 1) & 1;                                // 16-byte chunk within the 32-byte d slice
+#pragma unroll
+      for (int c = 0; c < MAXT / 4; ++c) {
+        if (c >= nchunks) break;
+#pragma unroll
+        for (int pr = 0; pr < 2; ++pr) {
+          const int T = 4 * c + 2 * pr;
+          if (T >= nt) break;  // uniform; nt is at most one past the last pair's first tile
+          const int row0 = 16 * T;
+          const lds_half_t* vsrc = row0 < kVRowsA ? v_lo + row0 * kD : v_hi + (row0 - kVRowsA) * kD;
+          // Unnormalised P of key tiles T, T + 1 as the A operand, split into
+          // fp16 hi (truncated) + lo (the exact fp32 remainder, rounded).  Tiles
+          // at or past nt hold exp(-inf) = 0.
+          // On the explicit chain the operand is P rounded to fp16 (the
+          // reference's fp16 probabilities), with no low part.
+          half8_t pa, pl;
+#pragma unroll
+          for (int i = 0; i < 4; i += 2) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              const float x0 = sc[T + u][i], x1 = sc[T + u][i + 1];
+              if constexpr (GENC) {
+                pa[4 * u + i] = (half_t)x0;
+                pa[4 * u + i + 1] = (half_t)x1;
+              } else {
+                const half2_t hi = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(x0, x1));
+                pa[4 * u + i] = hi[0];
+                pa[4 * u + i + 1] = hi[1];
+                pl[4 * u + i] = (half_t)(x0 - (float)hi[0]);
+                pl[4 * u + i + 1] = (half_t)(x1 - (float)hi[1]);
+              }
+            }
+          }
+          half8_t vb[4];
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) {
+            const lds_half_t* a = vsrc + tr_lane + (((2 * dt + tr_c) ^ tr_sw) << 3);
+            const short4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)a);
+            const short4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(a + 16 * kD));
+            const half4_t h0 = __builtin_bit_cast(half4_t, v0), h1 = __builtin_bit_cast(half4_t, v1);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              vb[dt][i] = h0[i];
+              vb[dt][4 + i] = h1[i];
+            }
+          }
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) o[dt] = mfma16x16x32(pa, vb[dt], o[dt]);
+          if constexpr (!GENC) {
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) o[dt] = mfma16x16x32(pl, vb[dt], o[dt]);
+          }
+        }
+      }
+      // lane holds O[qw + 4g + i][16 dt + lc]: stage 16 x 64 in LDS, write 128-byte rows
+      // (the softmax sum of query row r sits in lanes with lc = r)
+      half_t* ot = scratch_lds + wave * kScratchWave;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float inv_row = GENC ? 1.0f : __shfl(inv_sum, 4 * g + i, 64);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) ot[(4 * g + i) * 72 + 16 * dt + lc] = (half_t)(o[dt][i] * inv_row);
+      }
+      wave_lds_sync();
+      {
+        const int r = lane >> 3, cpos = lane & 7;  // 8 rows x 8 pieces per pass
+#pragma unroll
+        for (int pass = 0; pass < 2; ++pass) {
+          const int row = r + 8 * pass;
+          // packed rows: rows past the extent belong to the next batch row;
+          // rows from qlen on are not computed
+          if ((cur.row0 < 0 && q_len == nullptr) || qw + row < cur.qlen)
+            *reinterpret_cast<half8_t*>(out + ((cur.row0 >= 0 ? (int64_t)cur.row0 : (int64_t)b * L) + qw + row) * ldo +
+                                        (int64_t)h * kD + cpos * 8) =
+                *reinterpret_cast<const half8_t*>(ot + row * 72 + cpos * 8);
+        }
+      }
+    }();
+
+    if (!has_next) break;
+    if (!next_setup) ns = setup_of(nit);
+    cur = nit;
+    cs = ns;
+    item = next;
+  }
+}
+
+template <int SM, int MAXT>
+int launch_attention_maxt(const AttentionArgs& a, hipStream_t stream) {
+  const int ntq = (int)((a.L + kQT - 1) / kQT);
+  const int64_t items = a.B * a.H * ntq;
+  const int64_t cus = attention_persistent<MAXT>() ? device_cu_count() : items;
+  const dim3 grid((unsigned)(items < cus ? items : cus)), block(kThreads);
+  auto hq = static_cast<const half_t*>(a.q);
+  auto hk = static_cast<const half_t*>(a.k);
+  auto hv = static_cast<const half_t*>(a.v);
+  auto hpk = static_cast<const half_t*>(a.pk);
+  auto hpq = static_cast<const half_t*>(a.pq);
+  auto hm = static_cast<const half_t*>(a.mask);
+  auto ho = static_cast<half_t*>(a.out);
+  // element strides in 32 bits (checked by launch_deberta_attention)
+#define GD_ATTN2(OUTK)                                                                                            \
+  hipLaunchKernelGGL((deberta_attention_kernel<MAXT, OUTK, SM>), grid, block, 0, stream, hq, hk, hv, (int)a.qsb, \
+                     (int)a.qsh, (int)a.qsl, (int)a.ksb, (int)a.ksh, (int)a.ksl, (int)a.vsb, (int)a.vsh, (int)a.vsl, \
+                     hpk, hpq, (int)a.pksh, (int)a.pksp, (int)a.pqsh, (int)a.pqsp, hm, a.mask_kind, a.row_len,      \
+                     a.row_off, a.q_len, a.sched, a.n_sched, (int)a.B, (int)a.H, (int)a.L, (int)a.P, a.bucket_size, \
+                     a.scale_qk, a.scale16, a.scale_rel, a.rel_idx, ho, (int)a.ldo)
+  switch (a.output) {
+    case GD_ATTN_OUT_PROBS:
+      GD_ATTN2(GD_ATTN_OUT_PROBS);
+      break;
+    case GD_ATTN_OUT_CONTEXT:
+      GD_ATTN2(GD_ATTN_OUT_CONTEXT);
+      break;
+    default:
+      // the bias output exists on the chains that add a bias of their own
+      if constexpr (SM == kScoreDefault || SM == kScoreKernelBias) {
+        GD_ATTN2(GD_ATTN_OUT_BIAS);
+      } else {
+        return fail(GD_ERR_INVALID_ARGUMENT, "attention: no bias output on this score chain");
+      }
+      break;
+  }
+#undef GD_ATTN2
+  GD_LAUNCH_CHECK();
+  return GD_OK;
+}
+
+template <int SM>
+int launch_attention_sm(const AttentionArgs& a, hipStream_t stream) {
+  if (a.rel_idx == nullptr) return fail(GD_ERR_INVALID_ARGUMENT, "attention: no relative index table");
+  if (a.L <= 64) return launch_attention_maxt<SM, 4>(a, stream);
+  if (a.L <= 128) return launch_attention_maxt<SM, 8>(a, stream);
+  if (a.L <= 256) return launch_attention_maxt<SM, 16>(a, stream);
+  return launch_attention_maxt<SM, 32>(a, stream);
+}
+
+}  // namespace
+}  // namespace gd

@@ -28,6 +28,15 @@ int ensure_relative_index_table(hipStream_t stream);
 int launch_linear(const void* a, const void* w, const void* bias, void* c, int64_t m, int64_t n, int64_t k, int64_t lda,
                   int64_t ldc, const int32_t* a_rows, int64_t a_row_count, int epilogue_kind, hipStream_t stream);
 
+// Score chains of the attention kernel (which reference graph it reproduces).
+enum AttentionScore {
+  kScoreDefault = 0,             // default bias chain + SDPA (DeBERTa.swift:374-394)
+  kScoreExplicit = 1,            // default bias + explicit-score chain (useFastAttention=false, :397-409)
+  kScoreKernelBias = 2,          // relative-bias Metal kernel's bias + SDPA with it as the mask (:357-372, 383-385)
+  kScoreKernelBiasExplicit = 3,  // the same bias + explicit-score chain without where (:397-405)
+  kScoreFused = 4,               // fused-attention Metal kernel (useFusedAttentionKernel, :337-354)
+};
+
 struct AttentionArgs {
   const void* q;
   const void* k;
@@ -60,7 +69,24 @@ struct AttentionArgs {
   // n_sched = attention_schedule_slots(B, H, L) entries.
   const int32_t* sched = nullptr;
   int n_sched = 0;
+  // Score chain (AttentionScore) and, for the kernel-bias and fused chains,
+  // the scale the Metal kernels multiply (c2p + p2c) or (q.k + c2p + p2c)
+  // by (FusedKernels.swift:53,116).
+  int score = kScoreDefault;
+  float scale_rel = 0.f;
+  // Device address of the relative index table (set by
+  // launch_deberta_attention).
+  const int16_t* rel_idx = nullptr;
 };
+
+// Per-score-mode launchers (one translation unit each).
+int launch_attention_default(const AttentionArgs& args, hipStream_t stream);
+int launch_attention_explicit(const AttentionArgs& args, hipStream_t stream);
+int launch_attention_kernel_bias(const AttentionArgs& args, hipStream_t stream);
+int launch_attention_fused(const AttentionArgs& args, hipStream_t stream);
+// The relative index table's device address on the current device (filled
+// on first use, as ensure_relative_index_table).
+int relative_index_table_device(const int16_t** out, hipStream_t stream);
 
 // Slots of the persistent attention's item schedule for (B, H, L), 0 when
 // that launch takes no schedule (L > 256, or more than 2048 (b, h) pairs).

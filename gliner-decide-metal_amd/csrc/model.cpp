@@ -154,8 +154,6 @@ int Classifier::init(const WeightStore& store, const gd_config& cfg, uint32_t fl
   GD_CHECK_ARG(V > 0, "vocab_size must be positive");
   GD_CHECK_ARG(cfg.position_buckets == 256, "position_buckets must be 256 (the graph hard-codes 256/512)");
   GD_CHECK_ARG(cfg.layer_norm_eps > 0.f, "layer_norm_eps must be positive");
-  if (flags & GD_USE_GENERIC_ATTENTION)
-    return fail(GD_ERR_UNSUPPORTED, "the explicit-score attention path (useFastAttention=false) is not built");
 
   // Host-side check of every key, shape and dtype before any device work, so
   // a bad checkpoint fails without allocating (WeightStore.array checks,
@@ -281,7 +279,12 @@ int Classifier::layer_forward(int li, const void* mask, int64_t B, int64_t L, hi
   const int64_t C = cfg_.hidden_size, F = cfg_.intermediate_size, H = cfg_.num_attention_heads, D = C / H;
   const int64_t T = rows.tokens >= 0 ? rows.tokens : B * L;
   const float eps = cfg_.layer_norm_eps;
-  const uint32_t ln_flags = (flags_ & GD_USE_FUSED_KERNELS) ? 0u : GD_LN_SUM_F16;
+  // The reference holds a FusedKernels instance -- and its residual LN keeps
+  // x + residual in fp32 -- whenever any of the three kernel flags is set
+  // (DeBERTa.swift:230-232, 449-462).
+  const bool metal_ln =
+      (flags_ & (GD_USE_FUSED_KERNELS | GD_USE_CUSTOM_RELATIVE_KERNEL | GD_USE_FUSED_ATTENTION_KERNEL)) != 0;
+  const uint32_t ln_flags = metal_ln ? 0u : GD_LN_SUM_F16;
   char name[48];
 
   if (hook) hook->begin(stream);
@@ -317,6 +320,17 @@ int Classifier::layer_forward(int li, const void* mask, int64_t B, int64_t L, hi
   a.scale_qk = 1.0f / std::sqrt((float)(3 * D));
   a.scale16 = (float)(_Float16)std::sqrt((float)(3 * D));
   a.output = GD_ATTN_OUT_CONTEXT;
+  // Score chain per the constructor flags (DeBERTa.swift:337-409): the fused
+  // kernel returns before anything else; the custom relative kernel replaces
+  // the bias; useFastAttention = false takes the explicit-score path.
+  const bool explicit_scores = (flags_ & GD_USE_GENERIC_ATTENTION) != 0;
+  if (flags_ & GD_USE_FUSED_ATTENTION_KERNEL)
+    a.score = kScoreFused;
+  else if (flags_ & GD_USE_CUSTOM_RELATIVE_KERNEL)
+    a.score = explicit_scores ? kScoreKernelBiasExplicit : kScoreKernelBias;
+  else
+    a.score = explicit_scores ? kScoreExplicit : kScoreDefault;
+  a.scale_rel = a.scale_qk;  // 1 / sqrt(3 D), the Metal kernels' `scale` (:347, :366)
   a.out = ws_.ctx;
   a.ldo = C;
   a.row_len = rows.len;

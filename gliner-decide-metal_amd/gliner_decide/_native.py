@@ -47,7 +47,10 @@ GD_LN_SUM_F16 = 1
 GD_EPI_NONE, GD_EPI_BIAS, GD_EPI_BIAS_GELU, GD_EPI_BIAS_RELU = 0, 1, 2, 3
 GD_MASK_ATTENTION, GD_MASK_ADDITIVE = 0, 1
 GD_ATTN_OUT_PROBS, GD_ATTN_OUT_CONTEXT, GD_ATTN_OUT_BIAS = 0, 1, 2
+GD_ATTN_SCORE_DEFAULT, GD_ATTN_SCORE_EXPLICIT, GD_ATTN_SCORE_KERNEL_BIAS = 0x000, 0x100, 0x200
+GD_ATTN_SCORE_KERNEL_BIAS_EXPLICIT, GD_ATTN_SCORE_FUSED = 0x300, 0x400
 GD_USE_FUSED_KERNELS, GD_USE_COMPILED_GRAPH, GD_USE_GENERIC_ATTENTION, GD_FULL_ROWS = 1, 2, 4, 8
+GD_USE_CUSTOM_RELATIVE_KERNEL, GD_USE_FUSED_ATTENTION_KERNEL = 16, 32
 
 
 class GlinerDecideError(RuntimeError):

@@ -87,16 +87,19 @@ class GLiNERDecideClassifier:
     """Mirror of `GLiNERDecideClassifier.init` (DeBERTa.swift:188-196).
 
     weights: a WeightStore, a path to an fp16 safetensors file, or a dict of
-    numpy arrays keyed like the checkpoint.  use_fused_kernels keeps the
-    residual sum in fp32 (FusedKernels residual LN); use_compiled_graph
-    replays a captured hipGraph per input shape (MLX `compile`);
-    use_fast_attention=False (explicit-score path) is not built and raises.
-    use_custom_relative_kernel / use_fused_attention_kernel are accepted for
-    API compatibility: the fused relative-bias + softmax + P.V kernel is the
-    only attention path, so both select it.  full_rows (no counterpart in the
-    reference) makes classify compute every position; by default each row's
-    attention stops at its extent (last unmasked or marker-read position + 1),
-    which leaves the logits unchanged.
+    numpy arrays keyed like the checkpoint.  Every flag reproduces the
+    reference graph it selects (DeBERTa.swift:322-464): use_fused_kernels keeps
+    the residual sum in fp32 (FusedKernels residual LN);
+    use_fast_attention=False takes the explicit-score path (:397-409);
+    use_custom_relative_kernel uses the relative-bias Metal kernel's fp32 bias
+    as the attention mask (:357-372, 383-385); use_fused_attention_kernel the
+    fused-attention Metal kernel's fp32 score (:337-354); either of the last
+    two also switches the residual LNs to the fp32 sum, as the reference does
+    whenever it holds a FusedKernels instance.  use_compiled_graph replays a
+    captured hipGraph per input shape (MLX `compile`).  full_rows (no
+    counterpart in the reference) makes classify compute every position; by
+    default each row's attention stops at its extent (last unmasked or
+    marker-read position + 1), which leaves the logits unchanged.
     """
 
     def __init__(self, weights, configuration: DeBERTaV2Configuration | None = None, use_fused_kernels: bool = False,
@@ -119,6 +122,10 @@ class GLiNERDecideClassifier:
             flags |= N.GD_USE_COMPILED_GRAPH
         if not use_fast_attention:
             flags |= N.GD_USE_GENERIC_ATTENTION
+        if use_custom_relative_kernel:
+            flags |= N.GD_USE_CUSTOM_RELATIVE_KERNEL
+        if use_fused_attention_kernel:
+            flags |= N.GD_USE_FUSED_ATTENTION_KERNEL
         if full_rows:
             flags |= N.GD_FULL_ROWS
         cfg = self.configuration.to_native()
@@ -127,6 +134,9 @@ class GLiNERDecideClassifier:
         self._h = h
         self.use_fused_kernels = use_fused_kernels
         self.use_compiled_graph = use_compiled_graph
+        self.use_fast_attention = use_fast_attention
+        self.use_custom_relative_kernel = use_custom_relative_kernel
+        self.use_fused_attention_kernel = use_fused_attention_kernel
         self.full_rows = full_rows
 
     @property

@@ -24,6 +24,18 @@ def _dims(t: torch.Tensor, n: int, name: str):
     return tuple(t.shape)
 
 
+def _indices(c2p_indices, p2c_indices, H: int, L: int):
+    """General index tensors broadcast to [H, L, L], or (None, None) for the
+    closed form."""
+    if c2p_indices is None and p2c_indices is None:
+        return None, None
+    if c2p_indices is None or p2c_indices is None:
+        raise N.GlinerDecideError(N.GD_ERR_INVALID_ARGUMENT, "give both index tensors, or neither")
+    c2p = as_i32(c2p_indices, "c2p_indices").expand(1, H, L, L).reshape(H, L, L).contiguous()
+    p2c = as_i32(p2c_indices, "p2c_indices").expand(1, H, L, L).reshape(H, L, L).contiguous()
+    return c2p, p2c
+
+
 class FusedKernels:
     """Mirror of `FusedKernels` (FusedKernels.swift:7)."""
 
@@ -60,14 +72,15 @@ class FusedKernels:
                       batch: int, heads: int, sequence_length: int, head_dimension: int,
                       position_count: int) -> torch.Tensor:
         """(q.posK[c2p] + k.posQ[p2c]) * scale with masked keys := -65504,
-        general index tensors [1 or H, L, L]; returns [B, H, L, L] fp16."""
+        general index tensors [1 or H, L, L]; returns [B, H, L, L] fp16.
+        c2p_indices = p2c_indices = None selects the closed-form indices
+        (the ones the classifier builds) on the MFMA attention kernel."""
         q = as_f16(q, "q")
         k = as_f16(k, "k")
         if q.shape != k.shape or q.dim() != 4 or q.shape[2] != sequence_length or q.shape[3] != head_dimension:
             raise N.GlinerDecideError(N.GD_ERR_SHAPE, "q/k must both be [B, H, L, D]")
         H, L = heads, sequence_length
-        c2p = as_i32(c2p_indices, "c2p_indices").expand(1, H, L, L).reshape(H, L, L).contiguous()
-        p2c = as_i32(p2c_indices, "p2c_indices").expand(1, H, L, L).reshape(H, L, L).contiguous()
+        c2p, p2c = _indices(c2p_indices, p2c_indices, H, L)
         pk = as_f16(position_key, "position_key").reshape(H, position_count, head_dimension).contiguous()
         pq = as_f16(position_query, "position_query").reshape(H, position_count, head_dimension).contiguous()
         km = as_f16(key_mask, "key_mask").reshape(batch, L).contiguous()
@@ -81,7 +94,8 @@ class FusedKernels:
     def fused_attention(self, queries, keys, values, position_key, position_query, c2p_indices, p2c_indices,
                         key_mask, scale: float, batch: int, heads: int, sequence_length: int, head_dimension: int,
                         position_count: int) -> torch.Tensor:
-        """Whole attention with general indices; returns [B, L, H, D] fp16."""
+        """Whole attention with general indices (None for the closed form, on
+        the MFMA attention kernel); returns [B, L, H, D] fp16."""
         q = as_f16(queries, "queries")
         k = as_f16(keys, "keys")
         v = as_f16(values, "values")
@@ -90,8 +104,7 @@ class FusedKernels:
         if tuple(q.shape) != (batch, heads, sequence_length, head_dimension):
             raise N.GlinerDecideError(N.GD_ERR_SHAPE, "queries shape does not match the given dimensions")
         H, L = heads, sequence_length
-        c2p = as_i32(c2p_indices, "c2p_indices").expand(1, H, L, L).reshape(H, L, L).contiguous()
-        p2c = as_i32(p2c_indices, "p2c_indices").expand(1, H, L, L).reshape(H, L, L).contiguous()
+        c2p, p2c = _indices(c2p_indices, p2c_indices, H, L)
         pk = as_f16(position_key, "position_key").reshape(H, position_count, head_dimension).contiguous()
         pq = as_f16(position_query, "position_query").reshape(H, position_count, head_dimension).contiguous()
         km = as_f16(key_mask, "key_mask").reshape(batch, L).contiguous()
@@ -103,14 +116,19 @@ class FusedKernels:
 
     # -- default graph: relative bias + masked softmax (+ P.V) --------------
     def deberta_attention(self, q, k, v, position_key, position_query, mask, *, output: str = "context",
-                          mask_kind: str = "attention", out: torch.Tensor | None = None) -> torch.Tensor:
-        """Closed-form-index DeBERTa attention (DeBERTa.swift:322-395).
+                          mask_kind: str = "attention", out: torch.Tensor | None = None,
+                          score: str = "default") -> torch.Tensor:
+        """Closed-form-index DeBERTa attention (DeBERTa.swift:322-410).
 
         q, k, v: [B, H, L, D] views with contiguous D (any strides, e.g. the
         split of a fused [B, L, 3, H, D] projection); position_key /
         position_query: [H, P, D] views with contiguous D; mask: [B, L] fp16.
         output: "probs" -> [B, H, L, L]; "context" -> [B, L, H*D];
-        "bias" -> the SDPA additive mask [B, H, L, L]."""
+        "bias" -> the SDPA additive mask [B, H, L, L] (or the kernel bias).
+        score: the graph reproduced -- "default" (:374-394), "explicit"
+        (useFastAttention = false, :397-409), "kernel_bias"
+        (useCustomRelativeKernel, :357-372 + SDPA), "kernel_bias_explicit"
+        (both), "fused" (useFusedAttentionKernel, :337-354)."""
         for name, t in (("q", q), ("k", k)) + ((("v", v),) if v is not None else ()):
             if not t.is_cuda or t.dtype != torch.float16 or t.dim() != 4 or t.stride(3) != 1:
                 raise N.GlinerDecideError(N.GD_ERR_SHAPE, f"{name} must be a [B, H, L, D] fp16 GPU view with "
@@ -122,6 +140,9 @@ class FusedKernels:
         P = position_key.shape[1]
         mask = as_f16(mask, "mask").reshape(B, L).contiguous()
         kind = {"probs": N.GD_ATTN_OUT_PROBS, "context": N.GD_ATTN_OUT_CONTEXT, "bias": N.GD_ATTN_OUT_BIAS}[output]
+        sc = {"default": N.GD_ATTN_SCORE_DEFAULT, "explicit": N.GD_ATTN_SCORE_EXPLICIT,
+              "kernel_bias": N.GD_ATTN_SCORE_KERNEL_BIAS, "kernel_bias_explicit": N.GD_ATTN_SCORE_KERNEL_BIAS_EXPLICIT,
+              "fused": N.GD_ATTN_SCORE_FUSED}[score]
         mk = {"attention": N.GD_MASK_ATTENTION, "additive": N.GD_MASK_ADDITIVE}[mask_kind]
         if out is None:
             shape = (B, L, H * D) if kind == N.GD_ATTN_OUT_CONTEXT else (B, H, L, L)
@@ -133,7 +154,7 @@ class FusedKernels:
             N.GdBhld(ptr(vv), *vv.stride()[:3]),
             N.GdTable(ptr(position_key), position_key.stride(0), position_key.stride(1)),
             N.GdTable(ptr(position_query), position_query.stride(0), position_query.stride(1)),
-            ptr(mask), mk, B, H, L, D, P, 256, kind, ptr(out), ldo, stream_handle()))
+            ptr(mask), mk, B, H, L, D, P, 256, kind | sc, ptr(out), ldo, stream_handle()))
         return out
 
     # -- default graph: embedding stage (DeBERTa.swift:285-292) -------------

@@ -150,6 +150,10 @@ int gd_linear(const void* a, const void* w, const void* bias, void* c, int64_t m
  * in fp32, masked keys := -65504, fp16 output [B, H, L, L].
  * q, k: [B, H, L, D]; pos_key/pos_query: [H, P, D]; c2p/p2c: int32 [H, L, L];
  * key_mask: fp16 additive [B, L].
+ * c2p_indices = p2c_indices = NULL selects the closed-form indices the
+ * classifier builds (c2p[h,q,k] = p2c[h,k,q] = clip(bucket(q - k) + 256, 0,
+ * 511), DeBERTa.swift:498-519) and runs them on the MFMA attention kernel
+ * (D = 64, P = 512, L a multiple of 16 in [16, 512]).
  * Replaces FusedKernels.relativeBias (FusedKernels.swift:83-123, 214-258). */
 int gd_relative_bias(const void* q, const void* k, const void* pos_key, const void* pos_query,
                      const int32_t* c2p_indices, const int32_t* p2c_indices, const void* key_mask,
@@ -159,6 +163,8 @@ int gd_relative_bias(const void* q, const void* k, const void* pos_key, const vo
 /* Fully fused attention with general index tensors, FusedKernels semantics:
  * score = (q.k + q.pos_key[c2p] + k.pos_query[p2c]) * scale (fp32), masked
  * keys := -65504, softmax, out[b, q, h, :] = sum_k w v  -> [B, L, H, D] fp16.
+ * NULL index tensors select the closed-form indices, as for
+ * gd_relative_bias, on the MFMA attention kernel.
  * Replaces FusedKernels.fusedAttention (FusedKernels.swift:13-81, 160-210). */
 int gd_fused_attention(const void* q, const void* k, const void* v, const void* pos_key,
                        const void* pos_query, const int32_t* c2p_indices,
@@ -185,6 +191,29 @@ typedef struct gd_table {
 #define GD_ATTN_OUT_CONTEXT 1 /* context P.V as [B, L, H*D] fp16 (ldo = H*D) */
 #define GD_ATTN_OUT_BIAS 2    /* the SDPA additive mask fp16(bias + key mask) [B, H, L, L] */
 
+/* Score chains of gd_deberta_attention, OR'ed into `output` (one of them;
+ * DEFAULT when none).  Each reproduces one graph of
+ * GLiNERDecideClassifier.forward (DeBERTa.swift:322-410):
+ *  DEFAULT   the default relative bias and SDPA with bias + key mask (:374-394)
+ *  EXPLICIT  useFastAttention = false: fp16(fp16(q.k) / fp16(sqrt(3D))), the
+ *            fp16 add of the default bias, masked keys := -65504, fp16
+ *            probabilities, fp16(P.V) (:397-409)
+ *  KERNEL_BIAS  useCustomRelativeKernel: bias = fp16((c2p + p2c) / sqrt(3D))
+ *            with c2p, p2c in fp32 and masked keys := -65504
+ *            (FusedKernels.swift:83-123), the whole SDPA mask (:383-385);
+ *            with GD_ATTN_OUT_BIAS the output is that bias
+ *  KERNEL_BIAS_EXPLICIT  useCustomRelativeKernel with useFastAttention =
+ *            false: that bias added to the fp16 content score, no where
+ *            (:397-405)
+ *  FUSED     useFusedAttentionKernel: (q.k + c2p + p2c) / sqrt(3D) in fp32,
+ *            masked keys excluded, softmax, P.V (FusedKernels.swift:13-81)
+ * GD_ATTN_OUT_BIAS exists for DEFAULT and KERNEL_BIAS only. */
+#define GD_ATTN_SCORE_DEFAULT 0x000
+#define GD_ATTN_SCORE_EXPLICIT 0x100
+#define GD_ATTN_SCORE_KERNEL_BIAS 0x200
+#define GD_ATTN_SCORE_KERNEL_BIAS_EXPLICIT 0x300
+#define GD_ATTN_SCORE_FUSED 0x400
+
 /* Default-graph disentangled attention with closed-form log-bucket indices
  * (DeBERTa.swift:322-395, 498-551), one fused MFMA kernel:
  *   idx(q,k)  = clip(bucket(q - k) + 256, 0, 511)
@@ -199,8 +228,9 @@ typedef struct gd_table {
  * fills that device's relative index table (a small kernel and a stream
  * synchronisation); made on a stream that is capturing a graph it returns
  * GD_ERR_UNSUPPORTED instead, so a caller that captures makes one attention
- * call (or creates a classifier) on the device beforehand.  Replaces the
- * default relative-bias + SDPA chain and the generic path (:397-409). */
+ * call (or creates a classifier) on the device beforehand.
+ * `output` = GD_ATTN_OUT_* | GD_ATTN_SCORE_*.  Replaces the attention stage
+ * of GLiNERDecideClassifier.forward (:322-410) under each of its flags. */
 int gd_deberta_attention(gd_bhld q, gd_bhld k, gd_bhld v, gd_table pos_key, gd_table pos_query,
                          const void* mask, int32_t mask_kind, int64_t batch, int64_t heads,
                          int64_t seq_len, int64_t head_dim, int64_t positions,
@@ -243,7 +273,11 @@ typedef struct gd_classifier gd_classifier;
 /* Constructor flags mirroring GLiNERDecideClassifier.init (DeBERTa.swift:188-196). */
 #define GD_USE_FUSED_KERNELS 1u    /* useFusedKernels: residual LN keeps x + residual in fp32 */
 #define GD_USE_COMPILED_GRAPH 2u   /* useCompiledGraph: capture each shape's forward in a hipGraph */
-#define GD_USE_GENERIC_ATTENTION 4u /* useFastAttention = false (explicit-score path) -- unsupported */
+#define GD_USE_GENERIC_ATTENTION 4u /* useFastAttention = false: the explicit-score path (:397-409) */
+#define GD_USE_CUSTOM_RELATIVE_KERNEL 16u /* useCustomRelativeKernel: the relative-bias Metal kernel's
+                                             bias (:357-372); residual LNs as GD_USE_FUSED_KERNELS */
+#define GD_USE_FUSED_ATTENTION_KERNEL 32u /* useFusedAttentionKernel: the fused-attention Metal kernel
+                                             (:337-354); residual LNs as GD_USE_FUSED_KERNELS */
 /* No counterpart in the reference.  By default classify computes each row's
  * attention only up to its extent: the larger of (last position with
  * attention_mask > 0) + 1 and (last position a marker slot with

@@ -271,7 +271,8 @@ def relative_bias_default(q, k, pos_key, pos_query, c2p_idx, p2c_idx, head_size:
     return f16(s / scale, round16, dtype)
 
 
-def relative_bias_kernel(q, k, pos_key, pos_query, c2p_indices, p2c_indices, key_mask, scale: float):
+def relative_bias_kernel(q, k, pos_key, pos_query, c2p_indices, p2c_indices, key_mask, scale: float,
+                         round16: bool = True):
     """`gliner_decide_relative_bias` (FusedKernels.swift:83-123) with general
     index tensors.
 
@@ -299,7 +300,7 @@ def relative_bias_kernel(q, k, pos_key, pos_query, c2p_indices, p2c_indices, key
     score = (c2p + p2c) * np.float64(np.float32(scale))
     masked = np.asarray(key_mask, np.float64).reshape(B, 1, 1, L) < -60000.0
     score = np.where(masked, MASK_FILL, score)
-    return f16(score)
+    return f16(score, round16)
 
 
 # ---------------------------------------------------------------------------
@@ -341,24 +342,54 @@ def attention_default(q, k, v, bias, attention_mask, head_size: int, round16: bo
     return f16(np.transpose(ctx, (0, 2, 1, 3)).reshape(B, L, H * D), round16, dtype)
 
 
-def attention_generic(q, k, v, bias, attention_mask, head_size: int, round16: bool = True, dtype=np.float64):
-    """Explicit-score path (`--generic-attention`, DeBERTa.swift:397-409):
-    content = fp16(fp16(q k^T) / fp16 scale); scores = fp16(content + bias);
-    masked keys := -65504; P = softmax -> fp16; ctx = fp16(P v)."""
+def attention_sdpa_mask(q, k, v, mask, head_size: int, round16: bool = True, dtype=np.float64):
+    """MLXFast.scaledDotProductAttention with `mask` as the whole additive
+    mask (DeBERTa.swift:382-395): softmax(q k^T * (1/sqrt(3D)) + mask) v,
+    transposed to [B, L, H*D].  The useCustomRelativeKernel graph passes the
+    kernel's bias (masked keys already -65504) with no key mask added
+    (:383-385)."""
     q = np.asarray(q, dtype)
     k = np.asarray(k, dtype)
-    content = f16(f16(np.matmul(q, np.swapaxes(k, -1, -2)), round16, dtype) / scale_f16(head_size), round16,
-                  dtype)
-    scores = f16(content + np.asarray(bias, dtype), round16, dtype)
-    valid = (np.asarray(attention_mask, np.float64) > 0)[:, None, None, :]
-    masked = np.where(valid, scores, MASK_FILL)
-    p = f16(_softmax(masked), round16, dtype)
+    scores = np.matmul(q, np.swapaxes(k, -1, -2)) * dtype(scale_f32(head_size)) + np.asarray(mask, dtype)
+    with np.errstate(over="ignore", invalid="ignore"):
+        p = _softmax(scores)
+    ctx = np.matmul(p, np.asarray(v, dtype))
+    B, H, L, D = ctx.shape
+    return f16(np.transpose(ctx, (0, 2, 1, 3)).reshape(B, L, H * D), round16, dtype)
+
+
+def attention_generic(q, k, v, bias, attention_mask, head_size: int, round16: bool = True, dtype=np.float64,
+                      where_mask: bool = True, content_scale: float | None = None):
+    """Explicit-score path (`useFastAttention = false`, `--generic-attention`,
+    DeBERTa.swift:397-409):
+    content = fp16(fp16(q k^T) / fp16(sqrt(3 D)))   (:399, MLX fp16 matmul then fp16 divide)
+    scores  = fp16(content + bias)                   (:400)
+    masked keys := -65504 (`where`, :401-407; skipped with where_mask=False,
+    the useCustomRelativeKernel graph, whose bias already holds -65504)
+    P = fp16(softmax(scores)) (:407); ctx = fp16(P v) (:408) -> [B, L, H*D].
+    `content_scale` overrides fp16(sqrt(3 D)) (exact cross-checks only).
+
+    pinned by: scalar loops with explicit fp16 rounding at every op (tests),
+    and, with round16=False, the HF DeBERTa-v2 layer (float64).
+    """
+    q = np.asarray(q, dtype)
+    k = np.asarray(k, dtype)
+    cs = scale_f16(head_size) if content_scale is None else content_scale
+    content = f16(f16(np.matmul(q, np.swapaxes(k, -1, -2)), round16, dtype) / cs, round16, dtype)
+    with np.errstate(over="ignore"):
+        scores = f16(content + np.asarray(bias, dtype), round16, dtype)
+    if where_mask:
+        valid = (np.asarray(attention_mask, np.float64) > 0)[:, None, None, :]
+        scores = np.where(valid, scores, MASK_FILL)
+    with np.errstate(over="ignore", invalid="ignore"):
+        p = f16(_softmax(scores), round16, dtype)
     ctx = f16(np.matmul(p, np.asarray(v, dtype)), round16, dtype)
     B, H, L, D = ctx.shape
     return np.transpose(ctx, (0, 2, 1, 3)).reshape(B, L, H * D)
 
 
-def fused_attention_kernel(q, k, v, pos_key, pos_query, c2p_indices, p2c_indices, key_mask, scale: float):
+def fused_attention_kernel(q, k, v, pos_key, pos_query, c2p_indices, p2c_indices, key_mask, scale: float,
+                           round16: bool = True):
     """`gliner_decide_fused_attention` (FusedKernels.swift:13-81):
     score = (q.k + q.posK[c2p] + k.posQ[p2c]) * scale (fp32), masked keys
     (key_mask < -60000) := -65504, softmax with the running max seeded at
@@ -386,7 +417,53 @@ def fused_attention_kernel(q, k, v, pos_key, pos_query, c2p_indices, p2c_indices
     e = np.exp(score - m)
     w = e / e.sum(axis=-1, keepdims=True)
     out = np.matmul(w, v).transpose(0, 2, 1, 3)
-    return f16(out)
+    return f16(out, round16)
+
+
+def attention_stage(q, k, v, pos_key, pos_query, attention_mask, head_size: int, *, fast: bool = True,
+                    custom_bias: bool = False, fused: bool = False, round16: bool = True, dtype=np.float64,
+                    bias_scale: float | None = None):
+    """The attention stage of `forward` under the classifier's flags
+    (DeBERTa.swift:322-410); q, k, v [B, H, L, D], tables [H, P, D] ->
+    context [B, L, H*D].
+
+    fused (useFusedAttentionKernel, :337-354): the fused Metal kernel, score
+        (q.k + c2p + p2c) * (1/sqrt(3D)) in fp32, its output [B, L, H, D]
+        reshaped.
+    custom_bias (useCustomRelativeKernel, :357-372): the relative-bias Metal
+        kernel (fp32 c2p + p2c times the fp32 scale, masked keys -65504, fp16)
+        replaces the default bias; with `fast` it is the whole SDPA mask
+        (:383-385), else it is added to the content score with no `where`
+        (:401-403).
+    otherwise the default bias (:374-379), then SDPA with bias + key mask
+    (`fast`, :383-394) or the explicit-score path (:397-409).
+    `bias_scale` replaces both fp16(sqrt(3D)) divisors (exact cross-checks
+    against HF, which divides by the fp32 value).
+
+    pinned by: its pieces' pins (Metal-kernel known answers, brute force,
+    torch SDPA) and, with round16=False, the HF DeBERTa-v2 layer for every
+    flag combination (the flags change rounding points and masking, not the
+    exact mathematics).
+    """
+    B, H, L, D = np.shape(q)
+    c2p_idx, p2c_idx = relative_indices(L)
+    key_mask = additive_key_mask(attention_mask)[:, 0, 0, :]
+    if fused:
+        out = fused_attention_kernel(q, k, v, pos_key, pos_query, c2p_idx, p2c_idx, key_mask, scale_f32(D),
+                                     round16=round16)
+        return np.asarray(out, dtype).reshape(B, L, H * D)
+    if custom_bias:
+        scale = scale_f32(D) if bias_scale is None else 1.0 / bias_scale
+        bias = np.asarray(relative_bias_kernel(q, k, pos_key, pos_query, c2p_idx, p2c_idx, key_mask, scale,
+                                               round16=round16), dtype)
+        if fast:
+            return attention_sdpa_mask(q, k, v, bias, D, round16, dtype)
+        return attention_generic(q, k, v, bias, attention_mask, D, round16, dtype, where_mask=False,
+                                 content_scale=bias_scale)
+    bias = relative_bias_default(q, k, pos_key, pos_query, c2p_idx, p2c_idx, D, round16, dtype, bias_scale)
+    if fast:
+        return attention_default(q, k, v, bias, attention_mask, D, round16, dtype)
+    return attention_generic(q, k, v, bias, attention_mask, D, round16, dtype, content_scale=bias_scale)
 
 
 # ---------------------------------------------------------------------------
@@ -476,14 +553,20 @@ def relative_tables(weights: ModelWeights, config: Config, round16: bool = True,
 # ---------------------------------------------------------------------------
 def encoder_layer(hidden, lw: LayerWeights, pos_query, pos_key, attention_mask, config: Config,
                   round16: bool = True, dtype=np.float64, use_fused_kernels: bool = False,
-                  return_intermediates: bool = False, bias_scale: float | None = None):
-    """One DeBERTa layer of `forward` (DeBERTa.swift:296-428), default
-    fast-attention path.  hidden [B, L, C] -> [B, L, C].
+                  return_intermediates: bool = False, bias_scale: float | None = None,
+                  use_fast_attention: bool = True, use_custom_relative_kernel: bool = False,
+                  use_fused_attention_kernel: bool = False):
+    """One DeBERTa layer of `forward` (DeBERTa.swift:296-428).
+    hidden [B, L, C] -> [B, L, C].
 
-    use_fused_kernels mirrors `useFusedKernels` (DeBERTa.swift:449-462): the
-    residual sum is kept in fp32 (FusedKernels residual LN) instead of being
-    rounded to fp16 first.
+    The flags mirror GLiNERDecideClassifier.init (DeBERTa.swift:188-196):
+    the attention stage follows `attention_stage`; the residual LayerNorms use
+    the Metal kernel (fp32 sum, FusedKernels residual LN) whenever the
+    reference holds a FusedKernels instance, i.e. when any of
+    use_fused_kernels, use_custom_relative_kernel or use_fused_attention_kernel
+    is set (:230-232, :449-462); otherwise the fp16 sum `norm(x + residual)`.
     """
+    use_fused_kernels = use_fused_kernels or use_custom_relative_kernel or use_fused_attention_kernel
     B, L, C = hidden.shape
     H, D = config.num_attention_heads, config.head_size
     eps = config.layer_norm_eps
@@ -492,9 +575,9 @@ def encoder_layer(hidden, lw: LayerWeights, pos_query, pos_key, attention_mask, 
     q = np.transpose(qkv[:, :, 0], (0, 2, 1, 3))
     k = np.transpose(qkv[:, :, 1], (0, 2, 1, 3))
     v = np.transpose(qkv[:, :, 2], (0, 2, 1, 3))
-    c2p_idx, p2c_idx = relative_indices(L, config.position_buckets)
-    bias = relative_bias_default(q, k, pos_key, pos_query, c2p_idx, p2c_idx, D, round16, dtype, bias_scale)
-    ctx = attention_default(q, k, v, bias, attention_mask, D, round16, dtype)
+    ctx = attention_stage(q, k, v, pos_key, pos_query, attention_mask, D, fast=use_fast_attention,
+                          custom_bias=use_custom_relative_kernel, fused=use_fused_attention_kernel, round16=round16,
+                          dtype=dtype, bias_scale=bias_scale)
     res_ln = residual_layer_norm_kernel if use_fused_kernels else residual_layer_norm_default
     attn_out = linear(ctx, lw.out_w, lw.out_b, round16, dtype)
     h1 = res_ln(attn_out, hidden, lw.ln1_g, lw.ln1_b, eps, round16, dtype)
@@ -502,8 +585,7 @@ def encoder_layer(hidden, lw: LayerWeights, pos_query, pos_key, attention_mask, 
     ffn = linear(inter, lw.ffn_out_w, lw.ffn_out_b, round16, dtype)
     h2 = res_ln(ffn, h1, lw.ln2_g, lw.ln2_b, eps, round16, dtype)
     if return_intermediates:
-        return h2, dict(qkv=qkv.reshape(B, L, 3 * C), bias=bias, ctx=ctx, attn_out=attn_out, h1=h1,
-                        inter=inter, ffn=ffn)
+        return h2, dict(qkv=qkv.reshape(B, L, 3 * C), ctx=ctx, attn_out=attn_out, h1=h1, inter=inter, ffn=ffn)
     return h2
 
 
@@ -531,13 +613,16 @@ class OracleModel:
     """
 
     def __init__(self, weights: ModelWeights, config: Config, round16: bool = True, dtype=np.float64,
-                 use_fused_kernels: bool = False, bias_scale: float | None = None):
+                 use_fused_kernels: bool = False, bias_scale: float | None = None, use_fast_attention: bool = True,
+                 use_custom_relative_kernel: bool = False, use_fused_attention_kernel: bool = False):
         self.w = weights
         self.config = config
         self.round16 = round16
         self.dtype = dtype
         self.use_fused_kernels = use_fused_kernels
         self.bias_scale = bias_scale
+        self.flags = dict(use_fast_attention=use_fast_attention, use_custom_relative_kernel=use_custom_relative_kernel,
+                          use_fused_attention_kernel=use_fused_attention_kernel)
         self.tables = relative_tables(weights, config, round16, dtype)
 
     def embed(self, ids, attention_mask):
@@ -551,7 +636,7 @@ class OracleModel:
         for i in range(n):
             pq, pk = self.tables[i]
             h = encoder_layer(h, self.w.layers[i], pq, pk, attention_mask, self.config, self.round16,
-                              self.dtype, self.use_fused_kernels, bias_scale=self.bias_scale)
+                              self.dtype, self.use_fused_kernels, bias_scale=self.bias_scale, **self.flags)
         return h
 
     def forward(self, ids, attention_mask, marker_indices, marker_mask):

@@ -419,3 +419,126 @@ def test_general_index_kernels_vs_oracle_closed_form():
                                     dev(np.ascontiguousarray(pqh)), dev(c2p.astype(np.int32)),
                                     dev(p2c.astype(np.int32)), dev(key_mask), scale, B, H, L, 64, 512))
     assert np.max(np.abs(got - want)) <= 2e-3
+
+
+# ---------------------------------------------------------------------------
+# score chains of the classifier flags (DeBERTa.swift:337-409)
+# ---------------------------------------------------------------------------
+SCORE_FLAGS = {"explicit": dict(fast=False), "kernel_bias": dict(custom_bias=True),
+               "kernel_bias_explicit": dict(custom_bias=True, fast=False), "fused": dict(fused=True)}
+
+
+@pytest.mark.parametrize("L", [32, 96, 256, 512])
+@pytest.mark.parametrize("score", sorted(SCORE_FLAGS))
+def test_attention_score_chain_context(L, score):
+    """Context of each chain against the oracle's attention stage for the
+    same flags (B=2, H=2, one padded row).  Bound 4e-3 as the default chain:
+    the fp32 (GPU) vs float64 (oracle) accumulation moves an fp16 rounding
+    point by one ulp now and then, which moves a probability by ~1e-3
+    relative."""
+    B, H = 2, 2
+    q, k, v, pk, pq, mask = _attn_case(300 + L, B, H, L)
+    gpk, gpq = _gpu_tables(pk, pq, H)
+    pkh, pqh = _tables(pk, pq, H)
+    want = O.attention_stage(q, k, v, pkh, pqh, mask, 64, **SCORE_FLAGS[score])
+    got = host(fk().deberta_attention(dev(q), dev(k), dev(v), gpk, gpq, dev(mask), output="context", score=score))
+    assert got.shape == (B, L, H * 64)
+    err = np.abs(got - want)
+    assert err.max() <= 4e-3, err.max()
+    assert np.mean(err > 0) < 0.2  # mostly exact agreement with the rounded oracle
+
+
+@pytest.mark.parametrize("L", [32, 256, 512])
+@pytest.mark.parametrize("score", ["explicit", "kernel_bias", "fused"])
+def test_attention_score_chain_probs(L, score):
+    """Probabilities: masked keys exactly 0, rows sum to 1, |dP| <= 1e-3
+    against the oracle's probabilities of the same chain."""
+    B, H = 2, 2
+    q, k, v, pk, pq, mask = _attn_case(400 + L, B, H, L)
+    gpk, gpq = _gpu_tables(pk, pq, H)
+    pkh, pqh = _tables(pk, pq, H)
+    c2p, p2c = O.relative_indices(L)
+    km = np.where(mask > 0, 0.0, -65504.0)
+    if score == "explicit":
+        bias = O.relative_bias_default(q, k, pkh, pqh, c2p, p2c, 64)
+        qk = np.matmul(q.astype(np.float64), np.swapaxes(k, -1, -2).astype(np.float64))
+        s = O.f16(O.f16(O.f16(qk) / O.scale_f16(64)) + bias)
+        s = np.where(mask[:, None, None, :] > 0, s, -65504.0)
+        want = O.f16(O._softmax(s))
+    elif score == "kernel_bias":
+        bias = O.relative_bias_kernel(q, k, pkh, pqh, c2p, p2c, km, O.scale_f32(64))
+        qk = np.matmul(q.astype(np.float64), np.swapaxes(k, -1, -2).astype(np.float64))
+        want = O._softmax(qk * O.scale_f32(64) + bias)
+    else:
+        hh = np.arange(H)[:, None, None]
+        c2pt = np.einsum("bhqd,hqkd->bhqk", q.astype(np.float64), pkh.astype(np.float64)[hh, c2p[None]])
+        p2ct = np.einsum("bhkd,hqkd->bhqk", k.astype(np.float64), pqh.astype(np.float64)[hh, p2c.T[None]])
+        qk = np.matmul(q.astype(np.float64), np.swapaxes(k, -1, -2).astype(np.float64))
+        sc = np.where(mask[:, None, None, :] > 0, (qk + c2pt + p2ct) * O.scale_f32(64), -65504.0)
+        want = O._softmax(sc)
+    got = host(fk().deberta_attention(dev(q), dev(k), None, gpk, gpq, dev(mask), output="probs", score=score))
+    valid = np.broadcast_to(mask[:, None, None, :] > 0, got.shape)
+    assert np.all(got[~valid] == 0)
+    np.testing.assert_allclose(got.sum(-1), 1.0, atol=3e-3)
+    assert np.max(np.abs(got - want)) <= 1e-3
+
+
+@pytest.mark.parametrize("L", [32, 160, 256, 512])
+def test_relative_bias_closed_form_indices(L):
+    """gd_relative_bias with NULL indices (the MFMA kernel-bias chain) against
+    the oracle's Metal-kernel restatement on the closed-form indices: one
+    fp16 rounding of an fp32 sum, so within one ulp; masked keys exactly
+    -65504.  The general-index kernel on the same indices agrees too."""
+    B, H = 2, 3
+    q, k, v, pk, pq, mask = _attn_case(500 + L, B, H, L)
+    pkh, pqh = (np.ascontiguousarray(t) for t in _tables(pk, pq, H))
+    c2p, p2c = O.relative_indices(L)
+    key_mask = np.where(mask > 0, 0.0, -65504.0).astype(np.float16)
+    scale = O.scale_f32(64)
+    want = O.relative_bias_kernel(q, k, pkh, pqh, c2p, p2c, key_mask, scale)
+    got = host(fk().relative_bias(dev(q), dev(k), dev(pkh), dev(pqh), None, None, dev(key_mask), scale, B, H, L, 64,
+                                  512))
+    masked = np.broadcast_to(mask[:, None, None, :] == 0, got.shape)
+    assert np.all(got[masked] == -65504.0)
+    # |fp32 sum - exact| <= 4 sqrt(D) 2^-24 sum|terms| (as for the GEMMs), and
+    # each side rounds once to fp16 (half an ulp each): near-zero biases (c2p
+    # + p2c cancelling) sit on the 2^-24 subnormal grid, where the
+    # accumulation term is several ulps
+    acc = 4.0 * 8.0 * 2.0 ** -24 * O.relative_bias_kernel(np.abs(q), np.abs(k), np.abs(pkh), np.abs(pqh), c2p, p2c,
+                                                            np.zeros_like(key_mask), scale, round16=False)
+    valid = ~masked
+    err = np.abs(got - want)[valid]
+    bound = (np.maximum(ulp16(got), ulp16(want)) + acc)[valid]
+    assert np.all(err <= bound + 1e-12), (err - bound).max()
+    assert np.mean(err > 0) < 2e-2  # mostly the same fp16 value as the exactly rounded oracle
+    general = host(fk().relative_bias(dev(q), dev(k), dev(pkh), dev(pqh), dev(c2p.astype(np.int32)),
+                                      dev(p2c.astype(np.int32)), dev(key_mask), scale, B, H, L, 64, 512))
+    err = np.abs(got - general)[valid]
+    bound = (np.maximum(ulp16(got), ulp16(general)) + 2 * acc)[valid]
+    assert np.all(err <= bound + 1e-12), (err - bound).max()
+
+
+@pytest.mark.parametrize("L", [32, 256, 512])
+def test_fused_attention_closed_form_indices(L):
+    """gd_fused_attention with NULL indices (the MFMA fused chain) against the
+    oracle's restatement of the fused Metal kernel: [B, L, H, D] output."""
+    B, H = 2, 2
+    q, k, v, pk, pq, mask = _attn_case(600 + L, B, H, L)
+    pkh, pqh = (np.ascontiguousarray(t) for t in _tables(pk, pq, H))
+    c2p, p2c = O.relative_indices(L)
+    key_mask = np.where(mask > 0, 0.0, -65504.0).astype(np.float16)
+    scale = O.scale_f32(64)
+    want = O.fused_attention_kernel(q, k, v, pkh, pqh, c2p, p2c, key_mask, scale)
+    got = host(fk().fused_attention(dev(q), dev(k), dev(v), dev(pkh), dev(pqh), None, None, dev(key_mask), scale, B,
+                                    H, L, 64, 512))
+    assert got.shape == (B, L, H, 64)
+    assert np.max(np.abs(got - want)) <= 2e-3
+
+
+def test_attention_rejects_bias_output_on_chains_without_a_bias():
+    from gliner_decide import GlinerDecideError
+    q, k, v, pk, pq, mask = _attn_case(7, 1, 1, 32)
+    gpk, gpq = _gpu_tables(pk, pq, 1)
+    for score in ("explicit", "kernel_bias_explicit", "fused"):
+        with pytest.raises(GlinerDecideError):
+            fk().deberta_attention(dev(q), dev(k), dev(v), gpk, gpq, dev(mask), output="bias", score=score)

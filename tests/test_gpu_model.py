@@ -350,3 +350,97 @@ def test_bucket_mix_workload():
             rows = [v - 1]
             compare_decisions(got[rows], _oracle_rows(om, a, rows), [x.tasks[i] for i in rows])
     assert rows_run == 4096 and checked == {32, 64, 96, 128, 256, 512}
+
+
+# ---------------------------------------------------------------------------
+# every constructor flag of GLiNERDecideClassifier.init (DeBERTa.swift:188-196)
+# ---------------------------------------------------------------------------
+FLAG_SETS = {
+    "fused_kernels": dict(use_fused_kernels=True),
+    "generic_attention": dict(use_fast_attention=False),
+    "custom_relative_kernel": dict(use_custom_relative_kernel=True),
+    "custom_relative_generic": dict(use_custom_relative_kernel=True, use_fast_attention=False),
+    "fused_attention_kernel": dict(use_fused_attention_kernel=True),
+}
+
+
+@pytest.mark.parametrize("name", sorted(FLAG_SETS))
+def test_classifier_flags_match_oracle(name):
+    """Two full-width layers + head with padded rows under each flag set,
+    against OracleModel with the same flags: hidden states and logits, with
+    the bar of the default-path test (the spread between the float64 and
+    float32 restatements, x2, floor 2e-3).  Packed, padded and full-row
+    classify agree bit for bit."""
+    from gliner_decide import DecisionInput, GLiNERDecideClassifier
+    from gliner_decide.config import DeBERTaV2Configuration
+    from gliner_decide.synthetic import synthetic_weights
+    flags = FLAG_SETS[name]
+    pc = DeBERTaV2Configuration(num_hidden_layers=2, vocab_size=3000)
+    w = synthetic_weights(pc, seed=19)
+    oc = O.Config(**{k: getattr(pc, k) for k in O.Config.__dataclass_fields__})
+    gpu = GLiNERDecideClassifier(w, pc, **flags)
+    full = GLiNERDecideClassifier(w, pc, full_rows=True, **flags)
+    r = np.random.default_rng(5)
+    B, L = 3, 96
+    ids = r.integers(1000, 3000, size=(B, L)).astype(np.int32)
+    lengths = np.array([96, 61, 17])
+    mask = (np.arange(L)[None] < lengths[:, None]).astype(np.float16)
+    ids[mask == 0] = 0
+    mi = np.array([[[1, 2, 3, 4], [5, 6, 0, 0]]] * B, np.int32)
+    mm = np.array([[[1, 1, 1, 1], [1, 1, 0, 0]]] * B, np.float32)
+    inp = DecisionInput(ids, mask, mi, mm)
+    packed = gpu.classify(inp).logits.float().cpu().numpy()
+    padded = gpu.classify_device(*inp.to_device()).float().cpu().numpy()
+    every = full.classify_device(*inp.to_device()).float().cpu().numpy()
+    np.testing.assert_array_equal(packed, every)
+    np.testing.assert_array_equal(padded, every)
+    hid = gpu.encode(inp).float().cpu().numpy()
+    mw = O.ModelWeights.from_store(w, oc)
+    om = O.OracleModel(mw, oc, **flags)
+    want_h = om.encode(ids, mask)
+    om32 = O.OracleModel(O.ModelWeights.from_store(w, oc), oc, dtype=np.float32, **flags)
+    floor = np.max(np.abs(om32.encode(ids, mask).astype(np.float64) - want_h))
+    err = np.max(np.abs(hid - want_h))
+    assert err <= max(2e-3, 2 * floor), (name, err, floor)
+    want_logits = O.classifier_head(want_h, mi, mm, mw)
+    assert np.all(packed[mm == 0] == -10000.0)
+    assert np.max(np.abs(packed - want_logits)) <= 2e-3, name
+    # and the flag changes the computation: the default graph's logits differ
+    if name != "fused_kernels":
+        base = GLiNERDecideClassifier(w, pc).classify(inp).logits.float().cpu().numpy()
+        assert not np.array_equal(base, packed), name
+
+
+def test_safetensors_checkpoint_matches_oracle(tmp_path):
+    """The path of WeightStore(url:) (Weights.swift:26-28) over the format of
+    prepare_model.py:82-113: weights written with safetensors, read by the
+    library's own parser (gd_weight_store_load_safetensors), then classify.
+    The logits equal those of the classifier built from the same arrays
+    through gd_weight_store_add (bit for bit), and the oracle built from the
+    file's arrays (read back by the safetensors package) within 2e-3."""
+    from safetensors.numpy import load_file, save_file
+    from gliner_decide import DecisionInput, GLiNERDecideClassifier
+    from gliner_decide.config import DeBERTaV2Configuration
+    from gliner_decide.synthetic import synthetic_weights
+    from gliner_decide.weights import WeightStore
+    pc = DeBERTaV2Configuration(num_hidden_layers=2, vocab_size=3000)
+    w = synthetic_weights(pc, seed=29)
+    path = tmp_path / "gliner_decide_fp16.safetensors"
+    save_file(w, str(path), metadata={"precision": "float16", "scope": "encoder+classification-only"})
+    store = WeightStore(url=path)
+    assert len(store) == len(w)
+    from_file = GLiNERDecideClassifier(store, pc)
+    from_arrays = GLiNERDecideClassifier(w, pc)
+    r = np.random.default_rng(3)
+    B, L = 2, 64
+    ids = r.integers(1000, 3000, size=(B, L)).astype(np.int32)
+    mask = (np.arange(L)[None] < np.array([[64], [33]])).astype(np.float16)
+    ids[mask == 0] = 0
+    mi = np.array([[[1, 2, 3]]] * B, np.int32)
+    mm = np.ones((B, 1, 3), np.float32)
+    inp = DecisionInput(ids, mask, mi, mm)
+    got = from_file.classify(inp).logits.float().cpu().numpy()
+    np.testing.assert_array_equal(got, from_arrays.classify(inp).logits.float().cpu().numpy())
+    oc = O.Config(**{k: getattr(pc, k) for k in O.Config.__dataclass_fields__})
+    om = O.OracleModel(O.ModelWeights.from_store(load_file(str(path)), oc), oc)
+    assert np.max(np.abs(got - om.forward(ids, mask, mi, mm))) <= 2e-3

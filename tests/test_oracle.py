@@ -188,6 +188,99 @@ def test_attention_vs_torch_sdpa():
     np.testing.assert_allclose(got, want, atol=1e-6)  # the fp16 add of a -65504 mask vs -inf: identical probs
 
 
+def test_attention_sdpa_mask_vs_torch_sdpa():
+    """The useCustomRelativeKernel SDPA: the kernel's bias is the whole mask."""
+    r = np.random.default_rng(15)
+    B, H, L, D = 2, 2, 24, 64
+    q, k, v = (r.standard_normal((B, H, L, D)) for _ in range(3))
+    mask = r.standard_normal((B, H, L, L))
+    mask[1, :, :, 20:] = -65504.0
+    got = O.attention_sdpa_mask(q, k, v, mask, D, round16=False)
+    want = torch.nn.functional.scaled_dot_product_attention(
+        torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v), attn_mask=torch.from_numpy(mask),
+        scale=O.scale_f32(D)).numpy()
+    np.testing.assert_allclose(got, np.transpose(want, (0, 2, 1, 3)).reshape(B, L, H * D), atol=1e-12)
+
+
+def _generic_brute_force(q, k, v, bias, mask, D, where_mask=True):
+    """DeBERTa.swift:397-409 element by element: every fp16 array the MLX
+    graph writes is rounded with np.float16 on a Python float."""
+    B, H, L, _ = q.shape
+    s16 = float(np.float16(math.sqrt(3 * D)))
+    out = np.zeros((B, L, H * D))
+    for b in range(B):
+        for h in range(H):
+            for i in range(L):
+                scores = []
+                for j in range(L):
+                    qk = float(np.float16(sum(float(q[b, h, i, d]) * float(k[b, h, j, d]) for d in range(D))))
+                    content = float(np.float16(qk / s16))
+                    sc = float(np.float16(content + float(bias[b, h, i, j])))
+                    if where_mask and not mask[b, j] > 0:
+                        sc = -65504.0
+                    scores.append(sc)
+                m = max(scores)
+                e = [math.exp(x - m) for x in scores]
+                tot = math.fsum(e)
+                p = [float(np.float16(x / tot)) for x in e]
+                for d in range(D):
+                    out[b, i, h * D + d] = float(np.float16(math.fsum(p[j] * float(v[b, h, j, d]) for j in range(L))))
+    return out
+
+
+def test_attention_generic_brute_force():
+    """Explicit-score path: fp16(QK^T), fp16 divide by fp16(sqrt(3D)), fp16
+    add of the bias, where(valid, ., -65504), fp16 softmax, fp16 P.V."""
+    r = np.random.default_rng(11)
+    B, H, L, D = 2, 2, 12, 8
+    q, k, v = (r.standard_normal((B, H, L, D)).astype(np.float16) for _ in range(3))
+    bias = (2 * r.standard_normal((B, H, L, L))).astype(np.float16)
+    mask = np.ones((B, L), np.float16)
+    mask[1, 7:] = 0
+    got = O.attention_generic(q, k, v, bias, mask, D)
+    np.testing.assert_array_equal(got, _generic_brute_force(q, k, v, bias, mask, D))
+    # the useCustomRelativeKernel form: no where, the bias carries -65504
+    bias[1, :, :, 7:] = -65504.0
+    got = O.attention_generic(q, k, v, bias, mask, D, where_mask=False)
+    np.testing.assert_array_equal(got, _generic_brute_force(q, k, v, bias, mask, D, where_mask=False))
+
+
+def test_attention_generic_all_masked_row_is_uniform():
+    """where(valid, s, -65504) on a row with no valid key: every score is
+    -65504, so the softmax is uniform over all L keys and the context is the
+    mean of V (rounded through fp16 P)."""
+    r = np.random.default_rng(12)
+    B, H, L, D = 1, 1, 16, 8
+    q, k, v = (r.standard_normal((B, H, L, D)).astype(np.float16) for _ in range(3))
+    bias = r.standard_normal((B, H, L, L)).astype(np.float16)
+    got = O.attention_generic(q, k, v, bias, np.zeros((B, L), np.float16), D)
+    p16 = float(np.float16(1.0 / L))
+    want = O.f16(p16 * v.astype(np.float64).sum(axis=2))  # [B, H, D]
+    np.testing.assert_array_equal(got[0], np.broadcast_to(want[0, 0], (L, D)))
+
+
+def test_planted_generic_mistakes_are_caught():
+    """The brute force above distinguishes the plausible slips: the fp32
+    scale multiplied instead of the fp16 divide, QK^T not rounded first, and
+    a dropped where()."""
+    r = np.random.default_rng(13)
+    B, H, L, D = 1, 2, 12, 8
+    q, k, v = (r.standard_normal((B, H, L, D)).astype(np.float16) for _ in range(3))
+    bias = (2 * r.standard_normal((B, H, L, L))).astype(np.float16)
+    mask = np.ones((B, L), np.float16)
+    mask[0, 9:] = 0
+    truth = _generic_brute_force(q, k, v, bias, mask, D)
+    qk = np.matmul(q.astype(np.float64), np.swapaxes(k, -1, -2).astype(np.float64))
+    fp32_scale = O.f16(O.f16(qk) * O.scale_f32(D))
+    no_inner = O.f16(qk / O.scale_f16(D))
+    for content in (fp32_scale, no_inner):
+        scores = np.where(mask[:, None, None, :] > 0, O.f16(content + bias), -65504.0)
+        p = O.f16(O._softmax(scores))
+        bad = O.f16(np.matmul(p, v.astype(np.float64))).transpose(0, 2, 1, 3).reshape(B, L, H * D)
+        assert not np.array_equal(bad, truth)
+    assert not np.array_equal(O.attention_generic(q, k, v, bias, mask, D, where_mask=False), truth)
+
+
 # ---------------------------------------------------------------------------
 # Whole layers -- HF transformers DeBERTa-v2 (float64, same fp16 weights)
 # ---------------------------------------------------------------------------
@@ -220,6 +313,42 @@ def test_encoder_matches_hf_log_buckets_valid_rows(golden):
     m, _ = _oracle_for(dict(hidden_size=128, intermediate_size=256, num_hidden_layers=2, num_attention_heads=2,
                             vocab_size=512, classifier_hidden=256), seed=7)
     out = m.encode(g["ids"], g["mask"])
+    for b, n in enumerate(g["lengths"]):
+        np.testing.assert_allclose(out[b, :n], g["out"][b, :n], atol=2e-5)
+
+
+FLAG_SETS = [dict(use_fast_attention=False), dict(use_custom_relative_kernel=True),
+             dict(use_custom_relative_kernel=True, use_fast_attention=False), dict(use_fused_attention_kernel=True),
+             dict(use_fused_kernels=True)]
+
+
+@pytest.mark.parametrize("flags", FLAG_SETS, ids=lambda f: "+".join(sorted(f)))
+def test_every_classifier_flag_matches_hf_exactly(golden, flags):
+    """Each flag combination of GLiNERDecideClassifier.init changes where the
+    graph rounds and how it masks, not the mathematics: evaluated exactly
+    (round16=False) every one reproduces HF DeBERTa-v2 -- full width at L=32,
+    and at L=256 (log buckets) with a padded row, on its valid rows.  This
+    pins each mode's structure: which terms are summed, the index tensors
+    and their transposes, the mask placement, the output layouts."""
+    import sys
+    from pathlib import Path
+    sys.path.insert(0, str(Path(__file__).resolve().parents[1] / "gliner-decide-metal_amd"))
+    from gliner_decide.config import DeBERTaV2Configuration
+    from gliner_decide.synthetic import synthetic_weights
+
+    def model(cfg_kwargs, seed):
+        pc = DeBERTaV2Configuration(**cfg_kwargs)
+        w = synthetic_weights(pc, seed=seed)
+        oc = O.Config(**{k: getattr(pc, k) for k in O.Config.__dataclass_fields__})
+        hf_scale = float(np.float32(math.sqrt(3 * oc.head_size)))
+        return O.OracleModel(O.ModelWeights.from_store(w, oc), oc, round16=False, bias_scale=hf_scale, **flags)
+
+    g = golden("hf_layer_c1024_l32.npz")
+    out = model(dict(num_hidden_layers=1, vocab_size=2048), 1).encode(g["ids"], g["mask"])
+    np.testing.assert_allclose(out, g["out"], atol=2e-5)
+    g = golden("hf_encoder_c128_l256.npz")
+    out = model(dict(hidden_size=128, intermediate_size=256, num_hidden_layers=2, num_attention_heads=2,
+                     vocab_size=512, classifier_hidden=256), 7).encode(g["ids"], g["mask"])
     for b, n in enumerate(g["lengths"]):
         np.testing.assert_allclose(out[b, :n], g["out"][b, :n], atol=2e-5)
 
