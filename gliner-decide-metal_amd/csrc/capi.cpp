@@ -397,6 +397,21 @@ int gd_classifier_classify_packed(gd_classifier* model, const int32_t* input_ids
                               max_options, logits_out, as_stream(stream), total_tokens);
 }
 
+int gd_classifier_classify_static(gd_classifier* model, const int32_t* input_ids, const void* attention_mask,
+                                  const int32_t* marker_indices, const float* marker_mask, int64_t batch,
+                                  int64_t seq_len, int64_t max_heads, int64_t max_options, int64_t total_tokens,
+                                  void* logits_out, void* stream) {
+  clear_error();
+  GD_RETURN_IF_ERROR(check_forward_args(model, input_ids, attention_mask, batch, seq_len));
+  GD_CHECK_ARG(marker_indices && marker_mask && logits_out, "null marker or output pointer");
+  GD_CHECK_SHAPE(max_heads >= 1 && max_options >= 1 && batch * max_heads * max_options <= (1 << 24),
+                 "bad marker shape");
+  GD_CHECK_SHAPE(total_tokens >= -1 && total_tokens <= batch * seq_len, "total_tokens %lld outside [-1, %lld]",
+                 (long long)total_tokens, (long long)(batch * seq_len));
+  return model->impl.classify_static(input_ids, attention_mask, marker_indices, marker_mask, batch, seq_len, max_heads,
+                                     max_options, logits_out, as_stream(stream), total_tokens);
+}
+
 int gd_classifier_encode(gd_classifier* model, const int32_t* input_ids, const void* attention_mask, int64_t batch,
                          int64_t seq_len, int32_t num_layers, void* hidden_out, void* stream) {
   clear_error();

@@ -25,6 +25,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 
 #include "gd_common.hpp"
 #include "gd_kernels.hpp"
@@ -32,6 +33,16 @@
 namespace gd {
 
 namespace {
+
+// Workspace of classify_static, the classify that allocates nothing: one copy
+// of this array per GPU (each device holds it from the library's first use
+// there until the process ends), shared by every context on that GPU.  Host
+// code names it only in hipGetSymbolAddress; kernels take its per-device
+// address (static_ws_base_).
+constexpr size_t kStaticWorkspaceBytes = size_t(48) << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticWorkspaceBytes];
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {};  // device address of `scratch`, per device
 
 struct HipDeviceGuard {
   int prev = -1;
@@ -163,6 +174,7 @@ int Classifier::init(const WeightStore& store, const gd_config& cfg, uint32_t fl
     GD_RETURN_IF_ERROR(store.require(req.first, req.second, GD_F16, &t));
   }
   GD_HIP_CHECK(hipGetDevice(&device_));
+  GD_RETURN_IF_ERROR(init_static_workspace());    // this device's address of the no-alloc workspace
   GD_RETURN_IF_ERROR(ensure_gelu_table(stream));  // before any graph capture of the FFN
   GD_RETURN_IF_ERROR(ensure_relative_index_table(stream));  // and of the attention
 
@@ -230,9 +242,9 @@ int Classifier::init(const WeightStore& store, const gd_config& cfg, uint32_t fl
 
 int Classifier::reserve(int64_t B, int64_t L, int64_t Hh, int64_t O) {
   const int64_t T = B * L, M = B * Hh * O;
-  if (T <= ws_tokens_ && M <= ws_markers_) return GD_OK;
+  if (T <= ws_.tokens && M <= ws_.markers_cap) return GD_OK;
   const int64_t C = cfg_.hidden_size, F = cfg_.intermediate_size, CH = cfg_.classifier_hidden;
-  const int64_t nt = std::max(T, ws_tokens_), nm = std::max(M, ws_markers_);
+  const int64_t nt = std::max(T, ws_.tokens), nm = std::max(M, ws_.markers_cap);
   release_graphs();  // captured graphs reference the old workspace
   HipDeviceGuard guard(device_);
   (void)hipDeviceSynchronize();
@@ -243,7 +255,6 @@ int Classifier::reserve(int64_t B, int64_t L, int64_t Hh, int64_t O) {
   device_bytes_ -= ws_bytes_;
   const int64_t before = device_bytes_;
   ws_ = Workspace{};
-  ws_tokens_ = ws_markers_ = ws_sched_cap_ = 0;
   auto A = [&](size_t bytes, void** p) { return device_alloc(bytes, p, workspace_allocs_); };
   GD_RETURN_IF_ERROR(A((size_t)nt * C * 2, &ws_.hidden));
   GD_RETURN_IF_ERROR(A((size_t)nt * 3 * C * 2, &ws_.qkv));
@@ -266,14 +277,76 @@ int Classifier::reserve(int64_t B, int64_t L, int64_t Hh, int64_t O) {
   GD_RETURN_IF_ERROR(A((size_t)sched_cap * 4, &ws_.sched));
   GD_RETURN_IF_ERROR(A((size_t)nt * 4, &ws_.q_len));  // B <= B * L
   ws_bytes_ = device_bytes_ - before;
-  ws_tokens_ = nt;
-  ws_markers_ = nm;
-  ws_sched_cap_ = sched_cap;
+  ws_.tokens = nt;
+  ws_.markers_cap = nm;
+  ws_.sched_cap = sched_cap;
   return GD_OK;
 }
 
+// Takes this device's address of the static workspace, once per device (the
+// device is current: init runs on it).
+int Classifier::init_static_workspace() {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (device_ < 0 || device_ >= 64) return fail(GD_ERR_UNSUPPORTED, "device index out of range");
+  if (!g_scratch_ptr[device_]) {
+    void* p = nullptr;
+    GD_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    g_scratch_ptr[device_] = p;
+  }
+  static_ws_base_ = g_scratch_ptr[device_];
+  return GD_OK;
+}
+
+// The forward's buffers for T tokens, M marker slots and B batch rows, laid
+// out from `base` (each 256-byte aligned); returns the bytes they span.  No
+// graph staging (the static path runs eagerly).  With base = nullptr only
+// the size is computed.
+int64_t Classifier::carve_workspace(Workspace& w, uint8_t* base, int64_t T, int64_t M, int64_t B,
+                                    int64_t sched_slots) const {
+  const int64_t C = cfg_.hidden_size, F = cfg_.intermediate_size, CH = cfg_.classifier_hidden;
+  int64_t off = 0;
+  auto take = [&](int64_t bytes, void** p) {
+    *p = base ? base + off : nullptr;
+    off += (bytes + 255) / 256 * 256;
+  };
+  take(T * C * 2, &w.hidden);
+  take(T * 3 * C * 2, &w.qkv);
+  take(T * C * 2, &w.ctx);
+  take(T * C * 2, &w.tmp);
+  take(T * F * 2, &w.ffn);
+  take(M * 4, &w.marker_rows);
+  take(M * CH * 2, &w.inner);
+  take(B * 4, &w.row_len);
+  take((B + 1) * 4, &w.row_off);
+  take(T * 4, &w.row_map);
+  take(sched_slots * 4, &w.sched);
+  take(B * 4, &w.q_len);
+  w.tokens = T;
+  w.markers_cap = M;
+  w.sched_cap = sched_slots;
+  return off;
+}
+
+int Classifier::classify_static(const int32_t* ids, const void* mask, const int32_t* markers, const float* marker_mask,
+                                int64_t B, int64_t L, int64_t Hh, int64_t O, void* logits, hipStream_t stream,
+                                int64_t packed_tokens) {
+  if (!static_ws_base_) return fail(GD_ERR_UNSUPPORTED, "the static workspace has no device address");
+  const int64_t T = packed_tokens >= 0 ? packed_tokens : B * L, M = B * Hh * O;
+  const int64_t slots = attention_schedule_slots(B, cfg_.num_attention_heads, L);
+  Workspace w;
+  const int64_t need = carve_workspace(w, nullptr, T, M, B, slots);
+  if (need > (int64_t)kStaticWorkspaceBytes) {
+    set_error("classify_static: %lld tokens and %lld marker slots need %lld bytes of workspace; the static "
+              "workspace holds %zu (2048 tokens and 1024 marker slots at hidden 1024, intermediate 4096)",
+              (long long)T, (long long)M, (long long)need, kStaticWorkspaceBytes);
+    return GD_ERR_SHAPE;
+  }
+  carve_workspace(w, static_cast<uint8_t*>(static_ws_base_), T, M, B, slots);
+  return forward(w, ids, mask, markers, marker_mask, B, L, Hh, O, logits, stream, nullptr, packed_tokens);
+}
+
 // One encoder layer (DeBERTa.swift:296-428).
-int Classifier::layer_forward(int li, const void* mask, int64_t B, int64_t L, hipStream_t stream, StageHook* hook,
+int Classifier::layer_forward(const Workspace& w, int li, const void* mask, int64_t B, int64_t L, hipStream_t stream, StageHook* hook,
                               const Rows& rows, const int32_t* q_len, int64_t marker_count) {
   const Layer& Ly = layers_[li];
   const int64_t C = cfg_.hidden_size, F = cfg_.intermediate_size, H = cfg_.num_attention_heads, D = C / H;
@@ -289,7 +362,7 @@ int Classifier::layer_forward(int li, const void* mask, int64_t B, int64_t L, hi
 
   if (hook) hook->begin(stream);
   // QKV projection (:298-320)
-  GD_RETURN_IF_ERROR(launch_linear(ws_.hidden, Ly.qkv_w, Ly.qkv_b, ws_.qkv, T, 3 * C, C, C, 3 * C, nullptr, 0,
+  GD_RETURN_IF_ERROR(launch_linear(w.hidden, Ly.qkv_w, Ly.qkv_b, w.qkv, T, 3 * C, C, C, 3 * C, nullptr, 0,
                                    GD_EPI_BIAS, stream));
   if (hook) {
     std::snprintf(name, sizeof name, "layer_%d_attention_projection", li);
@@ -298,7 +371,7 @@ int Classifier::layer_forward(int li, const void* mask, int64_t B, int64_t L, hi
   }
   // relative bias + masked softmax + P.V (:322-410)
   AttentionArgs a{};
-  const half_t* qkv = static_cast<const half_t*>(ws_.qkv);
+  const half_t* qkv = static_cast<const half_t*>(w.qkv);
   a.q = qkv;
   a.k = qkv + C;
   a.v = qkv + 2 * C;
@@ -331,7 +404,7 @@ int Classifier::layer_forward(int li, const void* mask, int64_t B, int64_t L, hi
   else
     a.score = explicit_scores ? kScoreExplicit : kScoreDefault;
   a.scale_rel = a.scale_qk;  // 1 / sqrt(3 D), the Metal kernels' `scale` (:347, :366)
-  a.out = ws_.ctx;
+  a.out = w.ctx;
   a.ldo = C;
   a.row_len = rows.len;
   a.row_off = rows.off;
@@ -344,25 +417,25 @@ int Classifier::layer_forward(int li, const void* mask, int64_t B, int64_t L, hi
     hook->end(name, stream);
     hook->begin(stream);
   }
-  // Rows leaving the layer: all T in place in ws_.hidden, or the marker rows
-  // compact in ws_.qkv (free once the attention has read Q, K and V): their
-  // context rows (gathered into ws_.ffn, free until the FFN) go through the
+  // Rows leaving the layer: all T in place in w.hidden, or the marker rows
+  // compact in w.qkv (free once the attention has read Q, K and V): their
+  // context rows (gathered into w.ffn, free until the FFN) go through the
   // output projection, their hidden rows are gathered for the residual;
   // every later step is row-wise.
   const bool compact = marker_count >= 0;
   const int64_t R = compact ? marker_count : T;
-  void* hid = compact ? ws_.qkv : ws_.hidden;
-  void* ctx = compact ? ws_.ffn : ws_.ctx;
+  void* hid = compact ? w.qkv : w.hidden;
+  void* ctx = compact ? w.ffn : w.ctx;
   if (compact) {
-    const int32_t* rows_m = static_cast<const int32_t*>(ws_.marker_rows);
-    GD_RETURN_IF_ERROR(launch_gather_rows(ws_.ctx, rows_m, R, T, C, ctx, stream));
-    GD_RETURN_IF_ERROR(launch_gather_rows(ws_.hidden, rows_m, R, T, C, hid, stream));
+    const int32_t* rows_m = static_cast<const int32_t*>(w.marker_rows);
+    GD_RETURN_IF_ERROR(launch_gather_rows(w.ctx, rows_m, R, T, C, ctx, stream));
+    GD_RETURN_IF_ERROR(launch_gather_rows(w.hidden, rows_m, R, T, C, hid, stream));
   }
   // output projection + residual LayerNorm (:412-418)
   GD_RETURN_IF_ERROR(
-      launch_linear(ctx, Ly.out_w, Ly.out_b, ws_.tmp, R, C, C, C, C, nullptr, 0, GD_EPI_BIAS, stream));
+      launch_linear(ctx, Ly.out_w, Ly.out_b, w.tmp, R, C, C, C, C, nullptr, 0, GD_EPI_BIAS, stream));
   GD_RETURN_IF_ERROR(
-      launch_residual_layer_norm(ws_.tmp, hid, Ly.ln1_g, Ly.ln1_b, hid, R, C, eps, ln_flags, stream));
+      launch_residual_layer_norm(w.tmp, hid, Ly.ln1_g, Ly.ln1_b, hid, R, C, eps, ln_flags, stream));
   if (hook) {
     std::snprintf(name, sizeof name, "layer_%d_attention_output", li);
     hook->end(name, stream);
@@ -370,11 +443,11 @@ int Classifier::layer_forward(int li, const void* mask, int64_t B, int64_t L, hi
   }
   // feed-forward + residual LayerNorm (:420-427)
   GD_RETURN_IF_ERROR(
-      launch_linear(hid, Ly.inter_w, Ly.inter_b, ws_.ffn, R, F, C, C, F, nullptr, 0, GD_EPI_BIAS_GELU, stream));
+      launch_linear(hid, Ly.inter_w, Ly.inter_b, w.ffn, R, F, C, C, F, nullptr, 0, GD_EPI_BIAS_GELU, stream));
   GD_RETURN_IF_ERROR(
-      launch_linear(ws_.ffn, Ly.ffn_w, Ly.ffn_b, ws_.tmp, R, C, F, F, C, nullptr, 0, GD_EPI_BIAS, stream));
+      launch_linear(w.ffn, Ly.ffn_w, Ly.ffn_b, w.tmp, R, C, F, F, C, nullptr, 0, GD_EPI_BIAS, stream));
   GD_RETURN_IF_ERROR(
-      launch_residual_layer_norm(ws_.tmp, hid, Ly.ln2_g, Ly.ln2_b, hid, R, C, eps, ln_flags, stream));
+      launch_residual_layer_norm(w.tmp, hid, Ly.ln2_g, Ly.ln2_b, hid, R, C, eps, ln_flags, stream));
   if (hook) {
     std::snprintf(name, sizeof name, "layer_%d_feed_forward", li);
     hook->end(name, stream);
@@ -382,19 +455,19 @@ int Classifier::layer_forward(int li, const void* mask, int64_t B, int64_t L, hi
   return GD_OK;
 }
 
-int Classifier::encode_into_workspace(const int32_t* ids, const void* mask, int64_t B, int64_t L, int num_layers,
+int Classifier::encode_into_workspace(const Workspace& w, const int32_t* ids, const void* mask, int64_t B, int64_t L, int num_layers,
                                       hipStream_t stream, StageHook* hook, const Rows& rows) {
   const int64_t T = rows.tokens >= 0 ? rows.tokens : B * L;
   if (hook) hook->begin(stream);
-  GD_RETURN_IF_ERROR(launch_embedding_layer_norm(ids, mask, word_emb_, emb_g_, emb_b_, ws_.hidden, T,
+  GD_RETURN_IF_ERROR(launch_embedding_layer_norm(ids, mask, word_emb_, emb_g_, emb_b_, w.hidden, T,
                                                  cfg_.hidden_size, cfg_.vocab_size, cfg_.layer_norm_eps, err_flag_,
                                                  stream, rows.map, B * L));
   if (hook) hook->end("embedding", stream);
-  for (int i = 0; i < num_layers; ++i) GD_RETURN_IF_ERROR(layer_forward(i, mask, B, L, stream, hook, rows));
+  for (int i = 0; i < num_layers; ++i) GD_RETURN_IF_ERROR(layer_forward(w, i, mask, B, L, stream, hook, rows));
   return GD_OK;
 }
 
-int Classifier::forward(const int32_t* ids, const void* mask, const int32_t* markers, const float* marker_mask,
+int Classifier::forward(const Workspace& w, const int32_t* ids, const void* mask, const int32_t* markers, const float* marker_mask,
                         int64_t B, int64_t L, int64_t Hh, int64_t O, void* logits, hipStream_t stream,
                         StageHook* hook, int64_t packed_tokens, bool packed_exact) {
   const int64_t C = cfg_.hidden_size, CH = cfg_.classifier_hidden;
@@ -406,24 +479,24 @@ int Classifier::forward(const int32_t* ids, const void* mask, const int32_t* mar
   const bool packed = packed_tokens >= 0;
   Rows rows;
   if (packed || !(flags_ & GD_FULL_ROWS)) {
-    rows.len = static_cast<const int32_t*>(ws_.row_len);
-    GD_RETURN_IF_ERROR(launch_row_extent(mask, markers, marker_mask, B, L, Hh * O, static_cast<int32_t*>(ws_.row_len),
+    rows.len = static_cast<const int32_t*>(w.row_len);
+    GD_RETURN_IF_ERROR(launch_row_extent(mask, markers, marker_mask, B, L, Hh * O, static_cast<int32_t*>(w.row_len),
                                          stream));
   }
   if (packed) {
-    rows.off = static_cast<const int32_t*>(ws_.row_off);
-    rows.map = static_cast<const int32_t*>(ws_.row_map);
+    rows.off = static_cast<const int32_t*>(w.row_off);
+    rows.map = static_cast<const int32_t*>(w.row_map);
     rows.tokens = packed_tokens;
     GD_RETURN_IF_ERROR(launch_pack_rows(rows.len, B, L, packed_tokens, packed_exact,
-                                        static_cast<int32_t*>(ws_.row_off), static_cast<int32_t*>(ws_.row_map),
+                                        static_cast<int32_t*>(w.row_off), static_cast<int32_t*>(w.row_map),
                                         err_flag_, stream));
   }
   if (rows.len) {  // one item schedule for every layer's attention
     const int n = attention_schedule_slots(B, cfg_.num_attention_heads, L);
-    if (n > 0 && n <= ws_sched_cap_) {
+    if (n > 0 && n <= w.sched_cap) {
       GD_RETURN_IF_ERROR(launch_attention_schedule(rows.len, B, cfg_.num_attention_heads, L,
-                                                   static_cast<int32_t*>(ws_.sched), stream));
-      rows.sched = static_cast<const int32_t*>(ws_.sched);
+                                                   static_cast<int32_t*>(w.sched), stream));
+      rows.sched = static_cast<const int32_t*>(w.sched);
       rows.n_sched = n;
     }
   }
@@ -433,26 +506,26 @@ int Classifier::forward(const int32_t* ids, const void* mask, const int32_t* mar
   // attention on the M marker rows (unless GD_FULL_ROWS, or M > the
   // workspace's rows).  The logits are those of the full computation.
   const int N = cfg_.num_hidden_layers;
-  const bool prune = rows.len != nullptr && !(flags_ & GD_FULL_ROWS) && N > 0 && M > 0 && M <= ws_tokens_;
-  GD_RETURN_IF_ERROR(launch_marker_rows(markers, static_cast<int32_t*>(ws_.marker_rows), B, L, Hh * O, err_flag_,
+  const bool prune = rows.len != nullptr && !(flags_ & GD_FULL_ROWS) && N > 0 && M > 0 && M <= w.tokens;
+  GD_RETURN_IF_ERROR(launch_marker_rows(markers, static_cast<int32_t*>(w.marker_rows), B, L, Hh * O, err_flag_,
                                         stream, rows.off));
   if (prune)
     GD_RETURN_IF_ERROR(
-        launch_query_extent(markers, marker_mask, B, L, Hh * O, static_cast<int32_t*>(ws_.q_len), stream));
-  GD_RETURN_IF_ERROR(encode_into_workspace(ids, mask, B, L, prune ? N - 1 : N, stream, hook, rows));
+        launch_query_extent(markers, marker_mask, B, L, Hh * O, static_cast<int32_t*>(w.q_len), stream));
+  GD_RETURN_IF_ERROR(encode_into_workspace(w, ids, mask, B, L, prune ? N - 1 : N, stream, hook, rows));
   if (prune)
     GD_RETURN_IF_ERROR(
-        layer_forward(N - 1, mask, B, L, stream, hook, rows, static_cast<const int32_t*>(ws_.q_len), M));
+        layer_forward(w, N - 1, mask, B, L, stream, hook, rows, static_cast<const int32_t*>(w.q_len), M));
   // classifier (:430-444)
   if (hook) hook->begin(stream);
   if (prune)
-    GD_RETURN_IF_ERROR(launch_linear(ws_.qkv, cls0_w_, cls0_b_, ws_.inner, M, CH, C, C, CH, nullptr, 0,
+    GD_RETURN_IF_ERROR(launch_linear(w.qkv, cls0_w_, cls0_b_, w.inner, M, CH, C, C, CH, nullptr, 0,
                                      GD_EPI_BIAS_RELU, stream));
   else
-    GD_RETURN_IF_ERROR(launch_linear(ws_.hidden, cls0_w_, cls0_b_, ws_.inner, M, CH, C, C, CH,
-                                     static_cast<const int32_t*>(ws_.marker_rows), T > 0 ? T : 1, GD_EPI_BIAS_RELU,
+    GD_RETURN_IF_ERROR(launch_linear(w.hidden, cls0_w_, cls0_b_, w.inner, M, CH, C, C, CH,
+                                     static_cast<const int32_t*>(w.marker_rows), T > 0 ? T : 1, GD_EPI_BIAS_RELU,
                                      stream));
-  GD_RETURN_IF_ERROR(launch_head_output(ws_.inner, cls2_w_, cls2_b_, marker_mask, logits, M, CH, stream));
+  GD_RETURN_IF_ERROR(launch_head_output(w.inner, cls2_w_, cls2_b_, marker_mask, logits, M, CH, stream));
   if (hook) hook->end("classifier", stream);
   return GD_OK;
 }
@@ -462,7 +535,7 @@ int Classifier::classify(const int32_t* ids, const void* mask, const int32_t* ma
                          int64_t packed_tokens) {
   GD_RETURN_IF_ERROR(reserve(B, L, Hh, O));
   if (!(flags_ & GD_USE_COMPILED_GRAPH))
-    return forward(ids, mask, markers, marker_mask, B, L, Hh, O, logits, stream, nullptr, packed_tokens);
+    return forward(ws_, ids, mask, markers, marker_mask, B, L, Hh, O, logits, stream, nullptr, packed_tokens);
 
   // Compiled path (MLX compile, DeBERTa.swift:175-186, 249-261): the forward
   // for one shape is captured once into a hipGraph over the context's staging
@@ -488,7 +561,7 @@ int Classifier::classify(const int32_t* ids, const void* mask, const int32_t* ma
     // work; the instantiated graph is launched on the caller's stream below.
     if (!capture_stream_) GD_HIP_CHECK(hipStreamCreateWithFlags(&capture_stream_, hipStreamNonBlocking));
     GD_HIP_CHECK(hipStreamBeginCapture(capture_stream_, hipStreamCaptureModeThreadLocal));
-    int st = forward(static_cast<const int32_t*>(ws_.ids), ws_.mask, static_cast<const int32_t*>(ws_.markers),
+    int st = forward(ws_, static_cast<const int32_t*>(ws_.ids), ws_.mask, static_cast<const int32_t*>(ws_.markers),
                      static_cast<const float*>(ws_.marker_mask), B, L, Hh, O, ws_.logits, capture_stream_, nullptr,
                      packed_tokens, false);
     hipGraph_t graph = nullptr;
@@ -520,7 +593,7 @@ int Classifier::encode(const int32_t* ids, const void* mask, int64_t B, int64_t 
                        hipStream_t stream) {
   GD_RETURN_IF_ERROR(reserve(B, L, 1, 1));
   const int n = num_layers < 0 ? cfg_.num_hidden_layers : std::min(num_layers, cfg_.num_hidden_layers);
-  GD_RETURN_IF_ERROR(encode_into_workspace(ids, mask, B, L, n, stream, nullptr, Rows{}));
+  GD_RETURN_IF_ERROR(encode_into_workspace(ws_, ids, mask, B, L, n, stream, nullptr, Rows{}));
   GD_HIP_CHECK(hipMemcpyAsync(hidden_out, ws_.hidden, (size_t)B * L * cfg_.hidden_size * 2, hipMemcpyDeviceToDevice,
                               stream));
   return GD_OK;
@@ -532,7 +605,7 @@ int Classifier::layer(int li, const void* hidden_in, const void* mask, int64_t B
   GD_RETURN_IF_ERROR(reserve(B, L, 1, 1));
   const size_t bytes = (size_t)B * L * cfg_.hidden_size * 2;
   GD_HIP_CHECK(hipMemcpyAsync(ws_.hidden, hidden_in, bytes, hipMemcpyDeviceToDevice, stream));
-  GD_RETURN_IF_ERROR(layer_forward(li, mask, B, L, stream, nullptr, Rows{}));
+  GD_RETURN_IF_ERROR(layer_forward(ws_, li, mask, B, L, stream, nullptr, Rows{}));
   GD_HIP_CHECK(hipMemcpyAsync(hidden_out, ws_.hidden, bytes, hipMemcpyDeviceToDevice, stream));
   return GD_OK;
 }
@@ -575,7 +648,7 @@ int Classifier::classify_profiled(const int32_t* ids, const void* mask, const in
                                   gd_profile_event* events, int capacity, int* count, hipStream_t stream) {
   GD_RETURN_IF_ERROR(reserve(B, L, Hh, O));
   EventHook hook;
-  GD_RETURN_IF_ERROR(forward(ids, mask, markers, marker_mask, B, L, Hh, O, logits, stream, &hook));
+  GD_RETURN_IF_ERROR(forward(ws_, ids, mask, markers, marker_mask, B, L, Hh, O, logits, stream, &hook));
   if (hook.status != GD_OK) return fail(GD_ERR_HIP, "event record failed");
   GD_HIP_CHECK(hipStreamSynchronize(stream));
   int n = 0;

@@ -35,6 +35,11 @@ class Classifier {
   // extents, which it must equal); -1: every row is B x L tokens.
   int classify(const int32_t* ids, const void* mask, const int32_t* markers, const float* marker_mask, int64_t B,
                int64_t L, int64_t Hh, int64_t O, void* logits, hipStream_t stream, int64_t packed_tokens = -1);
+  // classify with the workspace in the library's static device array (no
+  // allocation, no graph); GD_ERR_SHAPE when the call's buffers exceed it.
+  int classify_static(const int32_t* ids, const void* mask, const int32_t* markers, const float* marker_mask,
+                      int64_t B, int64_t L, int64_t Hh, int64_t O, void* logits, hipStream_t stream,
+                      int64_t packed_tokens);
   int classify_profiled(const int32_t* ids, const void* mask, const int32_t* markers, const float* marker_mask,
                         int64_t B, int64_t L, int64_t Hh, int64_t O, void* logits, gd_profile_event* events,
                         int capacity, int* count, hipStream_t stream);
@@ -62,6 +67,7 @@ class Classifier {
     void* sched = nullptr;    // int32 [sched_cap]: attention item schedule under row extents
     void* q_len = nullptr;    // int32 [B]: last marker position + 1 per batch row (classify's last layer)
     void *ids = nullptr, *mask = nullptr, *markers = nullptr, *marker_mask = nullptr, *logits = nullptr;
+    int64_t tokens = 0, markers_cap = 0, sched_cap = 0;  // capacities: T, B*Hh*O, schedule slots
   };
   using ShapeKey = std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t>;  // B, L, Hh, O, packed tokens
   struct GraphEntry {
@@ -88,15 +94,17 @@ class Classifier {
   // leave the layer, compact (row i = marker slot i) in ws_.qkv; attention
   // queries stop at q_len[b] (the classifier reads nothing else of the last
   // layer).
-  int layer_forward(int li, const void* mask, int64_t B, int64_t L, hipStream_t stream, StageHook* hook,
+  int layer_forward(const Workspace& w, int li, const void* mask, int64_t B, int64_t L, hipStream_t stream, StageHook* hook,
                     const Rows& rows, const int32_t* q_len = nullptr, int64_t marker_count = -1);
-  int encode_into_workspace(const int32_t* ids, const void* mask, int64_t B, int64_t L, int num_layers,
+  int encode_into_workspace(const Workspace& w, const int32_t* ids, const void* mask, int64_t B, int64_t L, int num_layers,
                             hipStream_t stream, StageHook* hook, const Rows& rows);
   // packed_exact = false: packed_tokens is a capacity >= the extents' sum.
-  int forward(const int32_t* ids, const void* mask, const int32_t* markers, const float* marker_mask, int64_t B,
+  int forward(const Workspace& w, const int32_t* ids, const void* mask, const int32_t* markers, const float* marker_mask, int64_t B,
               int64_t L, int64_t Hh, int64_t O, void* logits, hipStream_t stream, StageHook* hook,
               int64_t packed_tokens = -1, bool packed_exact = true);
   void release_graphs();
+  int init_static_workspace();
+  int64_t carve_workspace(Workspace& w, uint8_t* base, int64_t T, int64_t M, int64_t B, int64_t sched_slots) const;
 
   gd_config cfg_{};
   uint32_t flags_ = 0;
@@ -110,7 +118,7 @@ class Classifier {
   void *cls0_w_ = nullptr, *cls0_b_ = nullptr, *cls2_w_ = nullptr, *cls2_b_ = nullptr;
   int32_t* err_flag_ = nullptr;
   Workspace ws_;
-  int64_t ws_tokens_ = 0, ws_markers_ = 0, ws_sched_cap_ = 0;
+  void* static_ws_base_ = nullptr;  // this device's address of the static workspace
   std::map<ShapeKey, GraphEntry> graphs_;
   hipStream_t capture_stream_ = nullptr;  // default priority, non-blocking
 };

@@ -120,6 +120,7 @@ _SIGNATURES = {
     "gd_classifier_reserve": (C.c_int, [vp, i64, i64, i64, i64]),
     "gd_classifier_classify": (C.c_int, [vp, vp, vp, vp, vp, i64, i64, i64, i64, vp, vp]),
     "gd_classifier_classify_packed": (C.c_int, [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, vp, vp]),
+    "gd_classifier_classify_static": (C.c_int, [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, vp, vp]),
     "gd_classifier_encode": (C.c_int, [vp, vp, vp, i64, i64, i32, vp, vp]),
     "gd_classifier_layer_forward": (C.c_int, [vp, i32, vp, vp, i64, i64, vp, vp]),
     "gd_classifier_classify_profiled": (C.c_int, [vp, vp, vp, vp, vp, i64, i64, i64, i64, vp,

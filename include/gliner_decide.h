@@ -334,6 +334,26 @@ int gd_classifier_classify_packed(gd_classifier* model, const int32_t* input_ids
                                   int64_t seq_len, int64_t max_heads, int64_t max_options, int64_t total_tokens,
                                   void* logits_out, void* stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory at call time (code under hipGraph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): classify with the activation workspace in
+ * the library's static device array instead of the context's workspace.  It
+ * calls no hipMalloc / hipFree and captures no graph.  total_tokens = -1 runs
+ * every row at B x L tokens (as gd_classifier_classify); total_tokens >= 0
+ * runs packed rows (as gd_classifier_classify_packed, same rule for the
+ * total).  The logits equal those of those entry points.
+ * Limit: the call's buffers must fit the 48 MiB array -- at hidden 1024 /
+ * intermediate 4096 / classifier 2048 that is up to 2048 tokens (B*L, or the
+ * packed total) with up to 1024 marker slots (B*Hh*O); larger calls return
+ * GD_ERR_SHAPE.  The array (one per GPU, held from the library's first use on
+ * that GPU until the process ends) is shared by every context on that GPU
+ * and keeps the last call's contents: calls that overlap on one GPU (two
+ * streams, threads or contexts) race. */
+int gd_classifier_classify_static(gd_classifier* model, const int32_t* input_ids, const void* attention_mask,
+                                  const int32_t* marker_indices, const float* marker_mask, int64_t batch,
+                                  int64_t seq_len, int64_t max_heads, int64_t max_options, int64_t total_tokens,
+                                  void* logits_out, void* stream);
+
 /* Encoder only: writes the final hidden states [B, L, hidden] fp16 after
  * `num_layers` layers (num_layers < 0 = all). */
 int gd_classifier_encode(gd_classifier* model, const int32_t* input_ids, const void* attention_mask,
