@@ -5,8 +5,11 @@ random-init fp16 weights of the real architecture).
 One step = one `classify` of a 32-row batch (embedding, 24 layers, classifier)
 with inputs resident in HBM.  Prints ONE JSON line on stdout (logs on stderr):
 rows/s over exactly --steps timed steps, the roofline of the dominant kernel
-(measured live with HIP events on the launch stream) and a CPU baseline (the
-numpy port of the reference graph on a bounded sample, this host's cores).
+(measured live with HIP events on the launch stream, first thing in the
+process: the same launch sequence as `--profile-kernel`, whose rocprofv3
+summary is committed under profiles/), a CPU baseline (the batched torch fp32
+restatement of the reference graph on this host's cores), the single layer at
+B=1 L=32 and the long-context batch (B=64, L=512).
 
 Kernel timings use rotating buffer sets larger than the 256 MB Infinity Cache
 so that HBM, not the cache, serves the reads.
@@ -27,6 +30,7 @@ for _p in (str(ROOT), str(ROOT / "gliner-decide-metal_amd")):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
+ROOFLINE_KERNEL = "ffn_up_gelu"  # the kernel with the largest share of the step (profiles/e2e_classify_b32_l256.md)
 FP16_DENSE_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
 ROTATE_BYTES = 600 << 20  # > 2x the 256 MB MALL
 
@@ -44,7 +48,7 @@ def parse():
     p.add_argument("--compiled", action="store_true", help="replay a captured hipGraph per step")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-bucket-mix", action="store_true", help="skip the mixed-length throughput field")
-    p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
+    p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--kernel-iters", type=int, default=60)
     p.add_argument("--profile-kernel", default=None,
                    choices=["residual_layernorm", "relbias_softmax", "relative_bias", "attention_context", "qkv_proj",
@@ -306,18 +310,17 @@ def calibration_copy(nbytes=256 << 20):
     return nbytes
 
 
-def roofline_of(kernels):
-    """The kernel with the largest time share of one forward step."""
-    best = max((v for v in kernels.values() if v["launches_per_step"] > 0),
-               key=lambda v: v["us"] * v["launches_per_step"])
+def roofline_of(name, best, iters):
+    """Roofline object of kernel `name` from its live measurement `best`."""
     if best["bound"] == "hbm":
         ach, peak, unit = best["gbs"], HBM_PEAK_GBS, "GB/s"
     else:
         ach, peak, unit = best["tflops"], FP16_DENSE_TFLOPS, "TFLOP/s"
-    name = [k for k, v in kernels.items() if v is best][0]
     traffic, source = profiled_traffic(name)
     return dict(kernel=name, bound=best["bound"], achieved=round(ach, 2), peak=peak, unit=unit,
                 frac=round(ach / peak, 4), traffic=traffic, traffic_source=source, avg_us=round(best["us"], 2),
+                launches=iters, measured="first in the process, the launch sequence of "
+                                        f"`bench.py --profile-kernel {name} --kernel-iters {iters}`",
                 algorithmic_per_launch=best["bytes"] if best["bound"] == "hbm" else best["flops"])
 
 
@@ -335,31 +338,94 @@ def profiled_traffic(kernel):
 
 
 # ---------------------------------------------------------------------------
-# CPU baseline: the numpy port of the reference graph (oracle), fp32
+# CPU baseline: the batched torch fp32 restatement of the reference graph
 # ---------------------------------------------------------------------------
-def cpu_baseline(weights, cfg, batch, budget_s):
+def cpu_baseline(weights, cfg, batch, budget_s, gpu_logits=None):
+    """Whole B=32 L=256 batches through oracle/torch_cpu.py (the default
+    reference graph in fp32, every row at the full bucket length) on this
+    host's cores (OMP_NUM_THREADS, else all), until `budget_s` is spent (at
+    least one batch), after a 2-row warm-up."""
     import numpy as np
+    import torch
     from oracle import deberta as O
-    try:
-        from threadpoolctl import threadpool_info
-        cores = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
-    except Exception:
-        cores = os.cpu_count() or 1
+    from oracle.torch_cpu import TorchCPUModel, cpu_description
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    torch.set_num_threads(threads)
     oc = O.Config(**{k: getattr(cfg, k) for k in O.Config.__dataclass_fields__})
-    w32 = {k: v.astype(np.float32) for k, v in weights.items()}
-    om = O.OracleModel(O.ModelWeights.from_store(w32, oc), oc, round16=False, dtype=np.float32)
+    m = TorchCPUModel(weights, oc)
     a = batch.arrays()
+    args = [a["input_ids"], a["attention_mask"], a["marker_indices"], a["marker_mask"]]
+    m.forward(*[x[:2] for x in args])
+    B = a["input_ids"].shape[0]
     done, t0 = 0, time.perf_counter()
-    while done < a["input_ids"].shape[0]:
-        s = slice(done, done + 1)
-        om.forward(a["input_ids"][s], a["attention_mask"][s], a["marker_indices"][s], a["marker_mask"][s])
+    while True:
+        logits = m.forward(*args)
         done += 1
-        if time.perf_counter() - t0 > budget_s:
+        if time.perf_counter() - t0 >= budget_s:
             break
     el = time.perf_counter() - t0
-    return dict(value=round(done / el, 3), unit="rows/s", cores=int(cores), kind="port",
-                sample=f"{done} row(s) of the B=32 L=256 batch through the numpy fp32 port of the reference graph "
-                       f"(24 layers + classifier), {el:.1f} s")
+    out = dict(value=round(B * done / el, 3), unit="rows/s", cores=torch.get_num_threads(), kind="port",
+               cpu=cpu_description(), backend=f"torch {torch.__version__} CPU, fp32",
+               sample=f"{done} whole batch(es) of B={B} L={a['input_ids'].shape[1]} through the batched torch fp32 "
+                      f"restatement of the reference graph (24 layers + classifier, every row at full length), "
+                      f"{el:.1f} s")
+    if gpu_logits is not None:  # the fp16 GPU chain against the fp32 CPU graph
+        out["max_abs_logit_diff_vs_gpu"] = round(float(np.max(np.abs(logits.numpy() - gpu_logits))), 5)
+    return out
+
+
+def single_layer_us(model, iters=200):
+    """One encoder layer at B=1, L=32 (hidden N(0,1), all-ones mask) through
+    gd_classifier_layer_forward, HIP events around `iters` back-to-back calls
+    on the launch stream.  Its bound: the layer's 25.2 MB of weights read
+    once at 8 TB/s."""
+    import torch
+    from gliner_decide.synthetic import layer_inputs
+    d = layer_inputs(seed=1)
+    h = torch.from_numpy(d["hidden"]).cuda()
+    mask = torch.from_numpy(d["mask"]).cuda()
+    for _ in range(10):
+        model.layer_forward(0, h, mask)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(iters):
+        model.layer_forward(0, h, mask)
+    end.record()
+    end.synchronize()
+    us = start.elapsed_time(end) * 1000.0 / iters
+    C, F = 1024, 4096
+    wbytes = (4 * C * C + 2 * C * F) * 2 + (6 * C + F + 4 * C) * 2
+    return dict(us=round(us, 2), weight_bytes=wbytes, bound_us=round(wbytes / HBM_PEAK_GBS / 1e3, 2),
+                frac_of_bound=round(wbytes / HBM_PEAK_GBS / 1e3 / us, 4), iters=iters,
+                sample="gd_classifier_layer_forward, B=1 L=32, layer 0 of the 24-layer model")
+
+
+def long_context_rate(model, steps=5, warmup=2):
+    """Rows/s at B=64, L=512 (every row full, 3 heads of 20/20/8 labels),
+    packed classify with inputs in HBM."""
+    import torch
+    from gliner_decide import DecisionInput
+    from gliner_decide.decode import row_extents
+    from gliner_decide.synthetic import long_context_batch
+    batch = long_context_batch(seed=6)
+    a = batch.arrays()
+    ids, mask, mk, mm = DecisionInput(**a).to_device()
+    B, L = ids.shape
+    model.reserve(B, L, mk.shape[1], mk.shape[2])
+    out = torch.empty((B, mk.shape[1], mk.shape[2]), dtype=torch.float16, device=ids.device)
+    total = int(row_extents(a["attention_mask"], a["marker_indices"], a["marker_mask"]).sum())
+    for _ in range(warmup):
+        model.classify_device(ids, mask, mk, mm, out, total_tokens=total)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        model.classify_device(ids, mask, mk, mm, out, total_tokens=total)
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    assert torch.isfinite(out.float()).all()
+    return dict(value=round(B * steps / el, 1), unit="rows/s", ms_per_step=round(el * 1000 / steps, 3), steps=steps,
+                sample="B=64 L=512 full rows, 3 heads (20/20/8 labels), packed classify")
 
 
 def main():
@@ -377,6 +443,11 @@ def main():
 
     torch.cuda.set_device(0)
     cfg = DeBERTaV2Configuration(vocab_size=128100)
+    if not args.profile_kernel and not args.serving:
+        # the roofline kernel first: the launch sequence of --profile-kernel in
+        # the same process state (nothing has run on the GPU yet)
+        roof_k = measure_kernels(cfg, args.kernel_iters, only=ROOFLINE_KERNEL)[ROOFLINE_KERNEL]
+        log(f"{ROOFLINE_KERNEL}: {roof_k['us']:.2f} us per launch over {args.kernel_iters} launches")
     if args.profile_kernel:
         kernels = measure_kernels(cfg, args.kernel_iters, only=args.profile_kernel)
         nb = calibration_copy()
@@ -459,7 +530,11 @@ def main():
     for k, v in kernels.items():
         extra = f"{v['gbs']:.0f} GB/s" if "gbs" in v and v["bound"] == "hbm" else f"{v.get('tflops', 0):.0f} TFLOP/s"
         log(f"  {k:20s} {v['us']:9.2f} us  {extra}")
-    roof = roofline_of(kernels)
+    roof = roofline_of(ROOFLINE_KERNEL, roof_k, args.kernel_iters)
+    layer1 = single_layer_us(model)
+    log(f"single layer B=1 L=32: {layer1}")
+    longctx = long_context_rate(model) if args.workload == "classify" else None
+    log(f"long context B=64 L=512: {longctx}")
 
     # after the kernel table: seconds of sustained load change the clocks the
     # short kernels above would be timed at
@@ -470,7 +545,7 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline and args.workload == "classify":
-        cpu = cpu_baseline(weights, cfg, batch, args.cpu_seconds)
+        cpu = cpu_baseline(weights, cfg, batch, args.cpu_seconds, packed_logits.float().cpu().numpy())
         log(f"cpu baseline: {cpu}")
 
     line = {
@@ -501,6 +576,8 @@ def main():
         "full_rows_s": round(B * args.steps / full_s, 2),
         "relative_bias_gbs": round(kernels["relative_bias"]["gbs"], 1),
         "relative_bias_frac_hbm": round(kernels["relative_bias"]["gbs"] / HBM_PEAK_GBS, 4),
+        "single_layer_b1_l32": layer1,
+        "long_context_b64_l512_rows_s": longctx,
     }
     print(json.dumps(line), flush=True)
 

@@ -53,11 +53,6 @@ __device__ __forceinline__ int dma_chunk(int lane, int blk) {
   return (lane & 7) ^ (((blk & 1) << 2) | (lane >> 4));
 }
 
-// GELU(y) = 0.5 y (1 + erf(y / sqrt 2)), evaluated through erfc so neither tail
-// cancels: with z = |y| / sqrt 2, GELU = y - 0.5 y erfc(z) for y >= 0 and
-// 0.5 y erfc(z) for y < 0.  erfc is the Chebyshev fit of Numerical Recipes in
-// C (2nd ed., section 6.2, "erfcc"): t = 1 / (1 + z / 2),
-// erfc(z) = t exp(-z^2 + P(t)), fractional error below 1.2e-7 for all z >= 0.
 // ---------------------------------------------------------------------------
 // GELU by table.  The GELU epilogue's input is the fp16 addMM output, so its
 // correctly rounded fp16 GELU can be looked up: one entry per fp16 value with

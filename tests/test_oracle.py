@@ -440,3 +440,28 @@ def test_planted_mistakes_are_caught(golden, monkeypatch):
     monkeypatch.setattr(O, "relative_bias_default", no_p2c)
     bad = m.encode(g["ids"], g["mask"])
     assert np.max(np.abs(bad - g["out"])) > 1e-3
+
+
+def test_torch_cpu_baseline_matches_oracle():
+    """The CPU baseline (oracle/torch_cpu.py, batched torch fp32) computes the
+    same graph as the numpy oracle evaluated exactly: logits within fp32
+    noise, padded rows and the log-bucket zone (L = 160) included."""
+    import sys
+    from pathlib import Path
+    sys.path.insert(0, str(Path(__file__).resolve().parents[1] / "gliner-decide-metal_amd"))
+    from gliner_decide.config import DeBERTaV2Configuration
+    from gliner_decide.synthetic import synthetic_weights
+    from oracle.torch_cpu import TorchCPUModel
+    pc = DeBERTaV2Configuration(hidden_size=128, intermediate_size=256, num_hidden_layers=2, num_attention_heads=2,
+                                vocab_size=512, classifier_hidden=256)
+    w = synthetic_weights(pc, seed=17)
+    oc = O.Config(**{k: getattr(pc, k) for k in O.Config.__dataclass_fields__})
+    r = np.random.default_rng(4)
+    B, L = 3, 160
+    ids = r.integers(10, 512, size=(B, L))
+    mask = (np.arange(L)[None] < np.array([[160], [97], [20]])).astype(np.float16)
+    mi = r.integers(0, 20, size=(B, 2, 4))
+    mm = (r.random((B, 2, 4)) < 0.7).astype(np.float32)
+    want = O.OracleModel(O.ModelWeights.from_store(w, oc), oc, round16=False).forward(ids, mask, mi, mm)
+    got = TorchCPUModel(w, oc).forward(ids, mask, mi, mm).numpy()
+    np.testing.assert_allclose(got, want, atol=1e-4, rtol=1e-4)
