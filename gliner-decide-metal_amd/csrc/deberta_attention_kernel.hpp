@@ -48,9 +48,6 @@
 
 namespace gd {
 
-// Compute units of the current device (cached per device).
-int device_cu_count();
-
 namespace {
 
 constexpr int kThreads = 512;

@@ -8,6 +8,9 @@
 
 namespace gd {
 
+// Compute units of the current device (cached per device).
+int device_cu_count();
+
 int launch_residual_layer_norm(const void* x, const void* residual, const void* gamma, const void* beta, void* out,
                                int64_t rows, int64_t cols, float eps, uint32_t flags, hipStream_t stream);
 

@@ -6,9 +6,11 @@
 //
 // gfx950 design: one wave64 per row.  For the model width (1024) each lane
 // owns 16 elements loaded as two 16-byte vectors per tensor, so a row is read
-// exactly once, held in registers, reduced with wave64 butterflies (mean, then
-// the centred second moment) and written once: 3 x 2 KiB of HBM traffic per
-// row for residual LN, the algorithmic minimum.
+// exactly once, held in registers, reduced across the wave with DPP moves
+// (mean, then the centred second moment; no LDS round trips) and written
+// once: 3 x 2 KiB of HBM traffic per row for residual LN, the algorithmic
+// minimum.  gamma and beta are loaded before the row so their latency does
+// not sit between the reductions and the stores.
 
 #include "gd_common.hpp"
 #include "gd_kernels.hpp"
@@ -55,12 +57,27 @@ __device__ __forceinline__ float load_row_sum(const half_t* x, const half_t* res
   return sum;
 }
 
+// gamma / beta of this lane's elements, loaded once before the row data so
+// their latency is off the path between the reductions and the stores.
 template <int VPL>
-__device__ __forceinline__ void normalize_store(RowVec<VPL>& r, float sum, const half_t* __restrict__ gamma,
-                                                const half_t* __restrict__ beta, half_t* out,
+struct Affine {
+  half8_t g[VPL], b[VPL];
+  __device__ __forceinline__ void load(const half_t* __restrict__ gamma, const half_t* __restrict__ beta, int lane) {
+    const half8_t* g8 = reinterpret_cast<const half8_t*>(gamma);
+    const half8_t* b8 = reinterpret_cast<const half8_t*>(beta);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      g[j] = g8[j * 64 + lane];
+      b[j] = b8[j * 64 + lane];
+    }
+  }
+};
+
+template <int VPL>
+__device__ __forceinline__ void normalize_store(RowVec<VPL>& r, float sum, const Affine<VPL>& aff, half_t* out,
                                                 int64_t row, int lane, float eps, float scale_mask) {
   constexpr int C = 64 * 8 * VPL;
-  const float mean = wave_sum(sum) * (1.0f / C);
+  const float mean = wave_sum_dpp(sum) * (1.0f / C);
   float sq = 0.f;
 #pragma unroll
   for (int j = 0; j < VPL; ++j)
@@ -69,15 +86,13 @@ __device__ __forceinline__ void normalize_store(RowVec<VPL>& r, float sum, const
       const float d = r.v[j][e] - mean;
       sq += d * d;
     }
-  const float var = wave_sum(sq) * (1.0f / C);
+  const float var = wave_sum_dpp(sq) * (1.0f / C);
   const float inv = 1.0f / sqrtf(var + eps);
-  const half8_t* g8 = reinterpret_cast<const half8_t*>(gamma);
-  const half8_t* b8 = reinterpret_cast<const half8_t*>(beta);
   half8_t* o8 = reinterpret_cast<half8_t*>(out + row * C);
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
-    const half8_t g = g8[j * 64 + lane];
-    const half8_t bb = b8[j * 64 + lane];
+    const half8_t g = aff.g[j];
+    const half8_t bb = aff.b[j];
     half8_t o;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -100,6 +115,8 @@ __global__ __launch_bounds__(256) void residual_ln_kernel(const half_t* x, const
                                                           int64_t rows, float eps, int round_sum) {
   const int lane = threadIdx.x & 63;
   const int64_t row0 = ((int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6)) * RPW;
+  Affine<VPL> aff;
+  aff.load(gamma, beta, lane);
   RowVec<VPL> r[RPW];
   float sum[RPW];
 #pragma unroll
@@ -107,7 +124,7 @@ __global__ __launch_bounds__(256) void residual_ln_kernel(const half_t* x, const
     if (row0 + i < rows) sum[i] = load_row_sum<VPL>(x, res, row0 + i, lane, round_sum != 0, r[i]);
 #pragma unroll
   for (int i = 0; i < RPW; ++i)
-    if (row0 + i < rows) normalize_store<VPL>(r[i], sum[i], gamma, beta, out, row0 + i, lane, eps, 1.0f);
+    if (row0 + i < rows) normalize_store<VPL>(r[i], sum[i], aff, out, row0 + i, lane, eps, 1.0f);
 }
 
 // Any width that is a multiple of 8: three passes like the reference kernel
@@ -183,11 +200,13 @@ __global__ __launch_bounds__(256) void embedding_ln_kernel(const int32_t* __rest
     if (error_flag && lane == 0) atomicOr(error_flag, 1);
     id = 0;
   }
+  Affine<VPL> aff;
+  aff.load(gamma, beta, lane);
   RowVec<VPL> r;
   const float sum = load_row_sum<VPL>(table, nullptr, id, lane, false, r);
   const float m = (float)mask[src];
   // out = fp16(fp16(LN) * fp16(mask)); for the usual 0/1 mask this is LN or 0.
-  normalize_store<VPL>(r, sum, gamma, beta, out, t, lane, eps, m);
+  normalize_store<VPL>(r, sum, aff, out, t, lane, eps, m);
 }
 
 __global__ __launch_bounds__(256) void embedding_ln_generic_kernel(const int32_t* __restrict__ ids,
