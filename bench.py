@@ -51,7 +51,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--kernel-iters", type=int, default=60)
     p.add_argument("--profile-kernel", default=None,
-                   choices=["residual_layernorm", "relbias_softmax", "relative_bias", "attention_context", "qkv_proj",
+                   choices=["residual_layernorm", "stream_ceiling", "relbias_softmax", "relative_bias", "attention_context", "qkv_proj",
                             "out_proj", "ffn_up_gelu", "ffn_down"],
                    help="only run this kernel (--kernel-iters launches on rotating buffers) followed by a 256 MiB "
                         "torch copy, for rocprofv3 counter runs; prints the kernel table, no JSON line")
@@ -135,6 +135,25 @@ def measure_kernels(model_cfg, iters, only=None):
         us = time_launches(ln, sets, iters)
         out["residual_layernorm"] = dict(kernel="residual_ln_kernel<2>", shape=[rows, cols], us=us, bytes=nbytes,
                                          gbs=nbytes / us / 1e3, bound="hbm", launches_per_step=48)
+        del sets
+
+    # the same bytes with no arithmetic: two 16-byte non-temporal reads and one
+    # write per piece (gd_stream_probe_add), the streaming ceiling of the LN's
+    # access pattern on this device
+    if want("stream_ceiling"):
+        rows, cols = 8192, 1024
+        nsets = max(2, ROTATE_BYTES // (3 * rows * cols * 2) + 1)
+        sets = [(torch.randn(rows, cols, device=dev).half(), torch.randn(rows, cols, device=dev).half(),
+                 torch.empty((rows, cols), device=dev, dtype=torch.float16)) for _ in range(nsets)]
+
+        def probe(s):
+            N.check(lib.gd_stream_probe_add(s[0].data_ptr(), s[1].data_ptr(), s[2].data_ptr(), rows * cols,
+                                            stream_handle()))
+
+        us = time_launches(probe, sets, iters)
+        nbytes = 3 * rows * cols * 2
+        out["stream_ceiling"] = dict(kernel="stream_probe_kernel", shape=[rows, cols], us=us, bytes=nbytes,
+                                     gbs=nbytes / us / 1e3, bound="hbm", launches_per_step=0)
         del sets
 
     # relative bias + masked softmax, B=32 H=16 L=256 D=64 -> P [32,16,256,256]
@@ -569,6 +588,9 @@ def main():
                     for k, v in kernels.items()},
         "fused_ln_gbs": round(kernels["residual_layernorm"]["gbs"], 1),
         "fused_ln_frac_hbm": round(kernels["residual_layernorm"]["gbs"] / HBM_PEAK_GBS, 4),
+        "stream_ceiling_gbs": round(kernels["stream_ceiling"]["gbs"], 1),
+        "fused_ln_frac_of_stream_ceiling": round(kernels["residual_layernorm"]["gbs"] / kernels["stream_ceiling"]["gbs"],
+                                                 4),
         "relbias_softmax_gbs": round(kernels["relbias_softmax"]["gbs"], 1),
         "relbias_softmax_frac_hbm": round(kernels["relbias_softmax"]["gbs"] / HBM_PEAK_GBS, 4),
         "bucket_mix_rows_s": mix,

@@ -10,6 +10,7 @@
 #include "gd_kernels.hpp"
 #include "model.hpp"
 #include "weights.hpp"
+#include "gliner_decide_diag.h"
 
 struct gd_weight_store {
   gd::WeightStore impl;
@@ -250,6 +251,14 @@ int gd_deberta_attention(gd_bhld q, gd_bhld k, gd_bhld v, gd_table pos_key, gd_t
   const float scale_rel = head_dim > 0 ? 1.0f / std::sqrt((float)(3 * head_dim)) : 0.f;
   return deberta_attention_checked(q, k, v, pos_key, pos_query, mask, mask_kind, batch, heads, seq_len, head_dim,
                                    positions, bucket_size, kind, score, scale_rel, out, ldo, as_stream(stream));
+}
+
+int gd_stream_probe_add(const void* a, const void* b, void* c, int64_t n, void* stream) {
+  clear_error();
+  GD_CHECK_ARG(n == 0 || (a && b && c), "null tensor pointer");
+  GD_CHECK_SHAPE(n >= 0 && n % 32 == 0, "n must be a non-negative multiple of 32");
+  GD_CHECK_ARG(aligned(a, 16) && aligned(b, 16) && aligned(c, 16), "pointers must be 16-byte aligned");
+  return launch_stream_probe_add(a, b, c, n, as_stream(stream));
 }
 
 int gd_relative_index_table(int32_t* out, int32_t n, int32_t bucket_size, int32_t max_position, void* stream) {

@@ -11,6 +11,9 @@ namespace gd {
 // Compute units of the current device (cached per device).
 int device_cu_count();
 
+// Streaming reference kernel (gd_stream_probe_add): c = a + b, n fp16.
+int launch_stream_probe_add(const void* a, const void* b, void* c, int64_t n, hipStream_t stream);
+
 int launch_residual_layer_norm(const void* x, const void* residual, const void* gamma, const void* beta, void* out,
                                int64_t rows, int64_t cols, float eps, uint32_t flags, hipStream_t stream);
 

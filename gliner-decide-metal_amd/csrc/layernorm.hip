@@ -248,7 +248,39 @@ __global__ __launch_bounds__(256) void embedding_ln_generic_kernel(const int32_t
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Streaming reference of the LayerNorm's traffic (gd_stream_probe_add): each
+// lane reads four 16-byte pieces of a and of b and writes four of c, all
+// non-temporal; a block of 256 lanes covers 1024 consecutive pieces.
+__global__ __launch_bounds__(256) void stream_probe_kernel(const half8_t* __restrict__ a,
+                                                           const half8_t* __restrict__ b, half8_t* __restrict__ c,
+                                                           int64_t n8) {
+  const int64_t base = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+  half8_t x[4], y[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int64_t i = base + v * 256;
+    if (i < n8) {
+      x[v] = __builtin_nontemporal_load(a + i);
+      y[v] = __builtin_nontemporal_load(b + i);
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int64_t i = base + v * 256;
+    if (i < n8) __builtin_nontemporal_store(x[v] + y[v], c + i);
+  }
+}
+
 }  // namespace
+
+int launch_stream_probe_add(const void* a, const void* b, void* c, int64_t n, hipStream_t stream) {
+  if (n == 0) return GD_OK;
+  const int64_t n8 = n / 8;
+  hipLaunchKernelGGL(stream_probe_kernel, dim3((unsigned)((n8 + 1023) / 1024)), dim3(256), 0, stream,
+                     static_cast<const half8_t*>(a), static_cast<const half8_t*>(b), static_cast<half8_t*>(c), n8);
+  GD_LAUNCH_CHECK();
+  return GD_OK;
+}
 
 int launch_residual_layer_norm(const void* x, const void* residual, const void* gamma, const void* beta, void* out,
                                int64_t rows, int64_t cols, float eps, uint32_t flags, hipStream_t stream) {

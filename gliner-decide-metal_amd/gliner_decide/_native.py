@@ -108,6 +108,7 @@ _SIGNATURES = {
     "gd_deberta_attention": (C.c_int, [GdBhld, GdBhld, GdBhld, GdTable, GdTable, vp, i32, i64, i64, i64, i64, i64,
                                        i32, i32, vp, i64, vp]),
     "gd_relative_index_table": (C.c_int, [vp, i32, i32, i32, vp]),
+    "gd_stream_probe_add": (C.c_int, [vp, vp, vp, i64, vp]),
     "gd_weight_store_create": (C.c_int, [C.POINTER(vp)]),
     "gd_weight_store_destroy": (None, [vp]),
     "gd_weight_store_add": (C.c_int, [vp, C.c_char_p, vp, i32, C.POINTER(i64), i32]),

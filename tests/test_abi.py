@@ -12,11 +12,11 @@ import pytest
 
 from gliner_decide import _native as N
 
-HEADER = Path(__file__).resolve().parents[1] / "include" / "gliner_decide.h"
+HEADERS = [Path(__file__).resolve().parents[1] / "include" / h for h in ("gliner_decide.h", "gliner_decide_diag.h")]
 
 
 def declared_functions():
-    text = HEADER.read_text()
+    text = "\n".join(h.read_text() for h in HEADERS)
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"^\s*(?:const\s+)?(?:int|void|char\s*\*|int64_t|char)\s*\**\s*(gd_\w+)\s*\(",
                                  text, flags=re.M)))

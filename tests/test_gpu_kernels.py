@@ -542,3 +542,17 @@ def test_attention_rejects_bias_output_on_chains_without_a_bias():
     for score in ("explicit", "kernel_bias_explicit", "fused"):
         with pytest.raises(GlinerDecideError):
             fk().deberta_attention(dev(q), dev(k), dev(v), gpk, gpq, dev(mask), output="bias", score=score)
+
+
+def test_stream_probe_adds():
+    """The streaming-ceiling diagnostic computes what it claims (c = a + b,
+    fp16), including a tail shorter than one block."""
+    from gliner_decide import _native as N
+    from gliner_decide.device import stream_handle
+    for n in (8192 * 1024, 32 * 37):
+        a = torch.randn(n, device="cuda").half()
+        b = torch.randn(n, device="cuda").half()
+        c = torch.empty_like(a)
+        N.check(N.lib().gd_stream_probe_add(a.data_ptr(), b.data_ptr(), c.data_ptr(), n, stream_handle()))
+        torch.cuda.synchronize()
+        assert torch.equal(c, a + b)
