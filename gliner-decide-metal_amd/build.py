@@ -121,7 +121,87 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
         raise RuntimeError("link failed:\n" + p.stdout + p.stderr)
     os.replace(tmp, LIB_PATH)
     build_frontend(verbose)
+    build_sanitized(verbose)
     return LIB_PATH
+
+
+# ---------------------------------------------------------------------------
+# Host sanitizer build: the host C++ that parses untrusted input (the
+# safetensors reader and the C-ABI around it; the tokenizer.json / charsmap /
+# schema front end) with AddressSanitizer and UndefinedBehaviorSanitizer, into
+# lib/sanitize/.  Device code is built exactly as in build(): each sanitizer
+# flag on a hipcc line is host-only (-Xarch_host).  tests/test_sanitized_host.py
+# runs the CPU tests of these paths against this build.
+# ---------------------------------------------------------------------------
+SAN_DIR = LIB_DIR / "sanitize"
+SAN_HOST_SOURCES = ("weights.cpp", "capi.cpp", "model.cpp")
+SAN_HOST_FLAGS = [
+    "-Xarch_host", "-fsanitize=address",
+    "-Xarch_host", "-fsanitize=undefined",
+    "-Xarch_host", "-fno-omit-frame-pointer",
+]
+SAN_CXX_FLAGS = [
+    "-fsanitize=address,undefined",
+    "-fno-omit-frame-pointer",
+    "-shared-libsan",
+]
+
+
+def llvm_dir() -> Path:
+    return Path(hipcc()).resolve().parent.parent / "lib" / "llvm"
+
+
+def asan_runtime() -> Path:
+    """The clang AddressSanitizer runtime both sanitized libraries link (to
+    LD_PRELOAD into an unsanitized interpreter)."""
+    found = sorted(llvm_dir().glob("lib/clang/*/lib/linux/libclang_rt.asan-x86_64.so"))
+    if not found:
+        raise RuntimeError("clang AddressSanitizer runtime not found")
+    return found[-1]
+
+
+def build_sanitized(verbose: bool = False) -> tuple[Path, Path]:
+    BUILD_DIR.mkdir(exist_ok=True)
+    SAN_DIR.mkdir(parents=True, exist_ok=True)
+
+    def run(cmd):
+        p = subprocess.run(cmd, capture_output=True, text=True)
+        log = "\n".join(line for line in (p.stdout + p.stderr).splitlines() if "packed-fp32-ops" not in line)
+        return p.returncode, log
+
+    # HIP library: the sanitized host objects linked with the regular device objects.
+    def one_hip(name):
+        obj = BUILD_DIR / f"san_{name}.o"
+        rc, log = run([hipcc(), "-x", "hip", "-c", str(CSRC / name), "-o", str(obj), *COMMON_FLAGS, "-g",
+                       *SAN_HOST_FLAGS])
+        return name, obj, rc, log
+
+    clangxx = str(llvm_dir() / "bin" / "clang++")
+
+    def one_fe(src):
+        obj = BUILD_DIR / f"san_frontend_{src.name}.o"
+        rc, log = run([clangxx, "-c", str(src), "-o", str(obj), *FRONTEND_FLAGS, "-g", *SAN_CXX_FLAGS])
+        return src.name, obj, rc, log
+
+    fe_sources = sorted(FRONTEND_SRC.glob("*.cpp"))
+    with cf.ThreadPoolExecutor(max_workers=6) as ex:
+        hip_res = list(ex.map(one_hip, SAN_HOST_SOURCES))
+        fe_res = list(ex.map(one_fe, fe_sources))
+    failures = [f"--- {n} ---\n{log}" for n, _, rc, log in hip_res + fe_res if rc != 0]
+    if failures:
+        raise RuntimeError("sanitized compilation failed:\n" + "\n".join(failures))
+    regular = [BUILD_DIR / (s.name + ".o") for s in sorted(CSRC.glob("*.hip"))]
+    hip_lib = SAN_DIR / LIB_PATH.name
+    rc, log = run([hipcc(), "-shared", f"--offload-arch={ARCH}", "-fPIC", "-o", str(hip_lib),
+                   *[str(o) for _, o, _, _ in hip_res], *map(str, regular), "-shared-libsan", *SAN_HOST_FLAGS[:4]])
+    if rc != 0:
+        raise RuntimeError("sanitized link failed:\n" + log)
+    fe_lib = SAN_DIR / FRONTEND_LIB_PATH.name
+    rc, log = run([clangxx, "-shared", "-o", str(fe_lib), *[str(o) for _, o, _, _ in fe_res], *SAN_CXX_FLAGS,
+                   *FRONTEND_LIBS])
+    if rc != 0:
+        raise RuntimeError("sanitized front-end link failed:\n" + log)
+    return hip_lib, fe_lib
 
 
 if __name__ == "__main__":
