@@ -159,6 +159,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   __shared__ __attribute__((aligned(1024))) half_t scratch_lds[kWaves * kScratchWave];
   __shared__ int16_t idx_tab[2 * 16 * MAXT];
   __shared__ __attribute__((aligned(16))) float mask_add[16 * MAXT];
+  __shared__ __attribute__((aligned(16))) int key_last[kWaves];  // per wave: last valid key + 1 among its keys, or 0
 
   // The stage buffers as LDS pointers: the DMA and the transposing reads
   // address them through these (no generic-to-LDS casts of computed pointers).
@@ -368,8 +369,10 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       // whose queries all lie past the extent computes nothing; it runs one
       // chunk step (its first stage is already in flight) and loads no V.
       const bool live = q0 < cur.qlen;
-      const int nt = live ? (cur.len + 15) >> 4 : 0;
-      const int nchunks = live ? (nt + 3) >> 2 : 1;
+      // Key tiles and chunks: set after chunk 0's barrier, once the key mask
+      // has been reduced (the initial values only keep chunk 0 running).
+      int nt = live ? (cur.len + 15) >> 4 : 0;
+      int nchunks = live ? (nt + 3) >> 2 : 1;
       const int klim = cur.klim;
       const bool active = qw < cur.qlen;
       const half_t* Kb = slice_base(K, b, h, cur.row0, ksb, ksh, ksl);
@@ -382,17 +385,29 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       // The key mask of batch row b as an additive term: 0 for a valid key,
       // -inf (probabilities) or -65504 (the SDPA mask output) for a masked
       // one; made visible by chunk 0's barrier.
+      bool valid = false;
       if (t < L) {
         const float m = (float)cs.mval;
-        const bool valid = mask_kind == GD_MASK_ATTENTION ? (m > 0.f) : !(m < -60000.f);
+        valid = mask_kind == GD_MASK_ATTENTION ? (m > 0.f) : !(m < -60000.f);
         mask_add[t] = valid ? 0.f : (OUT == GD_ATTN_OUT_BIAS ? -65504.f : -INFINITY);
       }
+      // Keys past the row's last valid one get probability exactly 0, so the
+      // probabilities and the context stop there (the bias output keeps
+      // every key: a masked key's bias is fp16(bias - 65504)).  A batch row
+      // with no valid key keeps the reference's degenerate softmax over every
+      // key (the masked scores themselves, below).  Each wave publishes the
+      // extent of its keys' valid ones; read after chunk 0's barrier.
+      if constexpr (OUT != GD_ATTN_OUT_BIAS) {
+        const uint64_t bal = __ballot(valid);
+        if (lane == 0) key_last[wave] = bal != 0 ? 64 * wave + 64 - __builtin_clzll(bal) : 0;
+      }
+      bool all_masked = false;  // uniform: set after chunk 0's barrier
 
       // ---- V for the P.V pass: rows [row_lo, row_hi) of the (b, h) slice
       // land row-major and swizzled like K at rows 0.. of an LDS buffer, by
       // DMA (placement: after the chunk loop).  Rows past the sequence repeat
       // row klim - 1; their probabilities are exactly 0. ----
-      const int v_rows = ((16 * nt + 31) >> 5) << 5;  // the P.V tile pairs reach this far
+      auto v_rows = [&]() { return ((16 * nt + 31) >> 5) << 5; };  // the P.V tile pairs reach this far
       auto issue_v = [&](lds_half_t* dst, int row_lo, int row_hi) {
         for (int blk = wave; 8 * blk < row_hi - row_lo; blk += kWaves) {  // uniform
           int key = row_lo + 8 * blk + blk_row;
@@ -401,19 +416,31 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
         }
       };
 
-      float sc[MAXT][4];  // tiles at or past nt are set to -inf after the chunk loop
+      float sc[MAXT][4];  // tiles at or past nt take no part in the softmax (probability 0)
 
 #pragma unroll
       for (int c = 0; c < MAXT / 4; ++c) {
         if (c >= nchunks) break;  // uniform
         wait_vmcnt<0>();
         __syncthreads();  // stage c landed everywhere; every wave is done with stage c - 1
+        if constexpr (OUT != GD_ATTN_OUT_BIAS) {
+          if (c == 0) {
+            const int4 a0 = *reinterpret_cast<const int4*>(key_last);
+            const int4 a1 = *reinterpret_cast<const int4*>(key_last + 4);
+            const int kext = __builtin_amdgcn_readfirstlane(
+                max(max(max(a0.x, a0.y), max(a0.z, a0.w)), max(max(a1.x, a1.y), max(a1.z, a1.w))));
+            all_masked = kext == 0;
+            const int klen = all_masked || kext > cur.len ? cur.len : kext;
+            nt = live ? (klen + 15) >> 4 : 0;
+            nchunks = live && nt > 0 ? (nt + 3) >> 2 : 1;
+          }
+        }
         half_t* const st = stages + (c & 1) * kStage;
         lds_half_t* const so = stages3 + ((c + 1) & 1) * kStage;  // free: every wave is done with stage c - 1
         if (c + 1 < nchunks) {
           issue_stage(so, Kb, PKh, PQh, (c + 1) * kKC, win(48 + c + 1), klim);
         } else if constexpr (OUT == GD_ATTN_OUT_CONTEXT) {  // V rows into the free buffer
-          if (!(c & 1) || !has_next) issue_v(so, 0, v_rows < kVRowsA ? v_rows : kVRowsA);
+          if (!(c & 1) || !has_next) issue_v(so, 0, v_rows() < kVRowsA ? v_rows() : kVRowsA);
         }
         const half_t* Ks = st;
         const half_t* PKs = st + kStageK;
@@ -428,9 +455,11 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
         // fixed 80 c2p and 32 p2c positions are computed (rows clamped to the
         // window; the extra ones are never gathered) and every score gathers
         // through the index table.  FULL: all 64 keys of the chunk exist.
-        auto chunk = [&](auto lin_c, auto full_c) {
+        // ALLM: the item's batch row has no valid key.
+        auto chunk = [&](auto lin_c, auto full_c, auto allm_c) {
           constexpr bool LIN = decltype(lin_c)::value;
           constexpr bool FULL = decltype(full_c)::value;  // LIN implies FULL
+          constexpr bool ALLM = decltype(allm_c)::value;
           // c2p for this wave's 16 queries and the chunk's keys: positions
           // [cw_lo, cw_lo + 80) = window rows [crow0, crow0 + 80)
           const int cw_lo = LIN ? qw - kc - (kKC - 1) + bucket_size : win(32 + c);
@@ -619,7 +648,23 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               float v;
-              if constexpr (SM == kScoreFused) {
+              if constexpr (ALLM) {
+                // Every key masked: the reference's scores with the mask term
+                // itself instead of -inf.  The fused kernel and the explicit
+                // chain's `where` set every score to -65504 (uniform
+                // weights); SDPA adds the kernel bias (-65504 on every key)
+                // or fp16(bias + -65504) in fp32; the kernel-bias explicit
+                // chain adds the bias in fp16.
+                if constexpr (SM == kScoreFused || SM == kScoreExplicit) {
+                  v = -65504.f;
+                } else if constexpr (SM == kScoreKernelBias) {
+                  v = fmaf(s_t[tt][i], scale_qk, -65504.f);
+                } else if constexpr (SM == kScoreKernelBiasExplicit) {
+                  v = round_f16(round_f16(round_f16(s_t[tt][i]) * inv_scale16) - 65504.f);
+                } else {
+                  v = fmaf(s_t[tt][i], scale_qk, round_f16(round_f16((float)sum16[i] * inv_scale16) - 65504.f));
+                }
+              } else if constexpr (SM == kScoreFused) {
                 v = ((s_t[tt][i] + c2p32[i]) + p2c32[i]) * scale_rel + madd[i];
               } else {
                 float bias16;
@@ -650,20 +695,15 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
         if (active) {
           const bool full = kc + kKC <= 16 * nt;
           const bool lin = full && (qw - kc - (kKC - 1) >= -kMid) && (qw + 15 - kc <= kMid);
-          if (lin)
-            chunk(std::true_type{}, std::true_type{});
+          if (all_masked)
+            chunk(std::false_type{}, std::false_type{}, std::true_type{});
+          else if (lin)
+            chunk(std::true_type{}, std::true_type{}, std::false_type{});
           else if (full)
-            chunk(std::false_type{}, std::true_type{});
+            chunk(std::false_type{}, std::true_type{}, std::false_type{});
           else
-            chunk(std::false_type{}, std::false_type{});
+            chunk(std::false_type{}, std::false_type{}, std::false_type{});
         }
-      }
-      if (nt < MAXT) {  // key tiles past the sequence take no part in the softmax
-#pragma unroll
-        for (int T = 0; T < MAXT; ++T)
-          if (T >= nt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) sc[T][i] = -INFINITY;
       }
       // The stage buffers are free from here on, except for V rows in flight
       // (context; waited for before the P.V pass) and the next item's stage.
@@ -679,8 +719,8 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       lds_half_t* const v_lo = stages3 + (v_in_0 ? 0 : kStage);  // V rows [0, kVRowsA)
       lds_half_t* const v_hi = stages3 + (v_in_0 ? kStage : 0);  // V rows [kVRowsA, v_rows)
       if constexpr (OUT == GD_ATTN_OUT_CONTEXT) {
-        if (last_in_1 && has_next) issue_v(v_lo, 0, v_rows < kVRowsA ? v_rows : kVRowsA);
-        if (MAXT * 16 > kVRowsA && v_rows > kVRowsA) issue_v(v_hi, kVRowsA, v_rows);  // no next item here
+        if (last_in_1 && has_next) issue_v(v_lo, 0, v_rows() < kVRowsA ? v_rows() : kVRowsA);
+        if (MAXT * 16 > kVRowsA && v_rows() > kVRowsA) issue_v(v_hi, kVRowsA, v_rows());  // no next item here
       }
       if (has_next) {  // after every V row; the set-up reads before the stage DMA (see setup_of)
         nit = decode(next);
@@ -695,8 +735,9 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
         float mx = -INFINITY;
 #pragma unroll
         for (int T = 0; T < MAXT; ++T)
+          if (T < nt)  // uniform
 #pragma unroll
-          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[T][i]);
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[T][i]);
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         const float mref = mx == -INFINITY ? 0.f : mx;
@@ -706,13 +747,19 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
         const float mref_l2 = mref * kLog2e;
         float sum = 0.f;
 #pragma unroll
-        for (int T = 0; T < MAXT; ++T)
+        for (int T = 0; T < MAXT; ++T) {
+          if (T < nt) {  // uniform
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float e = __builtin_amdgcn_exp2f(fmaf(sc[T][i], kLog2e, -mref_l2));  // v_exp_f32; exp2(-inf) = 0
-            sc[T][i] = e;
-            sum += e;
+            for (int i = 0; i < 4; ++i) {
+              const float e = __builtin_amdgcn_exp2f(fmaf(sc[T][i], kLog2e, -mref_l2));  // v_exp_f32; exp2(-inf) = 0
+              sc[T][i] = e;
+              sum += e;
+            }
+          } else {  // past the key extent: probability 0
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sc[T][i] = 0.f;
           }
+        }
         sum += __shfl_xor(sum, 16, 64);
         sum += __shfl_xor(sum, 32, 64);
         inv_sum = sum > 0.f ? 1.0f / sum : 0.f;
@@ -747,7 +794,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
         if (active) {
 #pragma unroll
           for (int T = 0; T < MAXT; ++T)
-            if (T < nt) {
+            if (16 * T < L) {  // tiles past the key extent hold 0 (probabilities) or the bias of every key
               half4_t v;
 #pragma unroll
               for (int i = 0; i < 4; ++i) v[i] = (half_t)sc[T][i];
@@ -799,7 +846,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
           const lds_half_t* vsrc = row0 < kVRowsA ? v_lo + row0 * kD : v_hi + (row0 - kVRowsA) * kD;
           // Unnormalised P of key tiles T, T + 1 as the A operand, split into
           // fp16 hi (truncated) + lo (the exact fp32 remainder, rounded).  Tiles
-          // at or past nt hold exp(-inf) = 0.
+          // at or past nt hold 0.
           // On the explicit chain the operand is P rounded to fp16 (the
           // reference's fp16 probabilities), with no low part.
           half8_t pa, pl;

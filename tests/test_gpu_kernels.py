@@ -483,6 +483,37 @@ def test_attention_score_chain_probs(L, score):
     assert np.max(np.abs(got - want)) <= 1e-3
 
 
+@pytest.mark.parametrize("L", [32, 256, 512])
+@pytest.mark.parametrize("score", ["default"] + sorted(SCORE_FLAGS))
+def test_attention_all_masked_row(L, score):
+    """A batch row with no valid key: the reference adds the mask term to
+    every score (fp16(bias + -65504) under SDPA, -65504 from the Metal
+    kernels and `where`), so its softmax is a degenerate one over every key,
+    not zeros.  Context against the oracle's attention stage (bound 4e-3, as
+    the other chains); probabilities sum to 1 and, on the default chain,
+    match the oracle within 1e-3 (the GPU forms q.k * s + mask in fp32,
+    whose grid at 65504 is 2^-8: |dP| <= P * 2^-9)."""
+    B, H = 2, 2
+    q, k, v, pk, pq, mask = _attn_case(500 + L, B, H, L)
+    mask[1] = 0
+    gpk, gpq = _gpu_tables(pk, pq, H)
+    pkh, pqh = _tables(pk, pq, H)
+    flags = SCORE_FLAGS.get(score, {})
+    want = O.attention_stage(q, k, v, pkh, pqh, mask, 64, **flags)
+    got = host(fk().deberta_attention(dev(q), dev(k), dev(v), gpk, gpq, dev(mask), output="context", score=score))
+    assert np.all(np.isfinite(got))
+    err = np.abs(got - want)
+    assert err.max() <= 4e-3, err.max()
+    assert np.abs(got[1]).max() > 0.05  # not the zeros of a softmax over no key
+    probs = host(fk().deberta_attention(dev(q), dev(k), None, gpk, gpq, dev(mask), output="probs", score=score))
+    np.testing.assert_allclose(probs.sum(-1), 1.0, atol=3e-3)
+    valid = np.broadcast_to(mask[:, None, None, :] > 0, probs.shape)
+    assert np.all(probs[0][~valid[0]] == 0)  # the row with valid keys keeps exact zeros
+    if score == "default":
+        _, want_p = _oracle_probs(q, k, pk, pq, mask)
+        assert np.max(np.abs(probs - want_p)) <= 1e-3
+
+
 @pytest.mark.parametrize("L", [32, 160, 256, 512])
 def test_relative_bias_closed_form_indices(L):
     """gd_relative_bias with NULL indices (the MFMA kernel-bias chain) against

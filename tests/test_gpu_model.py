@@ -356,6 +356,7 @@ def test_bucket_mix_workload():
 # every constructor flag of GLiNERDecideClassifier.init (DeBERTa.swift:188-196)
 # ---------------------------------------------------------------------------
 FLAG_SETS = {
+    "default": dict(),
     "fused_kernels": dict(use_fused_kernels=True),
     "generic_attention": dict(use_fast_attention=False),
     "custom_relative_kernel": dict(use_custom_relative_kernel=True),
@@ -370,7 +371,9 @@ def test_classifier_flags_match_oracle(name):
     against OracleModel with the same flags: hidden states and logits, with
     the bar of the default-path test (the spread between the float64 and
     float32 restatements, x2, floor 2e-3).  Packed, padded and full-row
-    classify agree bit for bit."""
+    classify agree bit for bit.  Row 3 has no valid token but unmasked
+    marker slots: the reference's degenerate softmax over every key
+    (DeBERTa.swift:329-335 with an all-zero mask) reaches its logits."""
     from gliner_decide import DecisionInput, GLiNERDecideClassifier
     from gliner_decide.config import DeBERTaV2Configuration
     from gliner_decide.synthetic import synthetic_weights
@@ -381,9 +384,9 @@ def test_classifier_flags_match_oracle(name):
     gpu = GLiNERDecideClassifier(w, pc, **flags)
     full = GLiNERDecideClassifier(w, pc, full_rows=True, **flags)
     r = np.random.default_rng(5)
-    B, L = 3, 96
+    B, L = 4, 96
     ids = r.integers(1000, 3000, size=(B, L)).astype(np.int32)
-    lengths = np.array([96, 61, 17])
+    lengths = np.array([96, 61, 17, 0])
     mask = (np.arange(L)[None] < lengths[:, None]).astype(np.float16)
     ids[mask == 0] = 0
     mi = np.array([[[1, 2, 3, 4], [5, 6, 0, 0]]] * B, np.int32)
@@ -406,7 +409,7 @@ def test_classifier_flags_match_oracle(name):
     assert np.all(packed[mm == 0] == -10000.0)
     assert np.max(np.abs(packed - want_logits)) <= 2e-3, name
     # and the flag changes the computation: the default graph's logits differ
-    if name != "fused_kernels":
+    if name not in ("default", "fused_kernels"):
         base = GLiNERDecideClassifier(w, pc).classify(inp).logits.float().cpu().numpy()
         assert not np.array_equal(base, packed), name
 

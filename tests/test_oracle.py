@@ -188,6 +188,31 @@ def test_attention_vs_torch_sdpa():
     np.testing.assert_allclose(got, want, atol=1e-6)  # the fp16 add of a -65504 mask vs -inf: identical probs
 
 
+def test_attention_all_masked_row_vs_torch_sdpa():
+    """A row with no valid key under SDPA: the additive mask is the fp16 sum
+    bias + -65504 (torch's half add: -65504 on the fp16 grid of spacing 32,
+    -inf past -65520, -65472 from +16 on), and the softmax runs over every
+    key -- a degenerate one, not zeros."""
+    r = np.random.default_rng(25)
+    B, H, L, D = 2, 2, 32, 64
+    q, k, v = (r.standard_normal((B, H, L, D)) for _ in range(3))
+    bias = r.standard_normal((B, H, L, L)).astype(np.float16)
+    bias[1, :, :, 3] = -20.0  # -> -inf
+    bias[1, :, :, 5] = 24.0  # -> -65472
+    mask = np.ones((B, L))
+    mask[1] = 0
+    got = O.attention_default(q, k, v, bias, mask, D, round16=False)
+    m16 = torch.from_numpy(bias) + torch.from_numpy(np.where(mask > 0, 0.0, -65504.0).astype(np.float16))[:, None, None]
+    assert torch.isinf(m16[1, :, :, 3]).all() and (m16[1, :, :, 5] == -65472.0).all()
+    want = torch.nn.functional.scaled_dot_product_attention(
+        torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v), attn_mask=m16.double(),
+        scale=O.scale_f32(D)).numpy()
+    want = np.transpose(want, (0, 2, 1, 3)).reshape(B, L, H * D)
+    # float64 scores near -65504 keep ~2^-36 absolute resolution
+    np.testing.assert_allclose(got, want, rtol=0, atol=1e-7)
+    assert np.abs(got[1]).max() > 0.1
+
+
 def test_attention_sdpa_mask_vs_torch_sdpa():
     """The useCustomRelativeKernel SDPA: the kernel's bias is the whole mask."""
     r = np.random.default_rng(15)
