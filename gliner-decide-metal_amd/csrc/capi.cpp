@@ -108,7 +108,8 @@ int gd_linear(const void* a, const void* w, const void* bias, void* c, int64_t m
                  (long long)k);
   GD_CHECK_SHAPE(lda >= k && lda % 8 == 0, "lda must be >= k and a multiple of 8");
   GD_CHECK_SHAPE(ldc >= n && ldc % 8 == 0, "ldc must be >= n and a multiple of 8");
-  GD_CHECK_ARG(aligned(a, 16) && aligned(w, 16) && aligned(c, 2), "a and w must be 16-byte aligned");
+  GD_CHECK_ARG(aligned(a, 16) && aligned(w, 16), "a and w must be 16-byte aligned");
+  GD_CHECK_ARG(aligned(c, 16), "c must be 16-byte aligned");
   GD_CHECK_SHAPE(!a_rows || (a_row_count > 0 && a_row_count <= 0x7fffffff), "a_row_count must be positive with a_rows");
   return launch_linear(a, w, bias, c, m, n, k, lda, ldc, a_rows, a_rows ? a_row_count : m, epilogue,
                        as_stream(stream));

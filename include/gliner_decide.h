@@ -128,7 +128,8 @@ typedef enum gd_epilogue {
 /* C[m, n] = epilogue(sum_k A[m, k] * W[n, k] (+ bias[n])), fp16 in/out, fp32
  * accumulation on MFMA.  W is [n, k] row-major (PyTorch Linear layout, as the
  * checkpoint stores it).  lda/ldc in elements.  Requires k % 64 == 0,
- * n % 128 == 0, lda % 8 == 0, ldc % 8 == 0.  When a_rows is not NULL, row m
+ * n % 128 == 0, lda % 8 == 0, ldc % 8 == 0, a, w and c 16-byte aligned.
+ * When a_rows is not NULL, row m
  * of A is A[a_rows[m], :] (row gather; used for the marker gather,
  * DeBERTa.swift:431-436); gathered indices are clamped into [0, a_row_count).
  * The first GD_EPI_BIAS_GELU call on a device fills that device's GELU table

@@ -56,6 +56,9 @@ def test_argument_validation_without_device():
     assert lib.gd_linear(FAKE, FAKE, None, FAKE, 8, 128, 64, 64, 128, None, 0, 1, None) == N.GD_ERR_INVALID_ARGUMENT
     assert lib.gd_linear(FAKE, FAKE, FAKE, FAKE, 8, 128, 64, 64, 128, FAKE, 0, 1, None) == N.GD_ERR_SHAPE
     assert lib.gd_linear(FAKE, FAKE, FAKE, FAKE, 8, 128, 64, 64, 128, None, 0, 9, None) == N.GD_ERR_INVALID_ARGUMENT
+    # the tile kernels store C in 16-byte row segments
+    assert lib.gd_linear(FAKE, FAKE, FAKE, FAKE + 8, 8, 128, 64, 64, 128, None, 0, 1, None) == N.GD_ERR_INVALID_ARGUMENT
+    assert "16-byte" in N.last_error()
     bh = N.GdBhld(FAKE, 0, 0, 64)
     tb = N.GdTable(FAKE, 512 * 64, 64)
     assert lib.gd_deberta_attention(bh, bh, bh, tb, tb, FAKE, 0, 1, 1, 40, 64, 512, 256, 0, FAKE, 40, None) == \
