@@ -137,14 +137,10 @@ def test_embedding_layer_norm():
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("m,n,k", [(1, 128, 64), (65, 256, 128), (300, 1024, 1024), (1000, 384, 192),
                                    (160, 1024, 4096), (160, 4096, 1024), (37, 2048, 1024),
-                                   (4096, 1024, 256), (8192, 3072, 1024),
+                                   (4096, 1024, 256), (8192, 3072, 1024), (8192, 4096, 1024),
                                    (4896, 4096, 256), (5500, 3072, 256)])  # split: whole rounds + 128x128 rest
 @pytest.mark.parametrize("epi", ["bias", "gelu", "relu", "none"])
 def test_linear(m, n, k, epi):
-    if m * n * k > 2 ** 31 and epi != "bias":
-        pytest.skip("large shape checked with the bias epilogue only")
-    if m in (4896, 5500) and epi in ("relu", "none"):
-        pytest.skip("the split launch is checked with the bias and GELU epilogues")
     r = np.random.default_rng(m + n + k)
     x = r.standard_normal((m, k)).astype(np.float16)
     w = (r.standard_normal((n, k)) / np.sqrt(k)).astype(np.float16)
@@ -161,9 +157,12 @@ def check_linear(out, x, w, b, epi):
     outputs (cancellation) are judged by the size of their terms, not by the
     ulp of the tiny result."""
     K = x.shape[1]
-    x64, w64 = x.astype(np.float64), w.astype(np.float64)
-    y = x64 @ w64.T + (b.astype(np.float64) if epi != "none" else 0.0)
-    acc = 4.0 * np.sqrt(K) * 2.0 ** -24 * (np.abs(x64) @ np.abs(w64).T)
+    # the products in float64 on the GPU (exact to ~1e-16 relative: fp16
+    # operands, float64 accumulation)
+    x64, w64 = torch.from_numpy(x).cuda().double(), torch.from_numpy(w).cuda().double()
+    y = (x64 @ w64.T).cpu().numpy() + (b.astype(np.float64) if epi != "none" else 0.0)
+    acc = 4.0 * np.sqrt(K) * 2.0 ** -24 * (x64.abs() @ w64.abs().T).cpu().numpy()
+    del x64, w64
     half = 0.5 * np.maximum(ulp16(y), ulp16(out))
     if epi in ("none", "bias"):
         bound, want = half + acc, y
