@@ -436,6 +436,7 @@ int gd_classifier_layer_forward(gd_classifier* model, int32_t layer_index, const
   clear_error();
   GD_RETURN_IF_ERROR(check_forward_args(model, hidden_in, attention_mask, batch, seq_len));
   GD_CHECK_ARG(hidden_out, "null output pointer");
+  GD_CHECK_ARG(aligned(hidden_in, 16) && aligned(hidden_out, 16), "hidden_in and hidden_out must be 16-byte aligned");
   return model->impl.layer(layer_index, hidden_in, attention_mask, batch, seq_len, hidden_out, as_stream(stream));
 }
 

@@ -347,7 +347,7 @@ int Classifier::classify_static(const int32_t* ids, const void* mask, const int3
 
 // One encoder layer (DeBERTa.swift:296-428).
 int Classifier::layer_forward(const Workspace& w, int li, const void* mask, int64_t B, int64_t L, hipStream_t stream, StageHook* hook,
-                              const Rows& rows, const int32_t* q_len, int64_t marker_count) {
+                              const Rows& rows, const int32_t* q_len, int64_t marker_count, const void* hidden_in) {
   const Layer& Ly = layers_[li];
   const int64_t C = cfg_.hidden_size, F = cfg_.intermediate_size, H = cfg_.num_attention_heads, D = C / H;
   const int64_t T = rows.tokens >= 0 ? rows.tokens : B * L;
@@ -360,9 +360,10 @@ int Classifier::layer_forward(const Workspace& w, int li, const void* mask, int6
   const uint32_t ln_flags = metal_ln ? 0u : GD_LN_SUM_F16;
   char name[48];
 
+  const void* in = hidden_in ? hidden_in : w.hidden;
   if (hook) hook->begin(stream);
   // QKV projection (:298-320)
-  GD_RETURN_IF_ERROR(launch_linear(w.hidden, Ly.qkv_w, Ly.qkv_b, w.qkv, T, 3 * C, C, C, 3 * C, nullptr, 0,
+  GD_RETURN_IF_ERROR(launch_linear(in, Ly.qkv_w, Ly.qkv_b, w.qkv, T, 3 * C, C, C, 3 * C, nullptr, 0,
                                    GD_EPI_BIAS, stream));
   if (hook) {
     std::snprintf(name, sizeof name, "layer_%d_attention_projection", li);
@@ -417,25 +418,27 @@ int Classifier::layer_forward(const Workspace& w, int li, const void* mask, int6
     hook->end(name, stream);
     hook->begin(stream);
   }
-  // Rows leaving the layer: all T in place in w.hidden, or the marker rows
-  // compact in w.qkv (free once the attention has read Q, K and V): their
-  // context rows (gathered into w.ffn, free until the FFN) go through the
-  // output projection, their hidden rows are gathered for the residual;
-  // every later step is row-wise.
+  // Rows leaving the layer: all T in w.hidden (the first residual LN reads
+  // the input rows and writes there), or the marker rows compact in w.qkv
+  // (free once the attention has read Q, K and V): their context rows
+  // (gathered into w.ffn, free until the FFN) go through the output
+  // projection, their hidden rows are gathered for the residual; every later
+  // step is row-wise.
   const bool compact = marker_count >= 0;
   const int64_t R = compact ? marker_count : T;
   void* hid = compact ? w.qkv : w.hidden;
   void* ctx = compact ? w.ffn : w.ctx;
+  const void* res = compact ? hid : in;
   if (compact) {
     const int32_t* rows_m = static_cast<const int32_t*>(w.marker_rows);
     GD_RETURN_IF_ERROR(launch_gather_rows(w.ctx, rows_m, R, T, C, ctx, stream));
-    GD_RETURN_IF_ERROR(launch_gather_rows(w.hidden, rows_m, R, T, C, hid, stream));
+    GD_RETURN_IF_ERROR(launch_gather_rows(in, rows_m, R, T, C, hid, stream));
   }
   // output projection + residual LayerNorm (:412-418)
   GD_RETURN_IF_ERROR(
       launch_linear(ctx, Ly.out_w, Ly.out_b, w.tmp, R, C, C, C, C, nullptr, 0, GD_EPI_BIAS, stream));
   GD_RETURN_IF_ERROR(
-      launch_residual_layer_norm(w.tmp, hid, Ly.ln1_g, Ly.ln1_b, hid, R, C, eps, ln_flags, stream));
+      launch_residual_layer_norm(w.tmp, res, Ly.ln1_g, Ly.ln1_b, hid, R, C, eps, ln_flags, stream));
   if (hook) {
     std::snprintf(name, sizeof name, "layer_%d_attention_output", li);
     hook->end(name, stream);
@@ -603,11 +606,11 @@ int Classifier::layer(int li, const void* hidden_in, const void* mask, int64_t B
                       hipStream_t stream) {
   GD_CHECK_ARG(li >= 0 && li < cfg_.num_hidden_layers, "layer index %d out of range", li);
   GD_RETURN_IF_ERROR(reserve(B, L, 1, 1));
-  const size_t bytes = (size_t)B * L * cfg_.hidden_size * 2;
-  GD_HIP_CHECK(hipMemcpyAsync(ws_.hidden, hidden_in, bytes, hipMemcpyDeviceToDevice, stream));
-  GD_RETURN_IF_ERROR(layer_forward(ws_, li, mask, B, L, stream, nullptr, Rows{}));
-  GD_HIP_CHECK(hipMemcpyAsync(hidden_out, ws_.hidden, bytes, hipMemcpyDeviceToDevice, stream));
-  return GD_OK;
+  // The layer reads hidden_in and its first residual LN writes hidden_out,
+  // which then serves as the layer's hidden rows: no staging copies.
+  Workspace w = ws_;
+  w.hidden = hidden_out;
+  return layer_forward(w, li, mask, B, L, stream, nullptr, Rows{}, nullptr, -1, hidden_in);
 }
 
 namespace {

@@ -94,8 +94,11 @@ class Classifier {
   // leave the layer, compact (row i = marker slot i) in ws_.qkv; attention
   // queries stop at q_len[b] (the classifier reads nothing else of the last
   // layer).
+  // hidden_in (optional): the layer's input rows when they are not w.hidden;
+  // the output is written to w.hidden either way.
   int layer_forward(const Workspace& w, int li, const void* mask, int64_t B, int64_t L, hipStream_t stream, StageHook* hook,
-                    const Rows& rows, const int32_t* q_len = nullptr, int64_t marker_count = -1);
+                    const Rows& rows, const int32_t* q_len = nullptr, int64_t marker_count = -1,
+                    const void* hidden_in = nullptr);
   int encode_into_workspace(const Workspace& w, const int32_t* ids, const void* mask, int64_t B, int64_t L, int num_layers,
                             hipStream_t stream, StageHook* hook, const Rows& rows);
   // packed_exact = false: packed_tokens is a capacity >= the extents' sum.

@@ -363,7 +363,8 @@ int gd_classifier_encode(gd_classifier* model, const int32_t* input_ids, const v
 
 /* One encoder layer (DeBERTa.swift:296-428) on caller hidden states:
  * hidden_out = layer_<layer_index>(hidden_in) for [B, L, hidden] fp16 with
- * the fp16 attention mask [B, L].  hidden_out may alias hidden_in. */
+ * the fp16 attention mask [B, L].  hidden_out may alias hidden_in; both are
+ * 16-byte aligned (the layer reads and writes them in place: no staging). */
 int gd_classifier_layer_forward(gd_classifier* model, int32_t layer_index, const void* hidden_in,
                                 const void* attention_mask, int64_t batch, int64_t seq_len,
                                 void* hidden_out, void* stream);
