@@ -544,6 +544,16 @@ def main():
     log(f"e2e full rows: {full_s * 1000 / args.steps:.3f} ms/step, {B * args.steps / full_s:.1f} rows/s")
     full.close()
     del full
+    # The reference's batch loop (main.swift:259-276): host arrays in, each
+    # batch's forward waited for and its logits read back before the next.
+    # PCIe-inclusive and synchronous; never `value`.
+    host_inp = DecisionInput(**host)
+    host_step = lambda: model.classify(host_inp).logits.cpu()  # noqa: E731
+    for _ in range(args.warmup):
+        host_step()
+    host_s = timed(host_step, args.steps)
+    assert torch.equal(model.classify(host_inp).logits, packed_logits), "host-array logits differ"
+    log(f"e2e host arrays, synchronous: {host_s * 1000 / args.steps:.3f} ms/step, {B * args.steps / host_s:.1f} rows/s")
 
     kernels = measure_kernels(cfg, args.kernel_iters)
     for k, v in kernels.items():
@@ -596,6 +606,7 @@ def main():
         "bucket_mix_rows_s": mix,
         "padded_rows_s": round(B * args.steps / padded_s, 2),
         "full_rows_s": round(B * args.steps / full_s, 2),
+        "host_sync_rows_s": round(B * args.steps / host_s, 2),
         "relative_bias_gbs": round(kernels["relative_bias"]["gbs"], 1),
         "relative_bias_frac_hbm": round(kernels["relative_bias"]["gbs"] / HBM_PEAK_GBS, 4),
         "single_layer_b1_l32": layer1,

@@ -35,7 +35,7 @@ COMMON_FLAGS = [
     "-Wno-unused-function",
     "-Wno-unused-variable",
     "-Wno-unused-command-line-argument",
-    # Packed fp32 VALU forms are not to be generated on this hardware pool.
+    # No packed fp32 VALU forms (v_pk_add/mul/fma_f32) in the generated code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{REPO / 'include'}",
     f"-I{CSRC}",

@@ -2,6 +2,7 @@
 // schedule, packed-row offsets), the relative index table the attention
 // kernel reads, and the dispatch of launch_deberta_attention over the score
 // modes (each instantiated in its own attention_sm_*.hip).
+#include <algorithm>
 #include <atomic>
 #include <climits>
 #include <cmath>
@@ -261,6 +262,9 @@ int launch_deberta_attention(const AttentionArgs& a, hipStream_t stream) {
     return fail(GD_ERR_INVALID_ARGUMENT, "attention: schedule does not match the launch");
   for (int64_t st : {a.qsb, a.qsh, a.qsl, a.ksb, a.ksh, a.ksl, a.vsb, a.vsh, a.vsl, a.pksh, a.pksp, a.pqsh, a.pqsp, a.ldo})
     if (st < 0 || st > INT32_MAX) return fail(GD_ERR_SHAPE, "attention: strides must lie in [0, 2^31)");
+  // the stage loads address a table row by its 32-bit byte offset from the head's first row
+  if (((a.P - 1) * std::max(a.pksp, a.pqsp) + 64) * 2 > INT32_MAX)
+    return fail(GD_ERR_SHAPE, "attention: position-table rows must lie within 2 GiB of a head's first row");
   if (a.output != GD_ATTN_OUT_PROBS && a.output != GD_ATTN_OUT_CONTEXT && a.output != GD_ATTN_OUT_BIAS)
     return fail(GD_ERR_INVALID_ARGUMENT, "attention: unknown output kind");
   if (a.output == GD_ATTN_OUT_BIAS && a.score != kScoreDefault && a.score != kScoreKernelBias)

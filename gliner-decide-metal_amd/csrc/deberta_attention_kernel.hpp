@@ -7,18 +7,20 @@
 // waves, wave w owning queries q0 + 16w .. q0 + 16w + 15.  The LDS holds one
 // workgroup per CU; up to L = 256 the grid has one workgroup per CU, each
 // looping over items and fetching the next item's first stage while it
-// finishes the current one.  Keys stream through LDS in chunks of 64.  For
-// a chunk, every relative index the workgroup can need, idx(q - k) for its
-// 128 queries and the chunk's 64 keys, lies in one window of at most 191
-// consecutive rows of the relative tables (idx is monotone in q - k), so the
-// stage of a chunk is
+// finishes the current one.  Keys stream through LDS in chunks of 64.  The
+// pairs (q, k) of a chunk have q - k in [bot, bot + 190], bot = q0 - kc - 63,
+// so the stage of a chunk is
 //     K rows        64 x 128 B
 //     posK window  192 x 128 B   (relative keys, for c2p)
 //     posQ window  192 x 128 B   (relative queries, for p2c)
-// fetched with global_load_lds_dwordx4 (16 B per lane straight into LDS; the
-// XOR swizzle of the 128-byte rows is applied on the global side) into one of
-// two buffers while the other chunk is computed.  Inside a chunk nothing
-// touches global memory:
+// where window row j holds table row idx(bot + j): the stage gathers table
+// rows through the index table, so inside the window the relative index is
+// the plain distance q - k - bot for every pair, in the log-bucket zone as in
+// the linear one, and every gather below is at a closed-form offset.  The
+// stage is fetched with global_load_lds_dwordx4 (16 B per lane straight into
+// LDS, each lane from its own table row; the XOR swizzle of the 128-byte rows
+// is applied on the global side) into one of two buffers while the other
+// chunk is computed.  Inside a chunk nothing touches global memory:
 //   c2p  per wave: C2P^T = posK[window] . Q^T over <= 80 positions (5 MFMA
 //        column tiles, v_mfma_f32_16x16x32_f16), rounded to fp16 (the
 //        reference's c2pRaw) into a per-wave LDS tile;
@@ -56,14 +58,13 @@ constexpr int kQT = 128;           // queries per workgroup
 constexpr int kKC = 64;            // keys per chunk
 constexpr int kD = 64;             // head dim
 constexpr int kWin = 192;          // relative-table rows per chunk window (>= 191)
-constexpr int kMid = 128;          // |q - k| <= kMid: idx(q - k) = q - k + 256 (bucket size 256)
 constexpr int kC2PCols = 80;       // per-wave c2p window (<= 79 positions)
 constexpr int kC2PStride = kC2PCols + 4;  // 168-byte rows keep the 8-byte stores aligned
 // Per-wave p2c tile (16 keys x 32 window positions), stored skewed: value
 // (key row kr, position p) at (kr + p) * kP2CSkew + kr.  A score's four keys
-// 4g .. 4g+3 in the linear zone share kr + p = 15 + lc, so its four p2c terms
-// are one aligned 8-byte read; rows of 24 halfs make those reads
-// conflict-free across the wave.
+// 4g .. 4g+3 share kr + p = 15 + lc, so its four p2c terms are one aligned
+// 8-byte read; rows of 24 halfs make those reads conflict-free across the
+// wave.
 constexpr int kP2CSkew = 24;
 constexpr int kP2CRows = 47;       // kr + p <= 15 + 31
 constexpr int kVRowsA = 448;       // V rows held by one stage buffer (448 x 128 B = 56 KiB)
@@ -182,48 +183,41 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
 
   // ---- stage loads: lane l of 1 KiB block `blk` writes physical chunk l%8 of
   // row 8*blk + l/8, so it fetches the logical chunk that swz() puts there.
-  // Every block this wave loads has the parity of the wave index.  `wlo` is
-  // the relative-table row at window row 0.  The chunk's pairs have
-  // q - k in [bot, top = bot + 190], bot = q0 - kc - 63.  When bot or top lies
-  // in the linear zone [-128, 128], wlo is the linear extrapolation bot + 256:
-  // every index the chunk needs lies in [wlo, wlo + 190] (log buckets keep
-  // |bucket(r)| <= |r| and stay beyond the linear zone's ends), and every
-  // wave whose own pairs are all linear finds its rows at closed-form,
-  // 16-aligned offsets.  Otherwise wlo = idx(bot).  wlo is then clamped to
-  // [0, 512 - 192] so that every window row exists (the indices lie in
-  // [0, 511]); the clamp moves only windows with no all-linear wave (their
-  // bot lies in (64, 128] or below -256). ----
+  // Every block this wave loads has the parity of the wave index.  Window row
+  // j of a chunk with lowest distance bot = q0 - kc - 63 is table row
+  // idx(bot + j), with the distance clamped to [-(L - 1), L - 1] (rows of
+  // distances past it are never gathered).  The table offsets are 32-bit
+  // byte offsets from the head's first row (checked by the launcher). ----
   const int blk_row = lane >> 3;
   const int blk_chunk = (lane & 7) ^ (((wave & 1) << 2) | (lane >> 4));
-  // byte offsets of this lane's 16-byte piece from a block's first table row
-  const uint32_t pk_lane = (uint32_t)((blk_row * pksp + blk_chunk * 8) * 2);
-  const uint32_t pq_lane = (uint32_t)((blk_row * pqsp + blk_chunk * 8) * 2);
-  auto window_lo = [&](int q0, int kc, auto&& idx_of) -> int {
-    const int bot = q0 - kc - (kKC - 1), top = bot + kQT + kKC - 2;
-    const bool lin = (bot >= -kMid && bot <= kMid) || (top >= -kMid && top <= kMid);
-    const int w = lin ? bot + bucket_size : idx_of(bot);
-    return w < 0 ? 0 : (w > 512 - kWin ? 512 - kWin : w);
-  };
   // Stage of key chunk kc into buffer st: kStageOps DMA instructions per wave.
-  auto issue_stage = [&](lds_half_t* st, const half_t* Kb, const half_t* PKh, const half_t* PQh, int kc, int wlo,
-                         int klim) {
+  // idx_of(r) maps a clamped distance to its table row.
+  auto issue_stage = [&](lds_half_t* st, const half_t* Kb, const half_t* PKh, const half_t* PQh, int kc, int bot,
+                         int klim, auto&& idx_of) {
+    int prow[kWin / 8 / kWaves];
+#pragma unroll
+    for (int j = 0; j < kWin / 8 / kWaves; ++j) {
+      int r = bot + 8 * (wave + kWaves * j) + blk_row;
+      r = r < -(L - 1) ? -(L - 1) : (r > L - 1 ? L - 1 : r);
+      prow[j] = idx_of(r);
+    }
     {  // K rows: 8 blocks of 8 rows, one per wave; rows from klim on repeat row klim - 1
       int key = kc + wave * 8 + blk_row;
       key = key < klim ? key : klim - 1;
       load_lds16(Kb + (int64_t)key * ksl + blk_chunk * 8, st + wave * 512);
     }
 #pragma unroll
-    for (int j = 0; j < kWin / 8 / kWaves; ++j) {  // 3 blocks per wave per table; rows wlo .. wlo + 191 exist
+    for (int j = 0; j < kWin / 8 / kWaves; ++j) {  // 3 blocks per wave per table
       const int blk = wave + kWaves * j;
-      const int p0 = wlo + blk * 8;  // uniform
-      load_lds16(PKh + (int64_t)p0 * pksp, pk_lane, st + kStageK + blk * 512);
-      load_lds16(PQh + (int64_t)p0 * pqsp, pq_lane, st + kStageK + kStageWin + blk * 512);
+      load_lds16(PKh, (uint32_t)((prow[j] * pksp + blk_chunk * 8) * 2), st + kStageK + blk * 512);
+      load_lds16(PQh, (uint32_t)((prow[j] * pqsp + blk_chunk * 8) * 2), st + kStageK + kStageWin + blk * 512);
     }
   };
   constexpr int kStageOps = 1 + 2 * (kWin / 8 / kWaves);
-  auto rel_arith = [&](int r) -> int {  // idx(r) computed: no memory wait in front of a DMA
-    return relative_index(r < -(L - 1) ? -(L - 1) : r, 256, 512);
-  };
+  // idx(r) computed (the first stage, issued before the LDS index table exists)
+  auto rel_arith = [&](int r) -> int { return relative_index(r, 256, 512); };
+  // idx(r) from the LDS index table
+  auto rel_lds = [&](int r) -> int { return idx_tab[r + L - 1]; };
 
   // ---- work items: (b, h, 128-query tile).  Up to L = 256 the grid holds
   // at most one workgroup per CU (the LDS allows no more) and workgroup w
@@ -286,42 +280,26 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     return Item{b, __builtin_amdgcn_readfirstlane(bh % H), empty ? ntq : __builtin_amdgcn_readfirstlane(bid % ntq), len,
                 len > 0 ? len : 1, row0, qlen};
   };
-  // Window start of chunk 0 per query tile (at most 4), lane qt of w0_tab.
-  const int w0_tab = window_lo(kQT * (lane & 3), 0, rel_arith);
-  auto stage0_of = [&](const Item& it, lds_half_t* st) {
+  // First stage of an item (chunk 0: bot = q0 - 63).
+  auto stage0_of = [&](const Item& it, lds_half_t* st, auto&& idx_of) {
     issue_stage(st, slice_base(K, it.b, it.h, it.row0, ksb, ksh, ksl), PK + (int64_t)it.h * pksh,
-                PQ + (int64_t)it.h * pqsh, 0, __builtin_amdgcn_readlane(w0_tab, it.qt), it.klim);
+                PQ + (int64_t)it.h * pqsh, 0, it.qt * kQT - (kKC - 1), it.klim, idx_of);
   };
-  // Per-thread set-up reads of an item: its key-mask entry, its lane of the
-  // window table and the Q fragments.  Window table (read with readlane):
-  // lane T < MAXT holds idx(qw - 16 T - 15), the first p2c position of key
-  // tile T; lane 32 + c holds idx(qw - 64 c - 63), the first c2p position of
-  // chunk c; lane 48 + c holds wlo of chunk c.
+  // Per-thread set-up reads of an item: its key-mask entry and the Q
+  // fragments.
   static_assert(2 * kThreads >= 2 * 16 * MAXT - 1 && kThreads >= 16 * MAXT, "one pass of set-up reads");
   struct Setup {
     half8_t qf0, qf1;  // Q[qw + lc][8g..] and [32 + 8g..] (B operand of K Q^T)
-    int win_tab;
     half_t mval;
   };
   // The global loads are unconditional (clamped rows; values of rows past
-  // the sequence are never used) and the window indices come from the LDS
-  // index table.  An item's set-up reads are issued before its stage DMA: any
-  // vmcnt wait the compiler places among them (it does not count the DMA,
-  // which is inline assembly) then cannot wait for that DMA.
-  auto rel_lds = [&](int r) -> int {
-    r = r < -(L - 1) ? -(L - 1) : (r > L - 1 ? L - 1 : r);
-    return idx_tab[r + L - 1];
-  };
+  // the sequence are never used).  An item's set-up reads are issued before
+  // its stage DMA: any vmcnt wait the compiler places among them (it does not
+  // count the DMA, which is inline assembly) then cannot wait for that DMA.
   auto setup_of = [&](const Item& it) -> Setup {
     Setup su;
     const int q0 = it.qt * kQT, qw = q0 + 16 * wave;
     su.mval = mask[(int64_t)it.b * L + (t < L ? t : L - 1)];
-    if (lane < 32)
-      su.win_tab = rel_lds(qw - 16 * lane - 15);
-    else if (lane < 48)
-      su.win_tab = rel_lds(qw - kKC * (lane - 32) - (kKC - 1));
-    else
-      su.win_tab = window_lo(q0, kKC * (lane - 48), rel_lds);
     const int qr = qw + lc < it.klim ? qw + lc : it.klim - 1;
     const half_t* qrow = slice_base(Q, it.b, it.h, it.row0, qsb, qsh, qsl) + (int64_t)qr * qsl;
     su.qf0 = *reinterpret_cast<const half8_t*>(qrow + 8 * g);
@@ -331,7 +309,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
 
   int item = blockIdx.x;
   Item cur = decode(item);
-  stage0_of(cur, stages3);
+  stage0_of(cur, stages3, rel_arith);
   // The index table, the same for every item, is built once.
   const int n_idx = 2 * L - 1;
   const int16_t id0 = t < n_idx ? rel_idx[t - (L - 1) + kRelSpan] : (int16_t)0;
@@ -380,8 +358,6 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       const half_t* PQh = PQ + (int64_t)h * pqsh;
       const half_t* Vb = slice_base(V, b, h, cur.row0, vsb, vsh, vsl);
       const half8_t qf0 = cs.qf0, qf1 = cs.qf1;
-      const int win_tab = cs.win_tab;
-      auto win = [&](int j) -> int { return __builtin_amdgcn_readlane(win_tab, j); };
       // The key mask of batch row b as an additive term: 0 for a valid key,
       // -inf (probabilities) or -65504 (the SDPA mask output) for a masked
       // one; made visible by chunk 0's barrier.
@@ -438,7 +414,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
         half_t* const st = stages + (c & 1) * kStage;
         lds_half_t* const so = stages3 + ((c + 1) & 1) * kStage;  // free: every wave is done with stage c - 1
         if (c + 1 < nchunks) {
-          issue_stage(so, Kb, PKh, PQh, (c + 1) * kKC, win(48 + c + 1), klim);
+          issue_stage(so, Kb, PKh, PQh, (c + 1) * kKC, q0 - (c + 1) * kKC - (kKC - 1), klim, rel_lds);
         } else if constexpr (OUT == GD_ATTN_OUT_CONTEXT) {  // V rows into the free buffer
           if (!(c & 1) || !has_next) issue_v(so, 0, v_rows() < kVRowsA ? v_rows() : kVRowsA);
         }
@@ -446,44 +422,24 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
         const half_t* PKs = st + kStageK;
         const half_t* PQs = st + kStageK + kStageWin;
         const int kc = c * kKC;
-        const int wlo = win(48 + c);
         // The chunk's work for this wave, in compile-time variants whose bodies
-        // have no branches, so the scheduler can overlap the tiles freely.  LIN
-        // (every (query, key) pair of this wave lies in the linear zone): every
-        // window offset is closed-form and 16-aligned and the gathers are
-        // contiguous.  Otherwise the window starts come from the lane table, the
-        // fixed 80 c2p and 32 p2c positions are computed (rows clamped to the
-        // window; the extra ones are never gathered) and every score gathers
-        // through the index table.  FULL: all 64 keys of the chunk exist.
-        // ALLM: the item's batch row has no valid key.
-        auto chunk = [&](auto lin_c, auto full_c, auto allm_c) {
-          constexpr bool LIN = decltype(lin_c)::value;
-          constexpr bool FULL = decltype(full_c)::value;  // LIN implies FULL
+        // have no branches, so the scheduler can overlap the tiles freely.
+        // Window row of the pair (q, k) is q - k - bot (bot = q0 - kc - 63):
+        // every offset below is closed-form and 16-aligned and the gathers
+        // are contiguous.  FULL: all 64 keys of the chunk exist.  ALLM: the
+        // item's batch row has no valid key.
+        auto chunk = [&](auto full_c, auto allm_c) {
+          constexpr bool FULL = decltype(full_c)::value;
           constexpr bool ALLM = decltype(allm_c)::value;
-          // c2p for this wave's 16 queries and the chunk's keys: positions
-          // [cw_lo, cw_lo + 80) = window rows [crow0, crow0 + 80)
-          const int cw_lo = LIN ? qw - kc - (kKC - 1) + bucket_size : win(32 + c);
-          const int crow0 = cw_lo - wlo;
-          // Off the linear zone a lane's window row r = crow0 + 16 tw + lc may run
-          // past the window; such rows hold positions this wave never gathers and
-          // are clamped to a row with the same r mod 16, so the swizzle term of
-          // the lane is the same for every tile.
-          const int crow_l = crow0 + lc;
-          const int crow_lim = kWin - 16 + (crow_l & 15);
-          const int csw_lo = (g ^ ((crow_l >> 1) & 7)) << 3, csw_hi = ((4 + g) ^ ((crow_l >> 1) & 7)) << 3;
+          // c2p for this wave's 16 queries and the chunk's keys: window rows
+          // [16 wave, 16 wave + 80) (distances qw - kc - 63 .. qw - kc + 16)
+          const int crow0 = 16 * wave;
           if constexpr (!B32) {  // the fp32 chains compute c2p per key tile instead
 #pragma unroll
           for (int tw = 0; tw < kC2PCols / 16; ++tw) {
             {
-              half8_t a0, a1;
-              if constexpr (LIN) {  // crow0 = 16 wave
-                a0 = *reinterpret_cast<const half8_t*>(PKs + (crow0 + 16 * tw) * kD + swz_lo);
-                a1 = *reinterpret_cast<const half8_t*>(PKs + (crow0 + 16 * tw) * kD + swz_hi);
-              } else {
-                const int row = crow_l + 16 * tw < crow_lim ? crow_l + 16 * tw : crow_lim;
-                a0 = *reinterpret_cast<const half8_t*>(PKs + row * kD + csw_lo);
-                a1 = *reinterpret_cast<const half8_t*>(PKs + row * kD + csw_hi);
-              }
+              const half8_t a0 = *reinterpret_cast<const half8_t*>(PKs + (crow0 + 16 * tw) * kD + swz_lo);
+              const half8_t a1 = *reinterpret_cast<const half8_t*>(PKs + (crow0 + 16 * tw) * kD + swz_hi);
               float4_t r = {0.f, 0.f, 0.f, 0.f};
               r = mfma16x16x32(a0, qf0, r);
               r = mfma16x16x32(a1, qf1, r);
@@ -496,37 +452,24 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
           }
 
           // Per 16-key tile tt: S^T = K Q^T (scores) and P2C = K . posQ[window]^T
-          // over the <= 31 positions [pp_lo, pp_lo + 16 nj) the tile needs, stored
-          // skewed into p2c_w.  Tiles are software-pipelined: tile tt's gathers are
-          // issued before tile tt+1's MFMAs and p2c stores (the LDS executes a
-          // wave's accesses in order, so one p2c buffer suffices), and tile tt is
-          // combined while those are in flight.
-          int pp_lo[4];
+          // over the 31 window rows [prow0, prow0 + 31) the tile needs (prow0 =
+          // 16 (wave - tt) + 48), stored skewed into p2c_w.  Tiles are
+          // software-pipelined: tile tt's gathers are issued before tile tt+1's
+          // MFMAs and p2c stores (the LDS executes a wave's accesses in order, so
+          // one p2c buffer suffices), and tile tt is combined while those are in
+          // flight.
           float4_t s_t[4];
           half8_t fk[2][2], fq[2][4];  // per tile parity: K rows (chunks g, 4+g), posQ rows (j = 0, 1)
           // Operand fragments of tile tt (LDS reads only; issued a tile ahead).
           auto prep_load = [&](int tt) {
-            const int k0 = kc + 16 * tt;
             const int par = tt & 1;
-            pp_lo[tt] = LIN ? qw - k0 - 15 + bucket_size : win(4 * c + tt);
-            const int prow0 = pp_lo[tt] - wlo;
-            const int prow_l = prow0 + lc;  // clamped as the c2p rows
-            const int prow_lim = kWin - 16 + (prow_l & 15);
-            const int psw_lo = (g ^ ((prow_l >> 1) & 7)) << 3, psw_hi = ((4 + g) ^ ((prow_l >> 1) & 7)) << 3;
+            const int prow0 = 16 * (wave - tt) + 48;
             fk[par][0] = *reinterpret_cast<const half8_t*>(Ks + 16 * tt * kD + swz_lo);
             fk[par][1] = *reinterpret_cast<const half8_t*>(Ks + 16 * tt * kD + swz_hi);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-              {
-                if constexpr (LIN) {  // prow0 = 16 (wave - tt) + 48
-                  fq[par][2 * j] = *reinterpret_cast<const half8_t*>(PQs + (prow0 + 16 * j) * kD + swz_lo);
-                  fq[par][2 * j + 1] = *reinterpret_cast<const half8_t*>(PQs + (prow0 + 16 * j) * kD + swz_hi);
-                } else {
-                  const int row = prow_l + 16 * j < prow_lim ? prow_l + 16 * j : prow_lim;
-                  fq[par][2 * j] = *reinterpret_cast<const half8_t*>(PQs + row * kD + psw_lo);
-                  fq[par][2 * j + 1] = *reinterpret_cast<const half8_t*>(PQs + row * kD + psw_hi);
-                }
-              }
+              fq[par][2 * j] = *reinterpret_cast<const half8_t*>(PQs + (prow0 + 16 * j) * kD + swz_lo);
+              fq[par][2 * j + 1] = *reinterpret_cast<const half8_t*>(PQs + (prow0 + 16 * j) * kD + swz_hi);
             }
           };
           // Scores and p2c of tile tt from its fragments; p2c stored skewed.
@@ -556,25 +499,14 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
               }
             }
             if constexpr (B32) {
-              // C2P^T = posK[the tile's 32 positions] . Q^T, the same window
-              // rows as the p2c fragments (every index of the tile lies in
-              // [pp_lo, pp_lo + 32)); lane holds (position 16 j + 4 g + i,
+              // C2P^T = posK[the tile's 32 window rows] . Q^T, the same window
+              // rows as the p2c fragments; lane holds (row 16 j + 4 g + i,
               // query lc).
-              const int prow0 = pp_lo[tt] - wlo;
-              const int prow_l = prow0 + lc;
-              const int prow_lim = kWin - 16 + (prow_l & 15);
-              const int psw_lo = (g ^ ((prow_l >> 1) & 7)) << 3, psw_hi = ((4 + g) ^ ((prow_l >> 1) & 7)) << 3;
+              const int prow0 = 16 * (wave - tt) + 48;
 #pragma unroll
               for (int j = 0; j < 2; ++j) {
-                half8_t a0, a1;
-                if constexpr (LIN) {
-                  a0 = *reinterpret_cast<const half8_t*>(PKs + (prow0 + 16 * j) * kD + swz_lo);
-                  a1 = *reinterpret_cast<const half8_t*>(PKs + (prow0 + 16 * j) * kD + swz_hi);
-                } else {
-                  const int row = prow_l + 16 * j < prow_lim ? prow_l + 16 * j : prow_lim;
-                  a0 = *reinterpret_cast<const half8_t*>(PKs + row * kD + psw_lo);
-                  a1 = *reinterpret_cast<const half8_t*>(PKs + row * kD + psw_hi);
-                }
+                const half8_t a0 = *reinterpret_cast<const half8_t*>(PKs + (prow0 + 16 * j) * kD + swz_lo);
+                const half8_t a1 = *reinterpret_cast<const half8_t*>(PKs + (prow0 + 16 * j) * kD + swz_hi);
                 float4_t r = {0.f, 0.f, 0.f, 0.f};
                 r = mfma16x16x32(a0, qf0, r);
                 r = mfma16x16x32(a1, qf1, r);
@@ -596,44 +528,24 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
             if (next) prep_load(tt + 1);  // fragment reads overlap this tile's gathers
             wave_lds_sync();  // tile tt's p2c stores (and the chunk's c2p) precede its gathers
             // Gather the two terms of score (q = qw + lc, k = k0 + 4g + i) at
-            // idx(q - k).  In the linear zone idx = q - k + 256: the four c2p
-            // terms are consecutive (descending) in the lane's c2p row and the
-            // four p2c terms are one 8-byte read.
+            // window row q - k - bot: the four c2p terms are consecutive
+            // (descending) in the lane's c2p row, at column 63 - 16 tt + lc -
+            // 4 g - i, and the four p2c terms (tile row 15 + lc - 4 g - i) are
+            // one 8-byte read.
             const float4_t madd = *reinterpret_cast<const float4_t*>(mask_add + k0 + 4 * g);
             half4_t c2p, p2c;
             float4_t c2p32, p2c32;
             if constexpr (B32) {
-              if constexpr (LIN) {  // position idx - pp_lo = 15 + lc - 4 g - i
-                const float* cp = c2pf + lc * kC2PF32Stride + 15 + lc - 4 * g;
+              const float* cp = c2pf + lc * kC2PF32Stride + 15 + lc - 4 * g;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) c2p32[i] = cp[-i];
-                const int row = 15 + lc;
-                p2c32 = *reinterpret_cast<const float4_t*>(p2cf + row * 16 + ((g ^ ((row >> 2) & 3)) << 2));
-              } else {
-                const int r0 = qw + lc - k0 - 4 * g + L - 1;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                  const int pos = idx_tab[r0 - i] - pp_lo[tt];  // 0 <= pos < 32
-                  c2p32[i] = c2pf[lc * kC2PF32Stride + pos];
-                  const int row = 4 * g + i + pos;
-                  p2c32[i] = p2cf[row * 16 + ((g ^ ((row >> 2) & 3)) << 2) + i];
-                }
-              }
-            } else if constexpr (LIN) {
-              const half_t* cp = c2p_w + lc * kC2PStride + (qw - k0 + bucket_size - cw_lo) + lc - 4 * g;
+              for (int i = 0; i < 4; ++i) c2p32[i] = cp[-i];
+              const int row = 15 + lc;
+              p2c32 = *reinterpret_cast<const float4_t*>(p2cf + row * 16 + ((g ^ ((row >> 2) & 3)) << 2));
+            } else {
+              const half_t* cp = c2p_w + lc * kC2PStride + 63 - 16 * tt + lc - 4 * g;
 #pragma unroll
               for (int i = 0; i < 4; ++i) c2p[i] = cp[-i];
               p2c = *reinterpret_cast<const half4_t*>(p2c_w + (15 + lc) * kP2CSkew + 4 * g);
-            } else {
-              const int r0 = qw + lc - k0 - 4 * g + L - 1;
-              const half_t* cb = c2p_w + lc * kC2PStride - cw_lo;
-              const half_t* pb = p2c_w + (4 * g - pp_lo[tt]) * kP2CSkew + 4 * g;
-#pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                const int id = idx_tab[r0 - i];  // 0 <= id < 512
-                c2p[i] = cb[id];
-                p2c[i] = pb[__mul24(id, kP2CSkew) + i * (kP2CSkew + 1)];
-              }
             }
             wave_lds_sync();  // these gathers precede the next tile's p2c stores
             if (next) prep_compute(tt + 1);
@@ -693,16 +605,12 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
           wave_lds_sync();  // the last gathers precede the next chunk's c2p / p2c stores
         };
         if (active) {
-          const bool full = kc + kKC <= 16 * nt;
-          const bool lin = full && (qw - kc - (kKC - 1) >= -kMid) && (qw + 15 - kc <= kMid);
           if (all_masked)
-            chunk(std::false_type{}, std::false_type{}, std::true_type{});
-          else if (lin)
-            chunk(std::true_type{}, std::true_type{}, std::false_type{});
-          else if (full)
-            chunk(std::false_type{}, std::true_type{}, std::false_type{});
+            chunk(std::false_type{}, std::true_type{});
+          else if (kc + kKC <= 16 * nt)
+            chunk(std::true_type{}, std::false_type{});
           else
-            chunk(std::false_type{}, std::false_type{}, std::false_type{});
+            chunk(std::false_type{}, std::false_type{});
         }
       }
       // The stage buffers are free from here on, except for V rows in flight
@@ -726,7 +634,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
         nit = decode(next);
         ns = setup_of(nit);
         next_setup = true;
-        stage0_of(nit, stages3);
+        stage0_of(nit, stages3, rel_lds);
         next_staged = true;
       }
 
