@@ -59,14 +59,17 @@ constexpr int kKC = 64;            // keys per chunk
 constexpr int kD = 64;             // head dim
 constexpr int kWin = 192;          // relative-table rows per chunk window (>= 191)
 constexpr int kC2PCols = 80;       // per-wave c2p window (<= 79 positions)
-constexpr int kC2PStride = kC2PCols + 4;  // 168-byte rows keep the 8-byte stores aligned
-// Per-wave p2c tile (16 keys x 32 window positions), stored skewed: value
-// (key row kr, position p) at (kr + p) * kP2CSkew + kr.  A score's four keys
-// 4g .. 4g+3 share kr + p = 15 + lc, so its four p2c terms are one aligned
-// 8-byte read; rows of 24 halfs make those reads conflict-free across the
-// wave.
-constexpr int kP2CSkew = 24;
-constexpr int kP2CRows = 47;       // kr + p <= 15 + 31
+// c2p rows of 88 halfs: the 8-byte stores of a wave and its 8-byte gathers
+// (which start at any half) spread over the 64 banks with at most two lanes
+// on one bank per pass.
+constexpr int kC2PStride = 88;
+// Per-wave p2c tile (16 keys x 32 window positions) row-major by key in rows
+// of 40 halfs: a lane's MFMA output (one key, four consecutive positions) is
+// one 8-byte store, and a score's four terms (keys 4g + i at positions
+// 15 + lc - 4g - i) are four 2-byte reads 39 halfs apart; both patterns are
+// conflict-free across the wave at this stride.
+constexpr int kP2TStride = 40;
+constexpr int kP2CRows = 47;       // fp32 chains: kr + p <= 15 + 31
 constexpr int kVRowsA = 448;       // V rows held by one stage buffer (448 x 128 B = 56 KiB)
 
 // LDS map (halfs).  The stage buffers are reused for the V^T chunks and the
@@ -77,11 +80,12 @@ constexpr int kStage = kStageK + 2 * kStageWin;   // 28672 halfs = 56 KiB
 // The kernel-bias and fused chains keep c2p and p2c in fp32 (the Metal
 // kernels never round them): per wave and key tile, c2p [16 queries][33]
 // over the tile's 32 positions (33-float rows spread a wave's gathers over
-// the banks) and p2c skewed as above in rows of 16 floats whose 16-byte block
-// index is XORed with bits 2..3 of the row (a linear-zone read of four p2c
-// terms is one conflict-free 16-byte read).
+// the banks) and p2c skewed, value (key row kr, position p) at row kr + p,
+// column kr, in rows of 16 floats whose 16-byte block index is XORed with
+// bits 2..3 of the row: a score's four keys 4g .. 4g+3 share kr + p =
+// 15 + lc, so its four p2c terms are one conflict-free 16-byte read.
 constexpr int kC2PF32Stride = 33;
-constexpr int kScratchWave16 = 16 * kC2PStride + kP2CRows * kP2CSkew;       // halfs
+constexpr int kScratchWave16 = 16 * kC2PStride + 16 * kP2TStride;           // halfs
 constexpr int kScratchWave32 = (16 * kC2PF32Stride + kP2CRows * 16) * 2;    // halfs
 constexpr int kScratchWave = kScratchWave16 > kScratchWave32 ? kScratchWave16 : kScratchWave32;
 static_assert(16 * 72 <= kScratchWave, "context staging fits a wave's scratch");
@@ -160,7 +164,9 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   __shared__ __attribute__((aligned(1024))) half_t scratch_lds[kWaves * kScratchWave];
   __shared__ int16_t idx_tab[2 * 16 * MAXT];
   __shared__ __attribute__((aligned(16))) float mask_add[16 * MAXT];
-  __shared__ __attribute__((aligned(16))) int key_last[kWaves];  // per wave: last valid key + 1 among its keys, or 0
+  // per wave w (keys 64w .. 64w + 63): last valid key + 1 among its keys, or
+  // 0, plus 1 << 16 when all 64 keys are valid
+  __shared__ __attribute__((aligned(16))) int key_last[kWaves];
 
   // The stage buffers as LDS pointers: the DMA and the transposing reads
   // address them through these (no generic-to-LDS casts of computed pointers).
@@ -177,7 +183,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   const int g = lane >> 4;   // lane group
   const float inv_scale16 = 1.0f / scale16;  // correctly rounded fp32 reciprocal
   half_t* c2p_w = scratch_lds + wave * kScratchWave;
-  half_t* p2c_w = c2p_w + 16 * kC2PStride;
+  half_t* p2c_w = c2p_w + 16 * kC2PStride;  // [16 keys][kP2TStride]
   float* const c2pf = reinterpret_cast<float*>(c2p_w);  // fp32 chains
   float* const p2cf = c2pf + 16 * kC2PF32Stride;
 
@@ -372,12 +378,15 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       // every key: a masked key's bias is fp16(bias - 65504)).  A batch row
       // with no valid key keeps the reference's degenerate softmax over every
       // key (the masked scores themselves, below).  Each wave publishes the
-      // extent of its keys' valid ones; read after chunk 0's barrier.
-      if constexpr (OUT != GD_ATTN_OUT_BIAS) {
+      // extent of its keys' valid ones and whether all 64 are valid (chunk
+      // `wave` then needs no mask term); read after chunk 0's barrier.
+      {
         const uint64_t bal = __ballot(valid);
-        if (lane == 0) key_last[wave] = bal != 0 ? 64 * wave + 64 - __builtin_clzll(bal) : 0;
+        if (lane == 0)
+          key_last[wave] = (bal != 0 ? 64 * wave + 64 - __builtin_clzll(bal) : 0) | (~bal == 0 ? 1 << 16 : 0);
       }
       bool all_masked = false;  // uniform: set after chunk 0's barrier
+      int chunk_valid = 0;      // uniform: bit c set when every key of chunk c is valid
 
       // ---- V for the P.V pass: rows [row_lo, row_hi) of the (b, h) slice
       // land row-major and swizzled like K at rows 0.. of an LDS buffer, by
@@ -399,12 +408,16 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
         if (c >= nchunks) break;  // uniform
         wait_vmcnt<0>();
         __syncthreads();  // stage c landed everywhere; every wave is done with stage c - 1
-        if constexpr (OUT != GD_ATTN_OUT_BIAS) {
-          if (c == 0) {
-            const int4 a0 = *reinterpret_cast<const int4*>(key_last);
-            const int4 a1 = *reinterpret_cast<const int4*>(key_last + 4);
+        if (c == 0) {
+          const int4 a0 = *reinterpret_cast<const int4*>(key_last);
+          const int4 a1 = *reinterpret_cast<const int4*>(key_last + 4);
+          chunk_valid = __builtin_amdgcn_readfirstlane(
+              ((a0.x >> 16) & 1) | ((a0.y >> 15) & 2) | ((a0.z >> 14) & 4) | ((a0.w >> 13) & 8) |
+              ((a1.x >> 12) & 16) | ((a1.y >> 11) & 32) | ((a1.z >> 10) & 64) | ((a1.w >> 9) & 128));
+          if constexpr (OUT != GD_ATTN_OUT_BIAS) {
             const int kext = __builtin_amdgcn_readfirstlane(
-                max(max(max(a0.x, a0.y), max(a0.z, a0.w)), max(max(a1.x, a1.y), max(a1.z, a1.w))));
+                max(max(max(a0.x & 0xffff, a0.y & 0xffff), max(a0.z & 0xffff, a0.w & 0xffff)),
+                    max(max(a1.x & 0xffff, a1.y & 0xffff), max(a1.z & 0xffff, a1.w & 0xffff))));
             all_masked = kext == 0;
             const int klen = all_masked || kext > cur.len ? cur.len : kext;
             nt = live ? (klen + 15) >> 4 : 0;
@@ -428,9 +441,11 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
         // every offset below is closed-form and 16-aligned and the gathers
         // are contiguous.  FULL: all 64 keys of the chunk exist.  ALLM: the
         // item's batch row has no valid key.
-        auto chunk = [&](auto full_c, auto allm_c) {
+        auto chunk = [&](auto full_c, auto allm_c, auto nomask_c) {
           constexpr bool FULL = decltype(full_c)::value;
           constexpr bool ALLM = decltype(allm_c)::value;
+          // NOMASK: every key of the chunk is valid (its mask term is 0)
+          constexpr bool NOMASK = decltype(nomask_c)::value;
           // c2p for this wave's 16 queries and the chunk's keys: window rows
           // [16 wave, 16 wave + 80) (distances qw - kc - 63 .. qw - kc + 16)
           const int crow0 = 16 * wave;
@@ -451,28 +466,33 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
           }
           }
 
-          // Per 16-key tile tt: S^T = K Q^T (scores) and P2C = K . posQ[window]^T
-          // over the 31 window rows [prow0, prow0 + 31) the tile needs (prow0 =
-          // 16 (wave - tt) + 48), stored skewed into p2c_w.  Tiles are
-          // software-pipelined: tile tt's gathers are issued before tile tt+1's
-          // MFMAs and p2c stores (the LDS executes a wave's accesses in order, so
-          // one p2c buffer suffices), and tile tt is combined while those are in
-          // flight.
+          // Per 16-key tile tt: S^T = K Q^T (scores) and P2C over the 32 window
+          // rows [prow0, prow0 + 32) the tile needs (prow0 = 16 (wave - tt) +
+          // 48) into p2c_w.  Tiles are software-pipelined: tile tt's gathers are
+          // issued before tile tt+1's MFMAs and p2c stores (the LDS executes a
+          // wave's accesses in order, so one p2c buffer suffices), and tile tt is
+          // combined while those are in flight.
           float4_t s_t[4];
           half8_t fk[2][2], fq[2][4];  // per tile parity: K rows (chunks g, 4+g), posQ rows (j = 0, 1)
           // Operand fragments of tile tt (LDS reads only; issued a tile ahead).
+          // Tile tt's posQ rows [prow0 + 16, prow0 + 32) are tile tt-1's rows
+          // [prow0', prow0' + 16) (prow0 = prow0' - 16): kept from its fragments.
           auto prep_load = [&](int tt) {
             const int par = tt & 1;
             const int prow0 = 16 * (wave - tt) + 48;
             fk[par][0] = *reinterpret_cast<const half8_t*>(Ks + 16 * tt * kD + swz_lo);
             fk[par][1] = *reinterpret_cast<const half8_t*>(Ks + 16 * tt * kD + swz_hi);
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-              fq[par][2 * j] = *reinterpret_cast<const half8_t*>(PQs + (prow0 + 16 * j) * kD + swz_lo);
-              fq[par][2 * j + 1] = *reinterpret_cast<const half8_t*>(PQs + (prow0 + 16 * j) * kD + swz_hi);
+            fq[par][0] = *reinterpret_cast<const half8_t*>(PQs + prow0 * kD + swz_lo);
+            fq[par][1] = *reinterpret_cast<const half8_t*>(PQs + prow0 * kD + swz_hi);
+            if (tt == 0) {
+              fq[par][2] = *reinterpret_cast<const half8_t*>(PQs + (prow0 + 16) * kD + swz_lo);
+              fq[par][3] = *reinterpret_cast<const half8_t*>(PQs + (prow0 + 16) * kD + swz_hi);
+            } else {
+              fq[par][2] = fq[par ^ 1][0];
+              fq[par][3] = fq[par ^ 1][1];
             }
           };
-          // Scores and p2c of tile tt from its fragments; p2c stored skewed.
+          // Scores and p2c of tile tt from its fragments.
           auto prep_compute = [&](int tt) {
             const int par = tt & 1;
             float4_t sv = {0.f, 0.f, 0.f, 0.f};
@@ -480,22 +500,24 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
             s_t[tt] = mfma16x16x32(fk[par][1], qf1, sv);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-              {
-                float4_t r = {0.f, 0.f, 0.f, 0.f};
+              float4_t r = {0.f, 0.f, 0.f, 0.f};
+              if constexpr (B32) {
+                // P2C = K . posQ^T: lane holds (kr = 4g + i, p = 16 j + lc),
+                // stored at row kr + p, column kr
                 r = mfma16x16x32(fk[par][0], fq[par][2 * j], r);
                 r = mfma16x16x32(fk[par][1], fq[par][2 * j + 1], r);
-                // lane holds (kr = 4g + i, p = 16 j + lc)
-                if constexpr (B32) {
 #pragma unroll
-                  for (int i = 0; i < 4; ++i) {
-                    const int row = 4 * g + i + 16 * j + lc;
-                    p2cf[row * 16 + ((g ^ ((row >> 2) & 3)) << 2) + i] = r[i];
-                  }
-                } else {  // converted in pairs
-                  const half4_t rh = __builtin_convertvector(r, half4_t);
-#pragma unroll
-                  for (int i = 0; i < 4; ++i) p2c_w[(4 * g + i + 16 * j + lc) * kP2CSkew + 4 * g + i] = rh[i];
+                for (int i = 0; i < 4; ++i) {
+                  const int row = 4 * g + i + 16 * j + lc;
+                  p2cf[row * 16 + ((g ^ ((row >> 2) & 3)) << 2) + i] = r[i];
                 }
+              } else {
+                // P2C^T = posQ . K^T: lane holds (p = 16 j + 4g + i, key lc),
+                // one 8-byte store of four fp16 values
+                r = mfma16x16x32(fq[par][2 * j], fk[par][0], r);
+                r = mfma16x16x32(fq[par][2 * j + 1], fk[par][1], r);
+                *reinterpret_cast<half4_t*>(p2c_w + lc * kP2TStride + 16 * j + 4 * g) =
+                    __builtin_convertvector(r, half4_t);
               }
             }
             if constexpr (B32) {
@@ -530,9 +552,10 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
             // Gather the two terms of score (q = qw + lc, k = k0 + 4g + i) at
             // window row q - k - bot: the four c2p terms are consecutive
             // (descending) in the lane's c2p row, at column 63 - 16 tt + lc -
-            // 4 g - i, and the four p2c terms (tile row 15 + lc - 4 g - i) are
-            // one 8-byte read.
-            const float4_t madd = *reinterpret_cast<const float4_t*>(mask_add + k0 + 4 * g);
+            // 4 g - i; the p2c terms are at tile position 15 + lc - 4 g - i of
+            // keys 4 g + i.
+            float4_t madd = {0.f, 0.f, 0.f, 0.f};
+            if constexpr (!NOMASK) madd = *reinterpret_cast<const float4_t*>(mask_add + k0 + 4 * g);
             half4_t c2p, p2c;
             float4_t c2p32, p2c32;
             if constexpr (B32) {
@@ -545,7 +568,9 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
               const half_t* cp = c2p_w + lc * kC2PStride + 63 - 16 * tt + lc - 4 * g;
 #pragma unroll
               for (int i = 0; i < 4; ++i) c2p[i] = cp[-i];
-              p2c = *reinterpret_cast<const half4_t*>(p2c_w + (15 + lc) * kP2CSkew + 4 * g);
+              const half_t* pt = p2c_w + 4 * g * (kP2TStride - 1) + 15 + lc;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) p2c[i] = pt[i * (kP2TStride - 1)];
             }
             wave_lds_sync();  // these gathers precede the next tile's p2c stores
             if (next) prep_compute(tt + 1);
@@ -577,7 +602,8 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
                   v = fmaf(s_t[tt][i], scale_qk, round_f16(round_f16((float)sum16[i] * inv_scale16) - 65504.f));
                 }
               } else if constexpr (SM == kScoreFused) {
-                v = ((s_t[tt][i] + c2p32[i]) + p2c32[i]) * scale_rel + madd[i];
+                v = ((s_t[tt][i] + c2p32[i]) + p2c32[i]) * scale_rel;
+                if constexpr (!NOMASK) v += madd[i];
               } else {
                 float bias16;
                 if constexpr (B32)
@@ -585,6 +611,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
                 else
                   bias16 = round_f16((float)sum16[i] * inv_scale16);
                 if constexpr (OUT == GD_ATTN_OUT_BIAS) {
+                  // (an unmasked key still takes the add: fp16(-0 + 0) = +0)
                   if constexpr (B32)
                     v = madd[i] != 0.f ? -65504.f : bias16;
                   else
@@ -594,9 +621,11 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
                   // rounds like the divide for every fp16 numerator), then the
                   // fp16 add of the bias
                   const float content = round_f16(round_f16(s_t[tt][i]) * inv_scale16);
-                  v = round_f16(content + bias16) + madd[i];
+                  v = round_f16(content + bias16);
+                  if constexpr (!NOMASK) v += madd[i];
                 } else {
-                  v = fmaf(s_t[tt][i], scale_qk, bias16) + madd[i];
+                  v = fmaf(s_t[tt][i], scale_qk, bias16);
+                  if constexpr (!NOMASK) v += madd[i];
                 }
               }
               sc[T][i] = v;
@@ -606,11 +635,13 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
         };
         if (active) {
           if (all_masked)
-            chunk(std::false_type{}, std::true_type{});
-          else if (kc + kKC <= 16 * nt)
-            chunk(std::true_type{}, std::false_type{});
+            chunk(std::false_type{}, std::true_type{}, std::false_type{});
+          else if (kc + kKC > 16 * nt)
+            chunk(std::false_type{}, std::false_type{}, std::false_type{});
+          else if ((chunk_valid >> c) & 1)
+            chunk(std::true_type{}, std::false_type{}, std::true_type{});
           else
-            chunk(std::false_type{}, std::false_type{});
+            chunk(std::true_type{}, std::false_type{}, std::false_type{});
         }
       }
       // The stage buffers are free from here on, except for V rows in flight
