@@ -330,7 +330,6 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     const bool has_next = kPersistent && next < n_items;  // uniform
     Item nit = cur;  // decoded once the chunk loop is done
     bool next_staged = false, next_setup = false;
-    Setup ns;  // the next item's set-up reads, once issued
 
     [&]() {
       // Lane-derived values of the item body are computed afresh per item
@@ -631,6 +630,13 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
               sc[T][i] = v;
             }
           }
+          if constexpr (!FULL) {  // key tiles of this chunk past the extent: probability 0
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt)
+              if (4 * c + tt >= nt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sc[4 * c + tt][i] = -INFINITY;
+          }
           wave_lds_sync();  // the last gathers precede the next chunk's c2p / p2c stores
         };
         if (active) {
@@ -663,22 +669,26 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       }
       if (has_next) {  // after every V row; the set-up reads before the stage DMA (see setup_of)
         nit = decode(next);
-        ns = setup_of(nit);
+        cs = setup_of(nit);  // (the item's own set-up values are dead by now)
         next_setup = true;
         stage0_of(nit, stages3, rel_lds);
         next_staged = true;
       }
 
+      // The softmax runs over whole chunks: key tiles of the last chunk past
+      // the extent hold -inf (set by the chunk), tiles of later chunks are
+      // set to probability 0 here.
       float inv_sum = 0.f;
       if (OUT != GD_ATTN_OUT_BIAS) {
         float mx = -INFINITY;
 #pragma unroll
-        for (int T = 0; T < MAXT; ++T)
-          if (T < nt)  // uniform
+        for (int c = 0; c < MAXT / 4; ++c)
+          if (c < nchunks)  // uniform
 #pragma unroll
-            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[T][i]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            for (int T = 4 * c; T < 4 * c + 4; ++T)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[T][i]);
+        mx = rows_max(mx);
         const float mref = mx == -INFINITY ? 0.f : mx;
         constexpr float kLog2e = 1.4426950408889634f;
         // exp(s - m) = 2^(s log2e - m log2e) as one fma per score; the rounding
@@ -686,21 +696,24 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
         const float mref_l2 = mref * kLog2e;
         float sum = 0.f;
 #pragma unroll
-        for (int T = 0; T < MAXT; ++T) {
-          if (T < nt) {  // uniform
+        for (int c = 0; c < MAXT / 4; ++c) {
+          if (c < nchunks) {  // uniform
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const float e = __builtin_amdgcn_exp2f(fmaf(sc[T][i], kLog2e, -mref_l2));  // v_exp_f32; exp2(-inf) = 0
-              sc[T][i] = e;
-              sum += e;
-            }
+            for (int T = 4 * c; T < 4 * c + 4; ++T)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const float e = __builtin_amdgcn_exp2f(fmaf(sc[T][i], kLog2e, -mref_l2));  // v_exp_f32; exp2(-inf) = 0
+                sc[T][i] = e;
+                sum += e;
+              }
           } else {  // past the key extent: probability 0
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sc[T][i] = 0.f;
+            for (int T = 4 * c; T < 4 * c + 4; ++T)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) sc[T][i] = 0.f;
           }
         }
-        sum += __shfl_xor(sum, 16, 64);
-        sum += __shfl_xor(sum, 32, 64);
+        sum = rows_sum(sum);
         inv_sum = sum > 0.f ? 1.0f / sum : 0.f;
         // The context path scales O once at the end instead of every
         // probability, except on the explicit chain, whose P.V multiplies the
@@ -740,11 +753,23 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
               *reinterpret_cast<half4_t*>(rows + lc * rs + 16 * T + 4 * g) = v;
             }
           wave_lds_sync();
-          const int per_row = L / 8;  // 16-byte pieces per row
-          for (int pce = lane; pce < 16 * per_row; pce += 64) {
-            const int r = pce / per_row, cpos = pce - r * per_row;
-            *reinterpret_cast<half8_t*>(out + (((int64_t)b * H + h) * L + qw + r) * L + cpos * 8) =
-                *reinterpret_cast<const half8_t*>(rows + r * rs + cpos * 8);
+          // Pass it covers rows kRowsPass it + lane / kPieces, 16-byte piece
+          // lane % kPieces of each (pieces from L / 8 on are past the row and
+          // not stored; their LDS reads stay in this wave's staging rows).
+          // Every LDS read is issued before the first store.
+          constexpr int kPieces = 2 * MAXT;
+          constexpr int kRowsPass = 64 / kPieces;
+          constexpr int kPasses = 16 / kRowsPass;
+          const int pr = lane / kPieces, cpos = lane % kPieces;
+          half8_t seg[kPasses];
+#pragma unroll
+          for (int it = 0; it < kPasses; ++it)
+            seg[it] = *reinterpret_cast<const half8_t*>(rows + (kRowsPass * it + pr) * rs + cpos * 8);
+          half_t* const orow = out + (((int64_t)b * H + h) * L + qw + pr) * L + cpos * 8;
+          if (cpos < L / 8) {
+#pragma unroll
+            for (int it = 0; it < kPasses; ++it)
+              *reinterpret_cast<half8_t*>(orow + (int64_t)kRowsPass * it * L) = seg[it];
           }
         }
         return;
@@ -853,9 +878,8 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
     }();
 
     if (!has_next) break;
-    if (!next_setup) ns = setup_of(nit);
+    if (!next_setup) cs = setup_of(nit);
     cur = nit;
-    cs = ns;
     item = next;
   }
 }

@@ -114,6 +114,35 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Max and sum over the four 16-lane rows of a wave (lanes l, l ^ 16, l ^ 32,
+// l ^ 48), every lane receiving the result: gfx950's row-swapping permlanes
+// (v_permlane16_swap: odd rows of the first operand <-> even rows of the
+// second; v_permlane32_swap: upper half of the first <-> lower half of the
+// second) give each lane its partner's value in VALU, without an LDS round
+// trip.  The pairs are combined as x_l op x_(l^16), then op x_(l^32): the
+// same operands, in the same order up to commutation, as the two xor
+// shuffles they replace, so the results are bitwise the same.
+__device__ __forceinline__ float rows_max(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                  false, false);
+  const uint32_t a0 = a[0], a1 = a[1];  // (elements extracted before the casts)
+  v = fmaxf(__builtin_bit_cast(float, a0), __builtin_bit_cast(float, a1));
+  const auto b = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                  false, false);
+  const uint32_t b0 = b[0], b1 = b[1];
+  return fmaxf(__builtin_bit_cast(float, b0), __builtin_bit_cast(float, b1));
+}
+__device__ __forceinline__ float rows_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                  false, false);
+  const uint32_t a0 = a[0], a1 = a[1];
+  v = __builtin_bit_cast(float, a0) + __builtin_bit_cast(float, a1);
+  const auto b = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                  false, false);
+  const uint32_t b0 = b[0], b1 = b[1];
+  return __builtin_bit_cast(float, b0) + __builtin_bit_cast(float, b1);
+}
+
 // Orders this wave's LDS writes before its later LDS reads by other lanes of
 // the same wave.  LDS operations of one wavefront execute in issue order, so
 // wavefront-scope fences emit no wait; they only stop the compiler from
