@@ -21,10 +21,10 @@
 // LDS, each lane from its own table row; the XOR swizzle of the 128-byte rows
 // is applied on the global side) into one of two buffers while the other
 // chunk is computed.  Inside a chunk nothing touches global memory:
-//   c2p  per wave: C2P^T = posK[window] . Q^T over <= 80 positions (5 MFMA
+//   c2p  per wave: C2P = Q . posK[window]^T over <= 80 positions (5 MFMA
 //        column tiles, v_mfma_f32_16x16x32_f16), rounded to fp16 (the
 //        reference's c2pRaw) into a per-wave LDS tile;
-//   per 16-key tile: S^T = K Q^T (2 MFMAs) and P2C = K . posQ[window]^T over
+//   per 16-key tile: S^T = K Q^T (2 MFMAs) and P2C^T = posQ[window] . K^T over
 //        <= 31 positions (4 MFMAs), fp16 into a per-wave LDS tile; each score
 //        gathers its two terms by idx and applies the reference rounding
 //        chain fp16(fp16(c2p + p2c) / fp16(sqrt(3D))).
@@ -59,10 +59,13 @@ constexpr int kKC = 64;            // keys per chunk
 constexpr int kD = 64;             // head dim
 constexpr int kWin = 192;          // relative-table rows per chunk window (>= 191)
 constexpr int kC2PCols = 80;       // per-wave c2p window (<= 79 positions)
-// c2p rows of 88 halfs: the 8-byte stores of a wave and its 8-byte gathers
-// (which start at any half) spread over the 64 banks with at most two lanes
-// on one bank per pass.
-constexpr int kC2PStride = 88;
+// Per-wave c2p tile [80 positions][16 queries] in rows of 24 halfs: a lane's
+// MFMA output (one position, four consecutive queries) is one aligned 8-byte
+// store, conflict-free across the wave, and a score's four terms (query lc at
+// positions 63 - 16 tt + lc - 4g - i) are four aligned 2-byte reads with at
+// most two lanes on one bank.  (Rows by query would make the four terms one
+// 8-byte read, but starting at any half: unaligned LDS reads stall.)
+constexpr int kC2PTStride = 24;
 // Per-wave p2c tile (16 keys x 32 window positions) row-major by key in rows
 // of 40 halfs: a lane's MFMA output (one key, four consecutive positions) is
 // one 8-byte store, and a score's four terms (keys 4g + i at positions
@@ -85,7 +88,7 @@ constexpr int kStage = kStageK + 2 * kStageWin;   // 28672 halfs = 56 KiB
 // bits 2..3 of the row: a score's four keys 4g .. 4g+3 share kr + p =
 // 15 + lc, so its four p2c terms are one conflict-free 16-byte read.
 constexpr int kC2PF32Stride = 33;
-constexpr int kScratchWave16 = 16 * kC2PStride + 16 * kP2TStride;           // halfs
+constexpr int kScratchWave16 = kC2PCols * kC2PTStride + 16 * kP2TStride;    // halfs
 constexpr int kScratchWave32 = (16 * kC2PF32Stride + kP2CRows * 16) * 2;    // halfs
 constexpr int kScratchWave = kScratchWave16 > kScratchWave32 ? kScratchWave16 : kScratchWave32;
 static_assert(16 * 72 <= kScratchWave, "context staging fits a wave's scratch");
@@ -183,7 +186,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   const int g = lane >> 4;   // lane group
   const float inv_scale16 = 1.0f / scale16;  // correctly rounded fp32 reciprocal
   half_t* c2p_w = scratch_lds + wave * kScratchWave;
-  half_t* p2c_w = c2p_w + 16 * kC2PStride;  // [16 keys][kP2TStride]
+  half_t* p2c_w = c2p_w + kC2PCols * kC2PTStride;  // [16 keys][kP2TStride]
   float* const c2pf = reinterpret_cast<float*>(c2p_w);  // fp32 chains
   float* const p2cf = c2pf + 16 * kC2PF32Stride;
 
@@ -454,13 +457,12 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
             {
               const half8_t a0 = *reinterpret_cast<const half8_t*>(PKs + (crow0 + 16 * tw) * kD + swz_lo);
               const half8_t a1 = *reinterpret_cast<const half8_t*>(PKs + (crow0 + 16 * tw) * kD + swz_hi);
+              // C2P = Q . posK^T: lane holds (query 4g + i, position 16 tw + lc)
               float4_t r = {0.f, 0.f, 0.f, 0.f};
-              r = mfma16x16x32(a0, qf0, r);
-              r = mfma16x16x32(a1, qf1, r);
-              half4_t hv;
-#pragma unroll
-              for (int i = 0; i < 4; ++i) hv[i] = (half_t)r[i];
-              *reinterpret_cast<half4_t*>(c2p_w + lc * kC2PStride + 16 * tw + 4 * g) = hv;
+              r = mfma16x16x32(qf0, a0, r);
+              r = mfma16x16x32(qf1, a1, r);
+              *reinterpret_cast<half4_t*>(c2p_w + (16 * tw + lc) * kC2PTStride + 4 * g) =
+                  __builtin_convertvector(r, half4_t);
             }
           }
           }
@@ -549,10 +551,9 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
             if (next) prep_load(tt + 1);  // fragment reads overlap this tile's gathers
             wave_lds_sync();  // tile tt's p2c stores (and the chunk's c2p) precede its gathers
             // Gather the two terms of score (q = qw + lc, k = k0 + 4g + i) at
-            // window row q - k - bot: the four c2p terms are consecutive
-            // (descending) in the lane's c2p row, at column 63 - 16 tt + lc -
-            // 4 g - i; the p2c terms are at tile position 15 + lc - 4 g - i of
-            // keys 4 g + i.
+            // window row q - k - bot: the c2p terms at tile position 63 - 16 tt
+            // + lc - 4 g - i of query lc, the p2c terms at tile position 15 + lc
+            // - 4 g - i of keys 4 g + i.
             float4_t madd = {0.f, 0.f, 0.f, 0.f};
             if constexpr (!NOMASK) madd = *reinterpret_cast<const float4_t*>(mask_add + k0 + 4 * g);
             half4_t c2p, p2c;
@@ -564,9 +565,9 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
               const int row = 15 + lc;
               p2c32 = *reinterpret_cast<const float4_t*>(p2cf + row * 16 + ((g ^ ((row >> 2) & 3)) << 2));
             } else {
-              const half_t* cp = c2p_w + lc * kC2PStride + 63 - 16 * tt + lc - 4 * g;
+              const half_t* cp = c2p_w + (63 - 16 * tt + lc - 4 * g) * kC2PTStride + lc;
 #pragma unroll
-              for (int i = 0; i < 4; ++i) c2p[i] = cp[-i];
+              for (int i = 0; i < 4; ++i) c2p[i] = cp[-i * kC2PTStride];
               const half_t* pt = p2c_w + 4 * g * (kP2TStride - 1) + 15 + lc;
 #pragma unroll
               for (int i = 0; i < 4; ++i) p2c[i] = pt[i * (kP2TStride - 1)];
