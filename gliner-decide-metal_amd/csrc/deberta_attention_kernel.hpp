@@ -757,7 +757,9 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
           // Pass it covers rows kRowsPass it + lane / kPieces, 16-byte piece
           // lane % kPieces of each (pieces from L / 8 on are past the row and
           // not stored; their LDS reads stay in this wave's staging rows).
-          // Every LDS read is issued before the first store.
+          // Every LDS read is issued before the first store.  The stores are
+          // non-temporal: the [B, H, L, L] output would otherwise evict the
+          // relative tables, which every item re-reads, from the L2.
           constexpr int kPieces = 2 * MAXT;
           constexpr int kRowsPass = 64 / kPieces;
           constexpr int kPasses = 16 / kRowsPass;
@@ -770,7 +772,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
           if (cpos < L / 8) {
 #pragma unroll
             for (int it = 0; it < kPasses; ++it)
-              *reinterpret_cast<half8_t*>(orow + (int64_t)kRowsPass * it * L) = seg[it];
+              __builtin_nontemporal_store(seg[it], reinterpret_cast<half8_t*>(orow + (int64_t)kRowsPass * it * L));
           }
         }
         return;
