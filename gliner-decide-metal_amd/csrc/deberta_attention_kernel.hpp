@@ -9,18 +9,22 @@
 // looping over items and fetching the next item's first stage while it
 // finishes the current one.  Keys stream through LDS in chunks of 64.  The
 // pairs (q, k) of a chunk have q - k in [bot, bot + 190], bot = q0 - kc - 63,
-// so the stage of a chunk is
+// so a chunk reads
 //     K rows        64 x 128 B
 //     posK window  192 x 128 B   (relative keys, for c2p)
 //     posQ window  192 x 128 B   (relative queries, for p2c)
-// where window row j holds table row idx(bot + j): the stage gathers table
+// where window row j holds table row idx(bot + j): the stages gather table
 // rows through the index table, so inside the window the relative index is
 // the plain distance q - k - bot for every pair, in the log-bucket zone as in
 // the linear one, and every gather below is at a closed-form offset.  The
-// stage is fetched with global_load_lds_dwordx4 (16 B per lane straight into
+// next chunk's window is this one's shifted by 64 distances, so the windows
+// live in two 256-row rings (distance d at ring row (d - q0 + 64) mod 256)
+// and a chunk's stage brings only its K rows (one of two buffers) and the
+// 64 window rows new to it; an item's first stage brings the whole window.
+// Stages go out with global_load_lds_dwordx4 (16 B per lane straight into
 // LDS, each lane from its own table row; the XOR swizzle of the 128-byte rows
-// is applied on the global side) into one of two buffers while the other
-// chunk is computed.  Inside a chunk nothing touches global memory:
+// is applied on the global side) while the chunk before is computed.  Inside
+// a chunk nothing touches global memory:
 //   c2p  per wave: C2P = Q . posK[window]^T over <= 80 positions (5 MFMA
 //        column tiles, v_mfma_f32_16x16x32_f16), rounded to fp16 (the
 //        reference's c2pRaw) into a per-wave LDS tile;
@@ -73,13 +77,19 @@ constexpr int kC2PTStride = 24;
 // conflict-free across the wave at this stride.
 constexpr int kP2TStride = 40;
 constexpr int kP2CRows = 47;       // fp32 chains: kr + p <= 15 + 31
-constexpr int kVRowsA = 448;       // V rows held by one stage buffer (448 x 128 B = 56 KiB)
 
-// LDS map (halfs).  The stage buffers are reused for the V^T chunks and the
-// output staging once the score loop is done.
-constexpr int kStageK = kKC * kD;                 // 4096
-constexpr int kStageWin = kWin * kD;              // 12288
-constexpr int kStage = kStageK + 2 * kStageWin;   // 28672 halfs = 56 KiB
+// LDS map of `stages` (halfs): K buffers 0 and 1, the posK and posQ rings,
+// and the V region (V rows 0 .. 255 for the P.V pass; free otherwise).  After
+// the score loop the rings hold the next item's first stage (persistent
+// workgroups); without a next item they take V rows 256 .. 511.
+constexpr int kKBuf = kKC * kD;                   // 4096: one chunk's K rows
+constexpr int kRingRows = 256;
+constexpr int kRing = kRingRows * kD;             // 16384
+constexpr int kVRowsA = 256;                      // V rows in the V region
+constexpr int kOffPK = 2 * kKBuf;
+constexpr int kOffPQ = kOffPK + kRing;
+constexpr int kOffV = kOffPQ + kRing;
+constexpr int kStagesLen = kOffV + kVRowsA * kD;  // 57344 halfs = 112 KiB
 // The kernel-bias and fused chains keep c2p and p2c in fp32 (the Metal
 // kernels never round them): per wave and key tile, c2p [16 queries][33]
 // over the tile's 32 positions (33-float rows spread a wave's gathers over
@@ -163,7 +173,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   // assembly the compiler does not track, so its reads of a stage never wait
   // for the next stage's loads in flight; the kernel orders them itself
   // (vmcnt + barrier before a stage is read).
-  __shared__ __attribute__((aligned(1024))) half_t stages[2 * kStage];  // stage buffers 0 and 1
+  __shared__ __attribute__((aligned(1024))) half_t stages[kStagesLen];
   __shared__ __attribute__((aligned(1024))) half_t scratch_lds[kWaves * kScratchWave];
   __shared__ int16_t idx_tab[2 * 16 * MAXT];
   __shared__ __attribute__((aligned(16))) float mask_add[16 * MAXT];
@@ -199,28 +209,30 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   // byte offsets from the head's first row (checked by the launcher). ----
   const int blk_row = lane >> 3;
   const int blk_chunk = (lane & 7) ^ (((wave & 1) << 2) | (lane >> 4));
-  // Stage of key chunk kc into buffer st: kStageOps DMA instructions per wave.
-  // idx_of(r) maps a clamped distance to its table row.
-  auto issue_stage = [&](lds_half_t* st, const half_t* Kb, const half_t* PKh, const half_t* PQh, int kc, int bot,
-                         int klim, auto&& idx_of) {
-    int prow[kWin / 8 / kWaves];
+  // Table rows of 8-row block blk of a window starting at distance bot: the
+  // lane's row of each table, into ring rows ring0 + 8 blk .. + 7 (ring0 a
+  // multiple of 64, so the block's swizzle is that of rows 8 blk ..).
+  auto stage_block = [&](const half_t* PKh, const half_t* PQh, int bot, int blk, int ring0, auto&& idx_of) {
+    int r = bot + 8 * blk + blk_row;
+    r = r < -(L - 1) ? -(L - 1) : (r > L - 1 ? L - 1 : r);
+    const int prow = idx_of(r);
+    const int off = (ring0 + 8 * blk) * kD;
+    load_lds16(PKh, (uint32_t)((prow * pksp + blk_chunk * 8) * 2), stages3 + kOffPK + off);
+    load_lds16(PQh, (uint32_t)((prow * pqsp + blk_chunk * 8) * 2), stages3 + kOffPQ + off);
+  };
+  // K rows kc .. kc + 63 into K buffer kb: 8 blocks of 8 rows, one per wave;
+  // rows from klim on repeat row klim - 1.
+  auto stage_k = [&](const half_t* Kb, int kc, int klim, int kb) {
+    int key = kc + wave * 8 + blk_row;
+    key = key < klim ? key : klim - 1;
+    load_lds16(Kb + (int64_t)key * ksl + blk_chunk * 8, stages3 + kb * kKBuf + wave * 512);
+  };
+  // An item's first stage (chunk 0, window distances bot .. bot + 191 at
+  // ring rows 0 .. 191): kStageOps DMA instructions per wave.
+  auto issue_stage0 = [&](const half_t* Kb, const half_t* PKh, const half_t* PQh, int bot, int klim, auto&& idx_of) {
+    stage_k(Kb, 0, klim, 0);
 #pragma unroll
-    for (int j = 0; j < kWin / 8 / kWaves; ++j) {
-      int r = bot + 8 * (wave + kWaves * j) + blk_row;
-      r = r < -(L - 1) ? -(L - 1) : (r > L - 1 ? L - 1 : r);
-      prow[j] = idx_of(r);
-    }
-    {  // K rows: 8 blocks of 8 rows, one per wave; rows from klim on repeat row klim - 1
-      int key = kc + wave * 8 + blk_row;
-      key = key < klim ? key : klim - 1;
-      load_lds16(Kb + (int64_t)key * ksl + blk_chunk * 8, st + wave * 512);
-    }
-#pragma unroll
-    for (int j = 0; j < kWin / 8 / kWaves; ++j) {  // 3 blocks per wave per table
-      const int blk = wave + kWaves * j;
-      load_lds16(PKh, (uint32_t)((prow[j] * pksp + blk_chunk * 8) * 2), st + kStageK + blk * 512);
-      load_lds16(PQh, (uint32_t)((prow[j] * pqsp + blk_chunk * 8) * 2), st + kStageK + kStageWin + blk * 512);
-    }
+    for (int j = 0; j < kWin / 8 / kWaves; ++j) stage_block(PKh, PQh, bot, wave + kWaves * j, 0, idx_of);
   };
   constexpr int kStageOps = 1 + 2 * (kWin / 8 / kWaves);
   // idx(r) computed (the first stage, issued before the LDS index table exists)
@@ -290,9 +302,9 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
                 len > 0 ? len : 1, row0, qlen};
   };
   // First stage of an item (chunk 0: bot = q0 - 63).
-  auto stage0_of = [&](const Item& it, lds_half_t* st, auto&& idx_of) {
-    issue_stage(st, slice_base(K, it.b, it.h, it.row0, ksb, ksh, ksl), PK + (int64_t)it.h * pksh,
-                PQ + (int64_t)it.h * pqsh, 0, it.qt * kQT - (kKC - 1), it.klim, idx_of);
+  auto stage0_of = [&](const Item& it, auto&& idx_of) {
+    issue_stage0(slice_base(K, it.b, it.h, it.row0, ksb, ksh, ksl), PK + (int64_t)it.h * pksh,
+                 PQ + (int64_t)it.h * pqsh, it.qt * kQT - (kKC - 1), it.klim, idx_of);
   };
   // Per-thread set-up reads of an item: its key-mask entry and the Q
   // fragments.
@@ -318,7 +330,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
 
   int item = blockIdx.x;
   Item cur = decode(item);
-  stage0_of(cur, stages3, rel_arith);
+  stage0_of(cur, rel_arith);
   // The index table, the same for every item, is built once.
   const int n_idx = 2 * L - 1;
   const int16_t id0 = t < n_idx ? rel_idx[t - (L - 1) + kRelSpan] : (int16_t)0;
@@ -426,16 +438,23 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
             nchunks = live && nt > 0 ? (nt + 3) >> 2 : 1;
           }
         }
-        half_t* const st = stages + (c & 1) * kStage;
-        lds_half_t* const so = stages3 + ((c + 1) & 1) * kStage;  // free: every wave is done with stage c - 1
+        // Chunk c + 1's stage: its K rows into K buffer (c + 1) & 1 and the 64
+        // window rows new to it (distances bot_(c+1) .. + 63) into ring rows
+        // (192 - 64 c) mod 256 .. + 63, the rows chunk c does not read (every
+        // wave is done with chunk c - 1, which read them last).
         if (c + 1 < nchunks) {
-          issue_stage(so, Kb, PKh, PQh, (c + 1) * kKC, q0 - (c + 1) * kKC - (kKC - 1), klim, rel_lds);
-        } else if constexpr (OUT == GD_ATTN_OUT_CONTEXT) {  // V rows into the free buffer
-          if (!(c & 1) || !has_next) issue_v(so, 0, v_rows() < kVRowsA ? v_rows() : kVRowsA);
+          stage_k(Kb, (c + 1) * kKC, klim, (c + 1) & 1);
+          stage_block(PKh, PQh, q0 - (c + 1) * kKC - (kKC - 1), wave, (kRingRows - kKC * (c + 1)) & (kRingRows - 1),
+                      rel_lds);
+        } else if constexpr (OUT == GD_ATTN_OUT_CONTEXT) {  // V rows into the V region
+          issue_v(stages3 + kOffV, 0, v_rows() < kVRowsA ? v_rows() : kVRowsA);
         }
-        const half_t* Ks = st;
-        const half_t* PKs = st + kStageK;
-        const half_t* PQs = st + kStageK + kStageWin;
+        const half_t* Ks = stages + (c & 1) * kKBuf;
+        const half_t* PKs = stages + kOffPK;
+        const half_t* PQs = stages + kOffPQ;
+        // ring row of chunk c's window row j (16-aligned j: the block's rows
+        // stay contiguous, and its swizzle is that of rows 0 .. 15)
+        auto rr = [&](int j) -> int { return ((j - kKC * c) & (kRingRows - 1)) * kD; };
         const int kc = c * kKC;
         // The chunk's work for this wave, in compile-time variants whose bodies
         // have no branches, so the scheduler can overlap the tiles freely.
@@ -455,8 +474,8 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
 #pragma unroll
           for (int tw = 0; tw < kC2PCols / 16; ++tw) {
             {
-              const half8_t a0 = *reinterpret_cast<const half8_t*>(PKs + (crow0 + 16 * tw) * kD + swz_lo);
-              const half8_t a1 = *reinterpret_cast<const half8_t*>(PKs + (crow0 + 16 * tw) * kD + swz_hi);
+              const half8_t a0 = *reinterpret_cast<const half8_t*>(PKs + rr(crow0 + 16 * tw) + swz_lo);
+              const half8_t a1 = *reinterpret_cast<const half8_t*>(PKs + rr(crow0 + 16 * tw) + swz_hi);
               // C2P = Q . posK^T: lane holds (query 4g + i, position 16 tw + lc)
               float4_t r = {0.f, 0.f, 0.f, 0.f};
               r = mfma16x16x32(qf0, a0, r);
@@ -483,11 +502,11 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
             const int prow0 = 16 * (wave - tt) + 48;
             fk[par][0] = *reinterpret_cast<const half8_t*>(Ks + 16 * tt * kD + swz_lo);
             fk[par][1] = *reinterpret_cast<const half8_t*>(Ks + 16 * tt * kD + swz_hi);
-            fq[par][0] = *reinterpret_cast<const half8_t*>(PQs + prow0 * kD + swz_lo);
-            fq[par][1] = *reinterpret_cast<const half8_t*>(PQs + prow0 * kD + swz_hi);
+            fq[par][0] = *reinterpret_cast<const half8_t*>(PQs + rr(prow0) + swz_lo);
+            fq[par][1] = *reinterpret_cast<const half8_t*>(PQs + rr(prow0) + swz_hi);
             if (tt == 0) {
-              fq[par][2] = *reinterpret_cast<const half8_t*>(PQs + (prow0 + 16) * kD + swz_lo);
-              fq[par][3] = *reinterpret_cast<const half8_t*>(PQs + (prow0 + 16) * kD + swz_hi);
+              fq[par][2] = *reinterpret_cast<const half8_t*>(PQs + rr(prow0 + 16) + swz_lo);
+              fq[par][3] = *reinterpret_cast<const half8_t*>(PQs + rr(prow0 + 16) + swz_hi);
             } else {
               fq[par][2] = fq[par ^ 1][0];
               fq[par][3] = fq[par ^ 1][1];
@@ -528,8 +547,8 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
               const int prow0 = 16 * (wave - tt) + 48;
 #pragma unroll
               for (int j = 0; j < 2; ++j) {
-                const half8_t a0 = *reinterpret_cast<const half8_t*>(PKs + (prow0 + 16 * j) * kD + swz_lo);
-                const half8_t a1 = *reinterpret_cast<const half8_t*>(PKs + (prow0 + 16 * j) * kD + swz_hi);
+                const half8_t a0 = *reinterpret_cast<const half8_t*>(PKs + rr(prow0 + 16 * j) + swz_lo);
+                const half8_t a1 = *reinterpret_cast<const half8_t*>(PKs + rr(prow0 + 16 * j) + swz_hi);
                 float4_t r = {0.f, 0.f, 0.f, 0.f};
                 r = mfma16x16x32(a0, qf0, r);
                 r = mfma16x16x32(a1, qf1, r);
@@ -654,25 +673,21 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       // The stage buffers are free from here on, except for V rows in flight
       // (context; waited for before the P.V pass) and the next item's stage.
       stage_barrier();
-      // Chunk c used buffer c & 1; the next item's first stage goes to buffer
-      // 0 now.  V rows [0, kVRowsA) are in buffer 1, loaded during the last
-      // chunk when that chunk was in buffer 0 and now otherwise, except
-      // without a next item when the last chunk was in buffer 1 (then in
-      // buffer 0, loaded during that chunk); rows from kVRowsA on (no next
-      // item) go to the other buffer now.
-      const bool last_in_1 = ((nchunks - 1) & 1) != 0;
-      const bool v_in_0 = last_in_1 && !has_next;
-      lds_half_t* const v_lo = stages3 + (v_in_0 ? 0 : kStage);  // V rows [0, kVRowsA)
-      lds_half_t* const v_hi = stages3 + (v_in_0 ? kStage : 0);  // V rows [kVRowsA, v_rows)
+      // The next item's first stage goes to K buffer 0 and the rings now.  V
+      // rows [0, kVRowsA) are in the V region (loaded during the last chunk);
+      // rows from kVRowsA on (L > 256: no next item) go to the posK ring now.
+      lds_half_t* const v_lo = stages3 + kOffV;   // V rows [0, kVRowsA)
+      lds_half_t* const v_hi = stages3 + kOffPK;  // V rows [kVRowsA, v_rows)
+      static_assert(MAXT * 16 <= kVRowsA || !kPersistent, "V rows past the V region need the rings");
+      static_assert(MAXT * 16 - kVRowsA <= kRingRows, "V rows fit the V region and one ring");
       if constexpr (OUT == GD_ATTN_OUT_CONTEXT) {
-        if (last_in_1 && has_next) issue_v(v_lo, 0, v_rows() < kVRowsA ? v_rows() : kVRowsA);
         if (MAXT * 16 > kVRowsA && v_rows() > kVRowsA) issue_v(v_hi, kVRowsA, v_rows());  // no next item here
       }
       if (has_next) {  // after every V row; the set-up reads before the stage DMA (see setup_of)
         nit = decode(next);
         cs = setup_of(nit);  // (the item's own set-up values are dead by now)
         next_setup = true;
-        stage0_of(nit, stages3, rel_lds);
+        stage0_of(nit, rel_lds);
         next_staged = true;
       }
 
@@ -729,29 +744,29 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       if (OUT == GD_ATTN_OUT_PROBS || OUT == GD_ATTN_OUT_BIAS) {
         // Stage this wave's 16 rows x L in LDS (rows padded by 16 bytes so the
         // 8-byte column stores of a wave hit distinct banks), then write
-        // 16-byte row segments.  At L <= 256 (where buffer 0 may hold the
-        // next item's stage) waves 0-3 stage in buffer 1, 4-7 in the scratch
-        // buffer; else waves 0-5 in the stage buffers, 6-7 in the scratch
-        // buffer.
+        // 16-byte row segments.  Rows 0-7 and 8-15 of wave w go to 8-row
+        // slots 2w and 2w + 1, which fill the V region (with a next item,
+        // whose first stage occupies K buffer 0 and the rings) or all of
+        // `stages` (without), then the scratch buffer.
         const int rs = L + 8;
-        constexpr int kRowsWave = 16 * (16 * MAXT + 8);
-        static_assert(MAXT > 16 || (4 * kRowsWave <= kStage && 4 * kRowsWave <= kWaves * kScratchWave),
-                      "probability staging");
-        static_assert(3 * kRowsWave <= kStage && 2 * kRowsWave <= kWaves * kScratchWave, "probability staging");
-        half_t* rows;
-        if constexpr (MAXT <= 16)
-          rows = (wave < 4 ? stages + kStage : scratch_lds) + (wave & 3) * kRowsWave;
-        else
-          rows = wave < 6 ? stages + (wave / 3) * kStage + (wave % 3) * kRowsWave
-                          : scratch_lds + (wave - 6) * kRowsWave;
+        constexpr int kSlot = 8 * (16 * MAXT + 8);
+        constexpr int kOffA = kPersistent ? kOffV : 0;
+        constexpr int kSlotsA = (kStagesLen - kOffA) / kSlot;
+        static_assert(kSlotsA + kWaves * kScratchWave / kSlot >= 2 * kWaves, "probability staging");
+        auto slot = [&](int sl) -> half_t* {
+          return sl < kSlotsA ? stages + kOffA + sl * kSlot : scratch_lds + (sl - kSlotsA) * kSlot;
+        };
+        half_t* const rows_lo = slot(2 * wave);      // rows 0-7
+        half_t* const rows_hi = slot(2 * wave + 1);  // rows 8-15
         if (active) {
+          half_t* const wrow = (lc < 8 ? rows_lo : rows_hi) + (lc & 7) * rs + 4 * g;
 #pragma unroll
           for (int T = 0; T < MAXT; ++T)
             if (16 * T < L) {  // tiles past the key extent hold 0 (probabilities) or the bias of every key
               half4_t v;
 #pragma unroll
               for (int i = 0; i < 4; ++i) v[i] = (half_t)sc[T][i];
-              *reinterpret_cast<half4_t*>(rows + lc * rs + 16 * T + 4 * g) = v;
+              *reinterpret_cast<half4_t*>(wrow + 16 * T) = v;
             }
           wave_lds_sync();
           // Pass it covers rows kRowsPass it + lane / kPieces, 16-byte piece
@@ -766,8 +781,9 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
           const int pr = lane / kPieces, cpos = lane % kPieces;
           half8_t seg[kPasses];
 #pragma unroll
-          for (int it = 0; it < kPasses; ++it)
-            seg[it] = *reinterpret_cast<const half8_t*>(rows + (kRowsPass * it + pr) * rs + cpos * 8);
+          for (int it = 0; it < kPasses; ++it)  // rows of pass it: all below 8 or all from 8 on
+            seg[it] = *reinterpret_cast<const half8_t*>((kRowsPass * (it + 1) <= 8 ? rows_lo : rows_hi) +
+                                                        ((kRowsPass * it + pr) & 7) * rs + cpos * 8);
           half_t* const orow = out + (((int64_t)b * H + h) * L + qw + pr) * L + cpos * 8;
           if (cpos < L / 8) {
 #pragma unroll
