@@ -63,19 +63,22 @@ constexpr int kKC = 64;            // keys per chunk
 constexpr int kD = 64;             // head dim
 constexpr int kWin = 192;          // relative-table rows per chunk window (>= 191)
 constexpr int kC2PCols = 80;       // per-wave c2p window (<= 79 positions)
-// Per-wave c2p tile [80 positions][16 queries] in rows of 24 halfs: a lane's
-// MFMA output (one position, four consecutive queries) is one aligned 8-byte
-// store, conflict-free across the wave, and a score's four terms (query lc at
-// positions 63 - 16 tt + lc - 4g - i) are four aligned 2-byte reads with at
-// most two lanes on one bank.  (Rows by query would make the four terms one
-// 8-byte read, but starting at any half: unaligned LDS reads stall.)
-constexpr int kC2PTStride = 24;
-// Per-wave p2c tile (16 keys x 32 window positions) row-major by key in rows
-// of 40 halfs: a lane's MFMA output (one key, four consecutive positions) is
-// one 8-byte store, and a score's four terms (keys 4g + i at positions
-// 15 + lc - 4g - i) are four 2-byte reads 39 halfs apart; both patterns are
-// conflict-free across the wave at this stride.
-constexpr int kP2TStride = 40;
+// Row strides of the per-wave c2p and p2c tiles, chosen against gfx950's LDS
+// as the bank-conflict counter shows it for these patterns: 32 banks of 4
+// bytes, 8-byte accesses served 16 lanes per cycle, 2-byte reads 32 lanes per
+// cycle (two lanes in one dword do not conflict).
+// c2p tile [80 positions][16 queries] in rows of 20 halfs: a lane's MFMA
+// output (one position, four consecutive queries) is one aligned 8-byte
+// store, conflict-free, and a score's four terms (query lc at positions
+// 63 - 16 tt + lc - 4g - i) are four aligned 2-byte reads with at most two
+// lanes on one bank.  (Rows by query would make the four terms one 8-byte
+// read, but starting at any half: unaligned LDS reads stall.)
+constexpr int kC2PTStride = 20;
+// p2c tile (16 keys x 32 window positions) row-major by key in rows of 44
+// halfs: a lane's MFMA output (one key, four consecutive positions) is one
+// 8-byte store, and a score's four terms (keys 4g + i at positions
+// 15 + lc - 4g - i) are four 2-byte reads 43 halfs apart; both conflict-free.
+constexpr int kP2TStride = 44;
 constexpr int kP2CRows = 47;       // fp32 chains: kr + p <= 15 + 31
 
 // LDS map of `stages` (halfs): K buffers 0 and 1, the posK and posQ rings,
