@@ -237,8 +237,10 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(const half_t* __restr
 // waits for its own loads of the next stage, the barrier makes every wave's
 // loads visible and frees this stage's buffer, the buffer is refilled with
 // the step NSTAGE ahead, and slice 0 of the next stage is read under the
-// remaining MFMAs.  The epilogue stages the fp16 tile through the stage
-// buffers and writes 16-byte coalesced row segments.
+// remaining MFMAs.  The MFMAs take W as the A operand, so a lane's
+// accumulators hold four consecutive output columns per group; the epilogue
+// stages the fp16 tile through the stage buffers with one conflict-free
+// 8-byte store per group and writes coalesced 8-byte row pieces.
 // ---------------------------------------------------------------------------
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -374,11 +376,14 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
     for (int j = 0; j < TN; ++j)
       fb[set][j] = *reinterpret_cast<const half8_t*>(st + BM * BK + Lay::offset(wn * WN + j * 32 + lr, 2 * slice + lk));
   };
+  // W rows as the MFMA A operand and A rows as B: lane (lr, lk) of tile (i, j)
+  // accumulates C row i * 32 + lr at columns j * 32 + 8 q + 4 lk + e % 4
+  // (q = e / 4), four consecutive columns per q.
   auto mma = [&](int set) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16(fa[set][i], fb[set][j], acc[i][j]);
+      for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16(fb[set][j], fa[set][i], acc[i][j]);
   };
   // Issue order of a [read slice s+1][MFMAs of slice s] block: MFMAs and
   // fragment reads alternate from the block's start (an MFMA first, so the
@@ -449,9 +454,35 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
   if constexpr (NSTAGE > 4) if (kt + 3 < nk) step(ic<3>{}, kt + 3);
   __syncthreads();  // all waves done reading the stage buffers; every load landed
 
-  constexpr int CHUNKS_PER_ROW = BN / 8;
-  constexpr int ROWS_PER_PASS = NT / CHUNKS_PER_ROW;
-  const int cc = t % CHUNKS_PER_ROW;
+  // ---- epilogue: C tile staged in LDS in rows of BN halfs, 8-byte unit u of
+  // row r at unit u ^ (r & 15): a lane's four consecutive columns are one
+  // 8-byte store and the 16 rows of a wave's store pass land on 16 distinct
+  // units (conflict-free); rows leave as 8-byte pieces, 16 lanes per 128 B.
+  constexpr int UPR = BN / 4;  // 8-byte units per row
+  static_assert(UPR % 16 == 0, "row swizzle stays inside the row");
+  // this lane's unit of tile (j, q) before the swizzle
+  auto unit_of = [&](int j, int q) { return (wn * WN + j * 32) / 4 + 2 * q + lk; };
+  // bias of this lane's columns
+  float bq[TN][4][4];
+  if constexpr (EPI != GD_EPI_NONE) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bq[j][q][e] = (float)bias[tile_n * BN + 4 * unit_of(j, q) + e];
+  }
+  // rows [row0, row0 + nrows) of the tile, staged at `buf(r)`, to global
+  auto store_rows = [&](int row0, int nrows, auto&& buf) {
+#pragma unroll 4
+    for (int idx = t; idx < nrows * UPR; idx += NT) {
+      const int r = idx / UPR, u = idx - r * UPR;
+      const int row = tile_m * BM + row0 + r;
+      if (row < M)
+        *reinterpret_cast<half4_t*>(C + (int64_t)row * ldc + tile_n * BN + 4 * u) =
+            *reinterpret_cast<const half4_t*>(buf(r) + 4 * (u ^ (r & 15)));
+    }
+  };
   if constexpr (GELU_TABLE) {
     // ---- GELU epilogue: table into st1 (and st2), C through st0 in passes ----
     // All of this thread's table pieces are loaded before any is stored, so
@@ -472,16 +503,16 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
     }
     __syncthreads();
     const half_t* tab2 = stage(ic<2 % NSTAGE>{});
-    half_t res[TM][TN][16];
+    half4_t res[TM][TN][4];
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const float b = (float)bias[tile_n * BN + wn * WN + j * 32 + lr];
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+      for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
-          res[i][j][e] = gelu_from_table((half_t)(acc[i][j][e] + b), st1, tab2, (uint32_t)TAB1);
-    }
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            res[i][j][q][e] = gelu_from_table((half_t)(acc[i][j][4 * q + e] + bq[j][q][e]), st1, tab2, (uint32_t)TAB1);
     constexpr int NPASS = (BM + RPA - 1) / RPA;
 #pragma unroll
     for (int pass = 0; pass < NPASS; ++pass) {
@@ -492,19 +523,13 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
 #pragma unroll
           for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int e = 0; e < 16; ++e)
-              st0[(row_lo + i * 32 + 4 * lk + 8 * (e >> 2) + (e & 3)) * BN + wn * WN + j * 32 + lr] = res[i][j][e];
+            for (int q = 0; q < 4; ++q)
+              *reinterpret_cast<half4_t*>(st0 + (row_lo + i * 32 + lr) * BN + 4 * (unit_of(j, q) ^ (lr & 15))) =
+                  res[i][j][q];
       }
       __syncthreads();
-      constexpr int kPassRowsMax = RPA;
-      const int pass_rows = BM - pass * RPA < kPassRowsMax ? BM - pass * RPA : kPassRowsMax;
-#pragma unroll 4
-      for (int r = t / CHUNKS_PER_ROW; r < pass_rows; r += ROWS_PER_PASS) {
-        const int row = tile_m * BM + pass * RPA + r;
-        if (row < M)
-          *reinterpret_cast<half8_t*>(C + (int64_t)row * ldc + tile_n * BN + cc * 8) =
-              *reinterpret_cast<const half8_t*>(st0 + r * BN + cc * 8);
-      }
+      const int pass_rows = BM - pass * RPA < RPA ? BM - pass * RPA : RPA;
+      store_rows(pass * RPA, pass_rows, [&](int r) { return st0 + r * BN; });
       __syncthreads();
     }
     return;
@@ -523,24 +548,20 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int rb = wm * WM + i * 32;  // a 32-row group lies inside one buffer
-    half_t* Cs = rows_of(rb / RPA) + (rb % RPA) * BN;
+    half_t* Cs = rows_of(rb / RPA) + (rb % RPA + lr) * BN;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int cl = wn * WN + j * 32 + lr;
-      const float b = (EPI != GD_EPI_NONE) ? (float)bias[tile_n * BN + cl] : 0.f;
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        Cs[(4 * lk + 8 * (e >> 2) + (e & 3)) * BN + cl] = epilogue<EPI>(acc[i][j][e], b);
-    }
+      for (int q = 0; q < 4; ++q) {
+        half4_t v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[e] = epilogue<EPI>(acc[i][j][4 * q + e], EPI != GD_EPI_NONE ? bq[j][q][e] : 0.f);
+        *reinterpret_cast<half4_t*>(Cs + 4 * (unit_of(j, q) ^ (lr & 15))) = v;
+      }
   }
   __syncthreads();
-#pragma unroll 4
-  for (int r = t / CHUNKS_PER_ROW; r < BM; r += ROWS_PER_PASS) {
-    const int row = tile_m * BM + r;
-    if (row < M)
-      *reinterpret_cast<half8_t*>(C + (int64_t)row * ldc + tile_n * BN + cc * 8) =
-          *reinterpret_cast<const half8_t*>(rows_of(r / RPA) + (r % RPA) * BN + cc * 8);
-  }
+  store_rows(0, BM, [&](int r) { return rows_of(r / RPA) + (r % RPA) * BN; });
 }
 
 template <int BM, int BN, int WAVES_M, int BK, int NSTAGE, int NW = 8>
