@@ -110,6 +110,222 @@ __global__ __launch_bounds__(64) void fused_attention_general_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// The relative bias with general indices on the matrix cores (D = 64, L a
+// multiple of 16).  One workgroup of 4 waves per (b, h, 64 queries, 128
+// keys), wave w owning queries q0 + 16 w .. + 15; 66 KB of LDS, so two
+// workgroups share a CU.  For every pass over 128 positions of the
+// tables: C2P = Q . posK[pass]^T (v_mfma_f32_16x16x32_f16, fp32) into an LDS
+// table [query][position]; then per 16-key block P2C = K . posQ[pass]^T into
+// a table [key][position]; each score takes its two terms from the tables at
+// its indices when they fall in the pass.  The c2p passes run before the p2c
+// passes, so a score accumulates (-0 + c2p) + p2c: the fp32 sum of the two
+// terms, as one addition, whatever pass each came from.  Indices outside
+// [0, P) are clamped, as the per-query kernel does.
+// ---------------------------------------------------------------------------
+constexpr int kGenPass = 128;              // table positions per pass
+constexpr int kGenStride = kGenPass + 4;   // fp32 row stride: float4 stores of 8 lanes hit 32 distinct banks
+
+__device__ __forceinline__ int gen_swz(int row, int chunk) { return row * 64 + ((chunk ^ ((row >> 1) & 7)) << 3); }
+
+constexpr int kGenKeyBlocks = 8;  // 16-key blocks per workgroup (128 keys: 66 KB of LDS, two workgroups per CU)
+
+__global__ __launch_bounds__(256) void relative_bias_general_mfma_kernel(
+    const half_t* __restrict__ q, const half_t* __restrict__ k, const half_t* __restrict__ pos_key,
+    const half_t* __restrict__ pos_query, const int32_t* __restrict__ c2p_idx, const int32_t* __restrict__ p2c_idx,
+    const half_t* __restrict__ key_mask, float scale, int H, int L, int P, half_t* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) float tab[64 * kGenStride];          // C2P [query][position]
+  __shared__ __attribute__((aligned(16))) half_t rows[kGenPass * 64];          // a pass's table rows
+  __shared__ __attribute__((aligned(16))) half_t krows[16 * kGenKeyBlocks * 64];  // the workgroup's K rows
+  // Workgroup -> (b, h, query block qb, key range ky).  Workgroups go to the
+  // 8 XCDs round-robin; with H a multiple of 8, XCD x takes heads
+  // x H / 8 .. (x + 1) H / 8 - 1 only, so its L2 holds just those heads'
+  // index tensors and position tables.
+  const int nqb = (L + 63) / 64, nky = (L / 16 + kGenKeyBlocks - 1) / kGenKeyBlocks;
+  int h, qb, ky, b;
+  {
+    const int w = blockIdx.x;
+    int r;
+    if (H % 8 == 0) {
+      const int hx = H / 8, l = w >> 3;
+      h = (w & 7) * hx + l % hx;
+      r = l / hx;
+    } else {
+      h = w % H;
+      r = w / H;
+    }
+    qb = r % nqb;
+    r /= nqb;
+    ky = r % nky;
+    b = r / nky;
+  }
+  const int bh = b * H + h;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int lc = lane & 15, g = lane >> 4;
+  const int qw = qb * 64 + 16 * wave;  // the wave's first query
+  const bool active = qw < L;          // uniform
+  const int qg = qw + lc;              // this lane's query in the score tile (keys 4 g .. 4 g + 3 of a block)
+  const int kb0 = kGenKeyBlocks * ky;  // first key block of this workgroup
+  const int nkb = L / 16 - kb0 < kGenKeyBlocks ? L / 16 - kb0 : kGenKeyBlocks;
+  constexpr int MAXKB = kGenKeyBlocks;
+  const half_t* qbase = q + (int64_t)bh * L * 64;
+  const half_t* kbase = k + (int64_t)bh * L * 64;
+  const half_t* pkh = pos_key + (int64_t)h * P * 64;
+  const half_t* pqh = pos_query + (int64_t)h * P * 64;
+  const int32_t* c2ph = c2p_idx + (int64_t)h * L * L;
+  const int32_t* p2ch = p2c_idx + (int64_t)h * L * L;
+  const int qr = qg < L ? qg : L - 1;
+  const half8_t qf0 = *reinterpret_cast<const half8_t*>(qbase + (int64_t)qr * 64 + 8 * g);
+  const half8_t qf1 = *reinterpret_cast<const half8_t*>(qbase + (int64_t)qr * 64 + 32 + 8 * g);
+
+  auto clampi = [&](int x) { return x < 0 ? 0 : (x >= P ? P - 1 : x); };
+  // This lane's indices, all loaded up front (one memory latency for the
+  // whole workgroup), clamped and packed two per register: c2p of keys
+  // 16 kb + 4 g + j at query qg, p2c of query qg at those keys.
+  uint32_t c2pk[MAXKB][2], p2ck[MAXKB][2];
+#pragma unroll
+  for (int kb = 0; kb < MAXKB; ++kb) {
+    const bool ok = qg < L && kb < nkb;
+    int4 ci = {0, 0, 0, 0};
+    int pi[4] = {0, 0, 0, 0};
+    if (ok) {
+      ci = *reinterpret_cast<const int4*>(c2ph + (int64_t)qg * L + 16 * (kb0 + kb) + 4 * g);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pi[j] = p2ch[(int64_t)(16 * (kb0 + kb) + 4 * g + j) * L + qg];
+    }
+    c2pk[kb][0] = (uint32_t)clampi(ci.x) | ((uint32_t)clampi(ci.y) << 16);
+    c2pk[kb][1] = (uint32_t)clampi(ci.z) | ((uint32_t)clampi(ci.w) << 16);
+    p2ck[kb][0] = (uint32_t)clampi(pi[0]) | ((uint32_t)clampi(pi[1]) << 16);
+    p2ck[kb][1] = (uint32_t)clampi(pi[2]) | ((uint32_t)clampi(pi[3]) << 16);
+  }
+  auto unpack = [](const uint32_t (&w)[2], int j) -> int { return (int)((w[j >> 1] >> (16 * (j & 1))) & 0xFFFFu); };
+
+  float acc[MAXKB][4];
+#pragma unroll
+  for (int kb = 0; kb < MAXKB; ++kb)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[kb][j] = -0.0f;
+  // the workgroup's K rows (keys 16 kb0 .. + 127, clamped to L - 1) into LDS
+  // (made visible by the first pass's barriers)
+#pragma unroll
+  for (int it = 0; it < 16 * kGenKeyBlocks * 8 / 256; ++it) {
+    const int i = t + 256 * it;
+    const int row = i >> 3, ch = i & 7;
+    const int key = 16 * kb0 + row < L ? 16 * kb0 + row : L - 1;
+    *reinterpret_cast<half8_t*>(krows + gen_swz(row, ch)) =
+        *reinterpret_cast<const half8_t*>(kbase + (int64_t)key * 64 + ch * 8);
+  }
+
+  // Passes 0 .. np - 1 gather c2p (posK rows), np .. 2 np - 1 p2c (posQ rows),
+  // pass p over table rows [128 (p mod np), + 128) (rows past P repeat row
+  // P - 1).  A pass's rows are read into registers during the pass before.
+  const int np = (P + kGenPass - 1) / kGenPass;
+  constexpr int kPieces = kGenPass * 8 / 256;  // 16-byte pieces per thread
+  half8_t pre[kPieces];
+  auto fetch_rows = [&](int pass) {
+    const half_t* src = pass < np ? pkh : pqh;
+    const int base = (pass < np ? pass : pass - np) * kGenPass;
+#pragma unroll
+    for (int it = 0; it < kPieces; ++it) {
+      const int i = t + 256 * it;
+      const int row = i >> 3, ch = i & 7;
+      const int prow = base + row < P ? base + row : P - 1;
+      pre[it] = *reinterpret_cast<const half8_t*>(src + (int64_t)prow * 64 + ch * 8);
+    }
+  };
+  fetch_rows(0);
+  float* const p2c64 = tab;  // p2c passes: P2C of 64 keys [key][kGenStride] in the C2P table's space
+  for (int pass = 0; pass < 2 * np; ++pass) {  // uniform
+    __syncthreads();  // the previous pass is done with `rows` and the tables
+#pragma unroll
+    for (int it = 0; it < kPieces; ++it) {
+      const int i = t + 256 * it;
+      *reinterpret_cast<half8_t*>(rows + gen_swz(i >> 3, i & 7)) = pre[it];
+    }
+    __syncthreads();
+    if (pass + 1 < 2 * np) fetch_rows(pass + 1);  // lands during this pass
+    const int base = (pass < np ? pass : pass - np) * kGenPass;
+    if (pass < np) {
+      // ---- c2p: C2P of this wave's queries, gathered by the wave itself ----
+      if (active) {
+#pragma unroll 4
+        for (int tp = 0; tp < kGenPass / 16; ++tp) {
+          const half8_t a0 = *reinterpret_cast<const half8_t*>(rows + gen_swz(16 * tp + lc, g));
+          const half8_t a1 = *reinterpret_cast<const half8_t*>(rows + gen_swz(16 * tp + lc, 4 + g));
+          float4_t r = {0.f, 0.f, 0.f, 0.f};
+          r = mfma16x16x32(a0, qf0, r);
+          r = mfma16x16x32(a1, qf1, r);  // lane: query lc, positions 16 tp + 4 g + i
+          *reinterpret_cast<float4_t*>(tab + (16 * wave + lc) * kGenStride + 16 * tp + 4 * g) = r;
+        }
+        wave_lds_sync();
+        if (qg < L) {
+#pragma unroll
+          for (int kb = 0; kb < MAXKB; ++kb) {
+            if (kb >= nkb) continue;  // uniform
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int c = unpack(c2pk[kb], j) - base;
+              if ((unsigned)c < (unsigned)kGenPass) acc[kb][j] += tab[(16 * wave + lc) * kGenStride + c];
+            }
+          }
+        }
+      }
+    } else {
+      // ---- p2c: P2C of 64 keys at a time (wave w: key block 4 kg + w) ----
+#pragma unroll
+      for (int kg = 0; kg < MAXKB / 4; ++kg) {
+        if (4 * kg >= nkb) continue;  // uniform
+        {
+          const int kb = 4 * kg + wave;  // rows past nkb hold clamped keys; never read
+          const half8_t kf0 = *reinterpret_cast<const half8_t*>(krows + gen_swz(16 * kb + lc, g));
+          const half8_t kf1 = *reinterpret_cast<const half8_t*>(krows + gen_swz(16 * kb + lc, 4 + g));
+#pragma unroll 4
+          for (int tp = 0; tp < kGenPass / 16; ++tp) {
+            const half8_t a0 = *reinterpret_cast<const half8_t*>(rows + gen_swz(16 * tp + lc, g));
+            const half8_t a1 = *reinterpret_cast<const half8_t*>(rows + gen_swz(16 * tp + lc, 4 + g));
+            float4_t r = {0.f, 0.f, 0.f, 0.f};
+            r = mfma16x16x32(a0, kf0, r);
+            r = mfma16x16x32(a1, kf1, r);  // lane: key lc, positions 16 tp + 4 g + i
+            *reinterpret_cast<float4_t*>(p2c64 + (16 * wave + lc) * kGenStride + 16 * tp + 4 * g) = r;
+          }
+        }
+        __syncthreads();
+        if (active && qg < L) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            if (4 * kg + u >= nkb) continue;  // uniform
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int pp = unpack(p2ck[4 * kg + u], j) - base;
+              if ((unsigned)pp < (unsigned)kGenPass)
+                acc[4 * kg + u][j] += p2c64[(16 * u + 4 * g + j) * kGenStride + pp];
+            }
+          }
+        }
+        __syncthreads();
+      }
+    }
+  }
+  // ---- scores: (c2p + p2c) * scale, masked keys -65504 ----
+  if (active && qg < L) {
+    half_t* orow = out + ((int64_t)bh * L + qg) * L;
+    const half_t* mrow = key_mask + (int64_t)b * L;
+#pragma unroll
+    for (int kb = 0; kb < MAXKB; ++kb) {
+      if (kb >= nkb) continue;
+      half4_t v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = 16 * (kb0 + kb) + 4 * g + j;
+        const float sc = acc[kb][j] * scale;
+        v[j] = (float)mrow[key] < -60000.f ? (half_t)-65504.f : (half_t)sc;
+      }
+      __builtin_nontemporal_store(v, reinterpret_cast<half4_t*>(orow + 16 * (kb0 + kb) + 4 * g));
+    }
+  }
+}
+
 __global__ void relative_index_table_kernel(int32_t* __restrict__ out, int n, int bucket_size, int max_position) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < 2 * n - 1) out[i] = relative_index(i - (n - 1), bucket_size, max_position);
@@ -122,6 +338,16 @@ int launch_relative_bias_general(const void* q, const void* k, const void* pos_k
                                  int64_t H, int64_t L, int64_t D, int64_t P, void* out, int32_t* error_flag,
                                  hipStream_t stream) {
   if (B * H * L == 0) return GD_OK;
+  // Indices travel packed in 16 bits, so the tables hold at most 65536 rows.
+  if (D == 64 && L % 16 == 0 && L <= 512 && P <= 65536 && error_flag == nullptr) {
+    const dim3 grid((unsigned)(B * H * ((L + 63) / 64) * ((L / 16 + kGenKeyBlocks - 1) / kGenKeyBlocks)));
+    hipLaunchKernelGGL(relative_bias_general_mfma_kernel, grid, dim3(256), 0, stream, static_cast<const half_t*>(q),
+                       static_cast<const half_t*>(k), static_cast<const half_t*>(pos_key),
+                       static_cast<const half_t*>(pos_query), c2p, p2c, static_cast<const half_t*>(key_mask), scale,
+                       (int)H, (int)L, (int)P, static_cast<half_t*>(out));
+    GD_LAUNCH_CHECK();
+    return GD_OK;
+  }
   hipLaunchKernelGGL(relative_bias_general_kernel, dim3((unsigned)(B * H * L)), dim3(64), (size_t)D * sizeof(float),
                      stream, static_cast<const half_t*>(q), static_cast<const half_t*>(k),
                      static_cast<const half_t*>(pos_key), static_cast<const half_t*>(pos_query), c2p, p2c,
