@@ -52,7 +52,8 @@ def parse():
     p.add_argument("--kernel-iters", type=int, default=60)
     p.add_argument("--profile-kernel", default=None,
                    choices=["residual_layernorm", "stream_ceiling", "relbias_softmax", "relative_bias", "attention_context", "qkv_proj",
-                            "out_proj", "ffn_up_gelu", "ffn_down"],
+                            "out_proj", "ffn_up_gelu", "ffn_down", "general_relative_bias",
+                            "general_fused_attention"],
                    help="only run this kernel (--kernel-iters launches on rotating buffers) followed by a 256 MiB "
                         "torch copy, for rocprofv3 counter runs; prints the kernel table, no JSON line")
     p.add_argument("--serving", action="store_true",
@@ -110,6 +111,8 @@ def measure_kernels(model_cfg, iters, only=None):
     from gliner_decide.device import stream_handle
     from gliner_decide.fused_kernels import FusedKernels
     from gliner_decide.synthetic import normal16, relbias_inputs
+    import math
+    import numpy as np
 
     fk = FusedKernels()
     lib = N.lib()
@@ -197,6 +200,37 @@ def measure_kernels(model_cfg, iters, only=None):
         out["relative_bias"] = dict(kernel="deberta_attention_kernel<16,BIAS>", shape=[B, H, L, L], us=us,
                                     bytes=nbytes, gbs=nbytes / us / 1e3, bound="hbm", launches_per_step=0)
         del sets
+
+    # the FusedKernels entry points with index tensors (any indices; here the
+    # unbucketed relative positions clip(q - k, -256, 255) + 256 of every head),
+    # B=32 H=16 L=256 P=512: the bias [B,H,L,L], and the whole attention [B,L,H,D]
+    if want("general_relative_bias") or want("general_fused_attention"):
+        P = 512
+        r = torch.arange(L)
+        rel = ((r[:, None] - r[None, :]).clamp(-256, 255) + 256).int()
+        c2p = rel.unsqueeze(0).expand(H, L, L).contiguous().to(dev)
+        p2c = rel.t().unsqueeze(0).expand(H, L, L).contiguous().to(dev)
+        pkh, pqh = pk.contiguous(), pq.contiguous()
+        km = torch.from_numpy(np.where(d["mask"] > 0, 0.0, -65504.0).astype(np.float16)).to(dev)
+        q0 = torch.from_numpy(d["q"]).to(dev)
+        k0 = torch.from_numpy(d["k"]).to(dev)
+        v0 = torch.from_numpy(d["k"][::-1].copy()).to(dev)
+        scale = 1.0 / math.sqrt(3 * D)
+        common = 2 * H * P * D * 2 + 2 * H * L * L * 4 + B * L * 2
+        if want("general_relative_bias"):
+            us = time_launches(lambda s: fk.relative_bias(q0, k0, pkh, pqh, c2p, p2c, km, scale, B, H, L, D, P), [0],
+                               iters)
+            nbytes = 2 * B * H * L * D * 2 + common + B * H * L * L * 2
+            out["general_relative_bias"] = dict(kernel="general_mfma_kernel<false>", shape=[B, H, L, L], us=us,
+                                                bytes=nbytes, gbs=nbytes / us / 1e3, bound="hbm", launches_per_step=0)
+        if want("general_fused_attention"):
+            us = time_launches(lambda s: fk.fused_attention(q0, k0, v0, pkh, pqh, c2p, p2c, km, scale, B, H, L, D, P),
+                               [0], iters)
+            nbytes = 3 * B * H * L * D * 2 + common + B * L * H * D * 2
+            out["general_fused_attention"] = dict(kernel="general_mfma_kernel<true>", shape=[B, H, L, D], us=us,
+                                                  bytes=nbytes, gbs=nbytes / us / 1e3, bound="hbm",
+                                                  launches_per_step=0)
+        del c2p, p2c, q0, k0, v0
 
     # attention as the encoder runs it: context output from the fused QKV layout
     T = B * L

@@ -111,37 +111,56 @@ __global__ __launch_bounds__(64) void fused_attention_general_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// The relative bias with general indices on the matrix cores (D = 64, L a
-// multiple of 16).  One workgroup of 4 waves per (b, h, 64 queries, 128
-// keys), wave w owning queries q0 + 16 w .. + 15; 66 KB of LDS, so two
-// workgroups share a CU.  For every pass over 128 positions of the
-// tables: C2P = Q . posK[pass]^T (v_mfma_f32_16x16x32_f16, fp32) into an LDS
-// table [query][position]; then per 16-key block P2C = K . posQ[pass]^T into
-// a table [key][position]; each score takes its two terms from the tables at
-// its indices when they fall in the pass.  The c2p passes run before the p2c
-// passes, so a score accumulates (-0 + c2p) + p2c: the fp32 sum of the two
-// terms, as one addition, whatever pass each came from.  Indices outside
-// [0, P) are clamped, as the per-query kernel does.
+// The general-index kernels on the matrix cores (D = 64, L a multiple of 16,
+// L <= 512, P <= 65536).  A workgroup of 4 waves owns (b, h, 64 queries),
+// wave w queries q0 + 16 w .. + 15, and takes the keys in blocks of 128: the
+// relative bias gives each key block a workgroup of its own, the fused
+// attention walks all of them.  66 KB of LDS, so two workgroups share a CU.
+// For a key block, every pass over 128 positions of the tables computes
+// C2P = Q . posK[pass]^T (v_mfma_f32_16x16x32_f16, fp32) into an LDS table
+// [query][position], or per 16-key block P2C = K . posQ[pass]^T into a table
+// [key][position]; each score takes its two terms from the tables at its
+// indices when they fall in the pass.  The c2p passes run before the p2c
+// passes, so a score accumulates (x + c2p) + p2c, x = -0 for the bias and
+// x = q.k for the fused attention: the reference's fp32 sum, term by term,
+// whatever pass a term came from.  Indices outside [0, P) are clamped, as the
+// per-query kernels do.
+//
+// Fused attention: scores (x + c2p + p2c) * scale (masked keys -65504) feed
+// an online softmax per query row (running max seeded at -65504, the
+// reference's seed), and P . V runs on the matrix cores with P split into
+// fp16 hi + lo (V rows in LDS, read transposed by ds_read_b64_tr_b16); the
+// output row is divided by the row's sum at the end.
 // ---------------------------------------------------------------------------
 constexpr int kGenPass = 128;              // table positions per pass
 constexpr int kGenStride = kGenPass + 4;   // fp32 row stride: float4 stores of 8 lanes hit 32 distinct banks
+// Column kGenPass of every table row holds -0, the term of a position outside
+// the pass (x + -0 = x for every fp32 x, signed zeros included).
+__device__ __forceinline__ int gen_col(int c) { return (unsigned)c < (unsigned)kGenPass ? c : kGenPass; }
+constexpr int kGenKeyBlocks = 8;           // 16-key blocks per key block (128 keys)
+
+typedef __attribute__((address_space(3))) void gen_lds_void_t;
+typedef __attribute__((address_space(3))) half_t gen_lds_half_t;
+typedef short gen_short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) gen_short4_t gen_lds_short4_t;
 
 __device__ __forceinline__ int gen_swz(int row, int chunk) { return row * 64 + ((chunk ^ ((row >> 1) & 7)) << 3); }
 
-constexpr int kGenKeyBlocks = 8;  // 16-key blocks per workgroup (128 keys: 66 KB of LDS, two workgroups per CU)
-
-__global__ __launch_bounds__(256) void relative_bias_general_mfma_kernel(
-    const half_t* __restrict__ q, const half_t* __restrict__ k, const half_t* __restrict__ pos_key,
-    const half_t* __restrict__ pos_query, const int32_t* __restrict__ c2p_idx, const int32_t* __restrict__ p2c_idx,
-    const half_t* __restrict__ key_mask, float scale, int H, int L, int P, half_t* __restrict__ out) {
+template <bool FUSED>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void general_mfma_kernel(
+    const half_t* __restrict__ q, const half_t* __restrict__ k, const half_t* __restrict__ v,
+    const half_t* __restrict__ pos_key, const half_t* __restrict__ pos_query, const int32_t* __restrict__ c2p_idx,
+    const int32_t* __restrict__ p2c_idx, const half_t* __restrict__ key_mask, float scale, int H, int L, int P,
+    half_t* __restrict__ out) {
   __shared__ __attribute__((aligned(16))) float tab[64 * kGenStride];          // C2P [query][position]
-  __shared__ __attribute__((aligned(16))) half_t rows[kGenPass * 64];          // a pass's table rows
-  __shared__ __attribute__((aligned(16))) half_t krows[16 * kGenKeyBlocks * 64];  // the workgroup's K rows
-  // Workgroup -> (b, h, query block qb, key range ky).  Workgroups go to the
-  // 8 XCDs round-robin; with H a multiple of 8, XCD x takes heads
-  // x H / 8 .. (x + 1) H / 8 - 1 only, so its L2 holds just those heads'
-  // index tensors and position tables.
+  __shared__ __attribute__((aligned(16))) half_t rows[kGenPass * 64];          // a pass's table rows (fused: V rows)
+  __shared__ __attribute__((aligned(16))) half_t krows[16 * kGenKeyBlocks * 64];  // the key block's K rows
+  // Workgroup -> (b, h, query block qb, key block ky; the fused kernel takes
+  // every key block).  Workgroups go to the 8 XCDs round-robin; with H a
+  // multiple of 8, XCD x takes heads x H / 8 .. (x + 1) H / 8 - 1 only, so
+  // its L2 holds just those heads' index tensors and position tables.
   const int nqb = (L + 63) / 64, nky = (L / 16 + kGenKeyBlocks - 1) / kGenKeyBlocks;
+  const int nky_wg = FUSED ? 1 : nky;
   int h, qb, ky, b;
   {
     const int w = blockIdx.x;
@@ -156,8 +175,8 @@ __global__ __launch_bounds__(256) void relative_bias_general_mfma_kernel(
     }
     qb = r % nqb;
     r /= nqb;
-    ky = r % nky;
-    b = r / nky;
+    ky = r % nky_wg;
+    b = r / nky_wg;
   }
   const int bh = b * H + h;
   const int t = threadIdx.x, lane = t & 63;
@@ -166,8 +185,6 @@ __global__ __launch_bounds__(256) void relative_bias_general_mfma_kernel(
   const int qw = qb * 64 + 16 * wave;  // the wave's first query
   const bool active = qw < L;          // uniform
   const int qg = qw + lc;              // this lane's query in the score tile (keys 4 g .. 4 g + 3 of a block)
-  const int kb0 = kGenKeyBlocks * ky;  // first key block of this workgroup
-  const int nkb = L / 16 - kb0 < kGenKeyBlocks ? L / 16 - kb0 : kGenKeyBlocks;
   constexpr int MAXKB = kGenKeyBlocks;
   const half_t* qbase = q + (int64_t)bh * L * 64;
   const half_t* kbase = k + (int64_t)bh * L * 64;
@@ -175,153 +192,287 @@ __global__ __launch_bounds__(256) void relative_bias_general_mfma_kernel(
   const half_t* pqh = pos_query + (int64_t)h * P * 64;
   const int32_t* c2ph = c2p_idx + (int64_t)h * L * L;
   const int32_t* p2ch = p2c_idx + (int64_t)h * L * L;
+  const half_t* mrow = key_mask + (int64_t)b * L;
   const int qr = qg < L ? qg : L - 1;
   const half8_t qf0 = *reinterpret_cast<const half8_t*>(qbase + (int64_t)qr * 64 + 8 * g);
   const half8_t qf1 = *reinterpret_cast<const half8_t*>(qbase + (int64_t)qr * 64 + 32 + 8 * g);
-
   auto clampi = [&](int x) { return x < 0 ? 0 : (x >= P ? P - 1 : x); };
-  // This lane's indices, all loaded up front (one memory latency for the
-  // whole workgroup), clamped and packed two per register: c2p of keys
-  // 16 kb + 4 g + j at query qg, p2c of query qg at those keys.
-  uint32_t c2pk[MAXKB][2], p2ck[MAXKB][2];
-#pragma unroll
-  for (int kb = 0; kb < MAXKB; ++kb) {
-    const bool ok = qg < L && kb < nkb;
-    int4 ci = {0, 0, 0, 0};
-    int pi[4] = {0, 0, 0, 0};
-    if (ok) {
-      ci = *reinterpret_cast<const int4*>(c2ph + (int64_t)qg * L + 16 * (kb0 + kb) + 4 * g);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) pi[j] = p2ch[(int64_t)(16 * (kb0 + kb) + 4 * g + j) * L + qg];
-    }
-    c2pk[kb][0] = (uint32_t)clampi(ci.x) | ((uint32_t)clampi(ci.y) << 16);
-    c2pk[kb][1] = (uint32_t)clampi(ci.z) | ((uint32_t)clampi(ci.w) << 16);
-    p2ck[kb][0] = (uint32_t)clampi(pi[0]) | ((uint32_t)clampi(pi[1]) << 16);
-    p2ck[kb][1] = (uint32_t)clampi(pi[2]) | ((uint32_t)clampi(pi[3]) << 16);
-  }
   auto unpack = [](const uint32_t (&w)[2], int j) -> int { return (int)((w[j >> 1] >> (16 * (j & 1))) & 0xFFFFu); };
 
-  float acc[MAXKB][4];
-#pragma unroll
-  for (int kb = 0; kb < MAXKB; ++kb)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[kb][j] = -0.0f;
-  // the workgroup's K rows (keys 16 kb0 .. + 127, clamped to L - 1) into LDS
-  // (made visible by the first pass's barriers)
-#pragma unroll
-  for (int it = 0; it < 16 * kGenKeyBlocks * 8 / 256; ++it) {
-    const int i = t + 256 * it;
-    const int row = i >> 3, ch = i & 7;
-    const int key = 16 * kb0 + row < L ? 16 * kb0 + row : L - 1;
-    *reinterpret_cast<half8_t*>(krows + gen_swz(row, ch)) =
-        *reinterpret_cast<const half8_t*>(kbase + (int64_t)key * 64 + ch * 8);
-  }
-
-  // Passes 0 .. np - 1 gather c2p (posK rows), np .. 2 np - 1 p2c (posQ rows),
-  // pass p over table rows [128 (p mod np), + 128) (rows past P repeat row
-  // P - 1).  A pass's rows are read into registers during the pass before.
+  // Steps of a key block: 0 .. np - 1 gather c2p (posK rows), np .. 2 np - 1
+  // p2c (posQ rows), step p over table rows [128 (p mod np), + 128) (rows
+  // past P repeat row P - 1); the fused kernel's step 2 np brings the key
+  // block's V rows.  A step's rows are read into registers during the step
+  // before (the first step of a key block repeats the first step of every
+  // key block, so it is fetched once up front and again during the V step).
   const int np = (P + kGenPass - 1) / kGenPass;
+  const int nsteps = 2 * np + (FUSED ? 1 : 0);
   constexpr int kPieces = kGenPass * 8 / 256;  // 16-byte pieces per thread
   half8_t pre[kPieces];
-  auto fetch_rows = [&](int pass) {
-    const half_t* src = pass < np ? pkh : pqh;
-    const int base = (pass < np ? pass : pass - np) * kGenPass;
+  auto fetch_rows = [&](int step, int ky_) {
 #pragma unroll
     for (int it = 0; it < kPieces; ++it) {
       const int i = t + 256 * it;
       const int row = i >> 3, ch = i & 7;
-      const int prow = base + row < P ? base + row : P - 1;
-      pre[it] = *reinterpret_cast<const half8_t*>(src + (int64_t)prow * 64 + ch * 8);
+      if (step < 2 * np) {
+        const int prow0 = (step < np ? step : step - np) * kGenPass + row;
+        const half_t* src = (step < np ? pkh : pqh) + (int64_t)(prow0 < P ? prow0 : P - 1) * 64;
+        pre[it] = *reinterpret_cast<const half8_t*>(src + ch * 8);
+      } else {
+        // V rows of keys past L are zeros (their probabilities are 0 too)
+        const int key = 16 * kGenKeyBlocks * ky_ + row;
+        pre[it] = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
+        if (key < L) pre[it] = *reinterpret_cast<const half8_t*>(v + ((int64_t)bh * L + key) * 64 + ch * 8);
+      }
     }
   };
-  fetch_rows(0);
-  float* const p2c64 = tab;  // p2c passes: P2C of 64 keys [key][kGenStride] in the C2P table's space
-  for (int pass = 0; pass < 2 * np; ++pass) {  // uniform
-    __syncthreads();  // the previous pass is done with `rows` and the tables
+
+  // fused: running max (per query row, the same in the row's four lanes),
+  // this lane's part of the row sum, and O^T (lane: query lc, d 16 dt + 4 g + i)
+  float m_run = -65504.f, l_run = 0.f;
+  float4_t o[4];
 #pragma unroll
-    for (int it = 0; it < kPieces; ++it) {
-      const int i = t + 256 * it;
-      *reinterpret_cast<half8_t*>(rows + gen_swz(i >> 3, i & 7)) = pre[it];
+  for (int dt = 0; dt < 4; ++dt) o[dt] = (float4_t){0.f, 0.f, 0.f, 0.f};
+
+  if (t < 64) tab[t * kGenStride + kGenPass] = -0.0f;  // visible after the first step's barriers
+  fetch_rows(0, 0);
+  for (int kyi = 0; kyi < (FUSED ? nky : 1); ++kyi) {  // uniform
+    const int kyb = FUSED ? kyi : ky;
+    const int kb0 = kGenKeyBlocks * kyb;  // first 16-key block of this key block
+    const int nkb = L / 16 - kb0 < kGenKeyBlocks ? L / 16 - kb0 : kGenKeyBlocks;
+    // This lane's indices, clamped and packed two per register: c2p of keys
+    // 16 kb + 4 g + j at query qg, p2c of query qg at those keys.
+    uint32_t c2pk[MAXKB][2], p2ck[MAXKB][2];
+#pragma unroll
+    for (int kb = 0; kb < MAXKB; ++kb) {
+      const bool ok = qg < L && kb < nkb;
+      int4 ci = {0, 0, 0, 0};
+      int pi[4] = {0, 0, 0, 0};
+      if (ok) {
+        ci = *reinterpret_cast<const int4*>(c2ph + (int64_t)qg * L + 16 * (kb0 + kb) + 4 * g);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pi[j] = p2ch[(int64_t)(16 * (kb0 + kb) + 4 * g + j) * L + qg];
+      }
+      c2pk[kb][0] = (uint32_t)clampi(ci.x) | ((uint32_t)clampi(ci.y) << 16);
+      c2pk[kb][1] = (uint32_t)clampi(ci.z) | ((uint32_t)clampi(ci.w) << 16);
+      p2ck[kb][0] = (uint32_t)clampi(pi[0]) | ((uint32_t)clampi(pi[1]) << 16);
+      p2ck[kb][1] = (uint32_t)clampi(pi[2]) | ((uint32_t)clampi(pi[3]) << 16);
     }
-    __syncthreads();
-    if (pass + 1 < 2 * np) fetch_rows(pass + 1);  // lands during this pass
-    const int base = (pass < np ? pass : pass - np) * kGenPass;
-    if (pass < np) {
-      // ---- c2p: C2P of this wave's queries, gathered by the wave itself ----
-      if (active) {
-#pragma unroll 4
-        for (int tp = 0; tp < kGenPass / 16; ++tp) {
-          const half8_t a0 = *reinterpret_cast<const half8_t*>(rows + gen_swz(16 * tp + lc, g));
-          const half8_t a1 = *reinterpret_cast<const half8_t*>(rows + gen_swz(16 * tp + lc, 4 + g));
-          float4_t r = {0.f, 0.f, 0.f, 0.f};
-          r = mfma16x16x32(a0, qf0, r);
-          r = mfma16x16x32(a1, qf1, r);  // lane: query lc, positions 16 tp + 4 g + i
-          *reinterpret_cast<float4_t*>(tab + (16 * wave + lc) * kGenStride + 16 * tp + 4 * g) = r;
-        }
-        wave_lds_sync();
-        if (qg < L) {
+    // The key block's K rows (clamped to L - 1) into LDS.  The previous key
+    // block's last reads of krows came before its V step's barriers.
 #pragma unroll
-          for (int kb = 0; kb < MAXKB; ++kb) {
-            if (kb >= nkb) continue;  // uniform
+    for (int it = 0; it < 16 * kGenKeyBlocks * 8 / 256; ++it) {
+      const int i = t + 256 * it;
+      const int row = i >> 3, ch = i & 7;
+      const int key = 16 * kb0 + row < L ? 16 * kb0 + row : L - 1;
+      *reinterpret_cast<half8_t*>(krows + gen_swz(row, ch)) =
+          *reinterpret_cast<const half8_t*>(kbase + (int64_t)key * 64 + ch * 8);
+    }
+    float acc[MAXKB][4];
+    if constexpr (FUSED) {
+      __syncthreads();  // K rows visible
+      // q.k of this wave's queries (lane: query lc, keys 16 kb + 4 g + i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const int c = unpack(c2pk[kb], j) - base;
-              if ((unsigned)c < (unsigned)kGenPass) acc[kb][j] += tab[(16 * wave + lc) * kGenStride + c];
-            }
-          }
-        }
+      for (int kb = 0; kb < MAXKB; ++kb) {
+        const half8_t kf0 = *reinterpret_cast<const half8_t*>(krows + gen_swz(16 * kb + lc, g));
+        const half8_t kf1 = *reinterpret_cast<const half8_t*>(krows + gen_swz(16 * kb + lc, 4 + g));
+        float4_t r = {0.f, 0.f, 0.f, 0.f};
+        r = mfma16x16x32(kf0, qf0, r);
+        r = mfma16x16x32(kf1, qf1, r);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[kb][j] = r[j];
       }
     } else {
-      // ---- p2c: P2C of 64 keys at a time (wave w: key block 4 kg + w) ----
 #pragma unroll
-      for (int kg = 0; kg < MAXKB / 4; ++kg) {
-        if (4 * kg >= nkb) continue;  // uniform
-        {
-          const int kb = 4 * kg + wave;  // rows past nkb hold clamped keys; never read
-          const half8_t kf0 = *reinterpret_cast<const half8_t*>(krows + gen_swz(16 * kb + lc, g));
-          const half8_t kf1 = *reinterpret_cast<const half8_t*>(krows + gen_swz(16 * kb + lc, 4 + g));
+      for (int kb = 0; kb < MAXKB; ++kb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[kb][j] = -0.0f;
+    }
+
+    float* const p2c64 = tab;  // p2c steps: P2C of 64 keys [key][kGenStride] in the C2P table's space
+    for (int step = 0; step < 2 * np; ++step) {  // uniform
+      __syncthreads();  // the previous step is done with `rows` and the tables
+#pragma unroll
+      for (int it = 0; it < kPieces; ++it) {
+        const int i = t + 256 * it;
+        *reinterpret_cast<half8_t*>(rows + gen_swz(i >> 3, i & 7)) = pre[it];
+      }
+      __syncthreads();
+      if (step + 1 < nsteps) fetch_rows(step + 1, kyb);  // lands during this step
+      const int base = (step < np ? step : step - np) * kGenPass;
+      if (step < np) {
+        // ---- c2p: C2P of this wave's queries, gathered by the wave itself ----
+        if (active) {
 #pragma unroll 4
           for (int tp = 0; tp < kGenPass / 16; ++tp) {
             const half8_t a0 = *reinterpret_cast<const half8_t*>(rows + gen_swz(16 * tp + lc, g));
             const half8_t a1 = *reinterpret_cast<const half8_t*>(rows + gen_swz(16 * tp + lc, 4 + g));
             float4_t r = {0.f, 0.f, 0.f, 0.f};
-            r = mfma16x16x32(a0, kf0, r);
-            r = mfma16x16x32(a1, kf1, r);  // lane: key lc, positions 16 tp + 4 g + i
-            *reinterpret_cast<float4_t*>(p2c64 + (16 * wave + lc) * kGenStride + 16 * tp + 4 * g) = r;
+            r = mfma16x16x32(a0, qf0, r);
+            r = mfma16x16x32(a1, qf1, r);  // lane: query lc, positions 16 tp + 4 g + i
+            *reinterpret_cast<float4_t*>(tab + (16 * wave + lc) * kGenStride + 16 * tp + 4 * g) = r;
           }
+          wave_lds_sync();
+          // Every score gathers a term; one whose position lies outside this
+          // pass reads the row's -0 column, which leaves the sum unchanged.
+          // (Blocks past nkb gather too, at index 0: their scores are never used.)
+          const float* const trow = tab + (16 * wave + lc) * kGenStride;
+#pragma unroll
+          for (int kb = 0; kb < MAXKB; ++kb)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[kb][j] += trow[gen_col(unpack(c2pk[kb], j) - base)];
         }
-        __syncthreads();
-        if (active && qg < L) {
+      } else {
+        // ---- p2c: P2C of 64 keys at a time (wave w: key block 4 kg + w) ----
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            if (4 * kg + u >= nkb) continue;  // uniform
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const int pp = unpack(p2ck[4 * kg + u], j) - base;
-              if ((unsigned)pp < (unsigned)kGenPass)
-                acc[4 * kg + u][j] += p2c64[(16 * u + 4 * g + j) * kGenStride + pp];
+        for (int kg = 0; kg < MAXKB / 4; ++kg) {
+          if (4 * kg >= nkb) continue;  // uniform
+          {
+            const int kb = 4 * kg + wave;  // rows past nkb hold clamped keys; never read
+            const half8_t kf0 = *reinterpret_cast<const half8_t*>(krows + gen_swz(16 * kb + lc, g));
+            const half8_t kf1 = *reinterpret_cast<const half8_t*>(krows + gen_swz(16 * kb + lc, 4 + g));
+#pragma unroll 4
+            for (int tp = 0; tp < kGenPass / 16; ++tp) {
+              const half8_t a0 = *reinterpret_cast<const half8_t*>(rows + gen_swz(16 * tp + lc, g));
+              const half8_t a1 = *reinterpret_cast<const half8_t*>(rows + gen_swz(16 * tp + lc, 4 + g));
+              float4_t r = {0.f, 0.f, 0.f, 0.f};
+              r = mfma16x16x32(a0, kf0, r);
+              r = mfma16x16x32(a1, kf1, r);  // lane: key lc, positions 16 tp + 4 g + i
+              *reinterpret_cast<float4_t*>(p2c64 + (16 * wave + lc) * kGenStride + 16 * tp + 4 * g) = r;
             }
           }
+          __syncthreads();
+          if (active) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+              for (int j = 0; j < 4; ++j)
+                acc[4 * kg + u][j] += p2c64[(16 * u + 4 * g + j) * kGenStride + gen_col(unpack(p2ck[4 * kg + u], j) - base)];
+          }
+          __syncthreads();
         }
-        __syncthreads();
       }
     }
-  }
-  // ---- scores: (c2p + p2c) * scale, masked keys -65504 ----
-  if (active && qg < L) {
-    half_t* orow = out + ((int64_t)bh * L + qg) * L;
-    const half_t* mrow = key_mask + (int64_t)b * L;
+
+    if constexpr (!FUSED) {
+      // ---- scores: (c2p + p2c) * scale, masked keys -65504 ----
+      if (active && qg < L) {
+        half_t* orow = out + ((int64_t)bh * L + qg) * L;
 #pragma unroll
-    for (int kb = 0; kb < MAXKB; ++kb) {
-      if (kb >= nkb) continue;
-      half4_t v;
+        for (int kb = 0; kb < MAXKB; ++kb) {
+          if (kb >= nkb) continue;
+          half4_t sv;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int key = 16 * (kb0 + kb) + 4 * g + j;
-        const float sc = acc[kb][j] * scale;
-        v[j] = (float)mrow[key] < -60000.f ? (half_t)-65504.f : (half_t)sc;
+          for (int j = 0; j < 4; ++j) {
+            const int key = 16 * (kb0 + kb) + 4 * g + j;
+            const float sc = acc[kb][j] * scale;
+            sv[j] = (float)mrow[key] < -60000.f ? (half_t)-65504.f : (half_t)sc;
+          }
+          __builtin_nontemporal_store(sv, reinterpret_cast<half4_t*>(orow + 16 * (kb0 + kb) + 4 * g));
+        }
       }
-      __builtin_nontemporal_store(v, reinterpret_cast<half4_t*>(orow + 16 * (kb0 + kb) + 4 * g));
+    } else {
+      // ---- online softmax over this key block, then P . V ----
+      constexpr float kLog2e = 1.4426950408889634f;
+      float bmax = m_run;
+#pragma unroll
+      for (int kb = 0; kb < MAXKB; ++kb) {
+        if (kb >= nkb) continue;  // uniform
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int key = 16 * (kb0 + kb) + 4 * g + j;
+          const float sc = (float)mrow[key] < -60000.f ? -65504.f : acc[kb][j] * scale;
+          acc[kb][j] = sc;
+          bmax = fmaxf(bmax, sc);
+        }
+      }
+      bmax = rows_max(bmax);
+      // exp(s - m) = 2^(s log2e - m log2e); the rounding of m log2e scales a
+      // whole row alike and cancels in the normalisation.
+      const float alpha = __builtin_amdgcn_exp2f(m_run * kLog2e - bmax * kLog2e);
+      m_run = bmax;
+      const float m_l2 = bmax * kLog2e;
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+#pragma unroll
+      for (int kb = 0; kb < MAXKB; ++kb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float e = kb < nkb ? __builtin_amdgcn_exp2f(fmaf(acc[kb][j], kLog2e, -m_l2)) : 0.f;
+          acc[kb][j] = e;
+          l_run += e;
+        }
+      // V step: the key block's V rows into `rows` (every wave's p2c reads
+      // of `rows` ended at the last step's closing barrier)
+#pragma unroll
+      for (int it = 0; it < kPieces; ++it) {
+        const int i = t + 256 * it;
+        *reinterpret_cast<half8_t*>(rows + gen_swz(i >> 3, i & 7)) = pre[it];
+      }
+      __syncthreads();
+      if (kyi + 1 < nky) fetch_rows(0, 0);  // the next key block's first step
+      if (active) {
+        // ds_read_b64_tr_b16: in each 16-lane group, source lane s names 4
+        // consecutive halfs and lane j receives element j % 4 of source lanes
+        // j / 4, 4 + j / 4, 8 + j / 4, 12 + j / 4.  Source lane lc of group g
+        // names V[16 T + 4 g + lc / 4][16 dt + 4 (lc % 4) ..], so lane (g, lc)
+        // receives V[16 T + 4 g + i][16 dt + lc], i = 0..3 (from 16 rows on,
+        // tile T + 1): with V as the A operand and P^T as the B operand the
+        // product lane holds O[query lc][16 dt + 4 g + i].  The swizzle term
+        // (row >> 1) & 7 of those rows is (2 g + lc / 8) & 7.
+        gen_lds_half_t* const rows3 = (gen_lds_half_t*)(gen_lds_void_t*)rows;
+        const int tr_sw = (2 * g + (lc >> 3)) & 7;
+        const int tr_lane = (4 * g + (lc >> 2)) * 64 + 4 * (lc & 1);
+        const int tr_c = (lc >> 1) & 1;
+#pragma unroll
+        for (int T = 0; T < MAXKB; T += 2) {
+          if (T >= nkb) continue;  // uniform; a tile T + 1 past nkb has P = 0 and zero V rows
+          half8_t pa, pl;
+#pragma unroll
+          for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int i = 0; i < 4; i += 2) {
+              const float x0 = acc[T + u][i], x1 = acc[T + u][i + 1];
+              const half2_t hi = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(x0, x1));
+              pa[4 * u + i] = hi[0];
+              pa[4 * u + i + 1] = hi[1];
+              pl[4 * u + i] = (half_t)(x0 - (float)hi[0]);
+              pl[4 * u + i + 1] = (half_t)(x1 - (float)hi[1]);
+            }
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) {
+            const gen_lds_half_t* a = rows3 + 16 * T * 64 + tr_lane + (((2 * dt + tr_c) ^ tr_sw) << 3);
+            const gen_short4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((gen_lds_short4_t*)a);
+            const gen_short4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((gen_lds_short4_t*)(a + 16 * 64));
+            const half4_t h0 = __builtin_bit_cast(half4_t, v0), h1 = __builtin_bit_cast(half4_t, v1);
+            half8_t vb;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              vb[i] = h0[i];
+              vb[4 + i] = h1[i];
+            }
+            o[dt] = mfma16x16x32(vb, pa, o[dt]);
+            o[dt] = mfma16x16x32(vb, pl, o[dt]);
+          }
+        }
+      }
+      // the next key block writes krows and `rows` only after its own
+      // barriers; this one's V reads end before the next step's first barrier
+      __syncthreads();
+    }
+  }
+  if constexpr (FUSED) {
+    if (active && qg < L) {
+      const float inv = 1.0f / rows_sum(l_run);
+      half_t* orow = out + (((int64_t)b * L + qg) * H + h) * 64;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        half4_t ov;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ov[i] = (half_t)(o[dt][i] * inv);
+        *reinterpret_cast<half4_t*>(orow + 16 * dt + 4 * g) = ov;
+      }
     }
   }
 }
@@ -341,8 +492,8 @@ int launch_relative_bias_general(const void* q, const void* k, const void* pos_k
   // Indices travel packed in 16 bits, so the tables hold at most 65536 rows.
   if (D == 64 && L % 16 == 0 && L <= 512 && P <= 65536 && error_flag == nullptr) {
     const dim3 grid((unsigned)(B * H * ((L + 63) / 64) * ((L / 16 + kGenKeyBlocks - 1) / kGenKeyBlocks)));
-    hipLaunchKernelGGL(relative_bias_general_mfma_kernel, grid, dim3(256), 0, stream, static_cast<const half_t*>(q),
-                       static_cast<const half_t*>(k), static_cast<const half_t*>(pos_key),
+    hipLaunchKernelGGL(general_mfma_kernel<false>, grid, dim3(256), 0, stream, static_cast<const half_t*>(q),
+                       static_cast<const half_t*>(k), nullptr, static_cast<const half_t*>(pos_key),
                        static_cast<const half_t*>(pos_query), c2p, p2c, static_cast<const half_t*>(key_mask), scale,
                        (int)H, (int)L, (int)P, static_cast<half_t*>(out));
     GD_LAUNCH_CHECK();
@@ -362,6 +513,17 @@ int launch_fused_attention_general(const void* q, const void* k, const void* v, 
                                    float scale, int64_t B, int64_t H, int64_t L, int64_t D, int64_t P, void* out,
                                    int32_t* error_flag, hipStream_t stream) {
   if (B * H * L == 0) return GD_OK;
+  // Indices travel packed in 16 bits, so the tables hold at most 65536 rows.
+  if (D == 64 && L % 16 == 0 && L <= 512 && P <= 65536 && error_flag == nullptr) {
+    const dim3 grid((unsigned)(B * H * ((L + 63) / 64)));
+    hipLaunchKernelGGL(general_mfma_kernel<true>, grid, dim3(256), 0, stream, static_cast<const half_t*>(q),
+                       static_cast<const half_t*>(k), static_cast<const half_t*>(v),
+                       static_cast<const half_t*>(pos_key), static_cast<const half_t*>(pos_query), c2p, p2c,
+                       static_cast<const half_t*>(key_mask), scale, (int)H, (int)L, (int)P,
+                       static_cast<half_t*>(out));
+    GD_LAUNCH_CHECK();
+    return GD_OK;
+  }
   hipLaunchKernelGGL(fused_attention_general_kernel, dim3((unsigned)(B * H * L)), dim3(64),
                      (size_t)(D + L) * sizeof(float), stream, static_cast<const half_t*>(q),
                      static_cast<const half_t*>(k), static_cast<const half_t*>(v), static_cast<const half_t*>(pos_key),

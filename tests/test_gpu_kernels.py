@@ -565,6 +565,67 @@ def test_fused_attention_closed_form_indices(L):
     assert np.max(np.abs(got - want)) <= 2e-3
 
 
+@pytest.mark.parametrize("L,P,H", [(32, 512, 2), (144, 300, 2), (256, 512, 8), (512, 512, 1)])
+def test_general_index_kernels_random_indices(L, P, H):
+    """gd_relative_bias and gd_fused_attention with arbitrary index tensors
+    (the matrix-core kernels: D = 64, L a multiple of 16) against the
+    oracle's restatement of the Metal kernels.  Per-head random indices;
+    L = 144 leaves a partial key block (one 16-key block) and a query block
+    with one active wave, P = 300 a partial table pass; the last batch row
+    has every key masked (the reference's uniform softmax over -65504)."""
+    B = 3
+    r = np.random.default_rng(900 + L)
+    q, k, v = (r.standard_normal((B, H, L, 64)).astype(np.float16) for _ in range(3))
+    pkh, pqh = (r.standard_normal((H, P, 64)).astype(np.float16) for _ in range(2))
+    c2p = r.integers(0, P, size=(H, L, L)).astype(np.int32)
+    p2c = r.integers(0, P, size=(H, L, L)).astype(np.int32)
+    lengths = np.array([L, max(1, L // 3), 0])
+    key_mask = np.where(np.arange(L)[None, :] < lengths[:, None], 0.0, -65504.0).astype(np.float16)
+    scale = O.scale_f32(64)
+    want = O.relative_bias_kernel(q, k, pkh, pqh, c2p, p2c, key_mask, scale)
+    got = host(fk().relative_bias(dev(q), dev(k), dev(pkh), dev(pqh), dev(c2p), dev(p2c), dev(key_mask), scale, B, H,
+                                  L, 64, P))
+    masked = np.broadcast_to(key_mask[:, None, None, :] < -60000, got.shape)
+    assert np.all(got[masked] == -65504.0)
+    acc = 4.0 * 8.0 * 2.0 ** -24 * O.relative_bias_kernel(np.abs(q), np.abs(k), np.abs(pkh), np.abs(pqh), c2p, p2c,
+                                                            np.zeros_like(key_mask), scale, round16=False)
+    err = np.abs(got - want)[~masked]
+    bound = (np.maximum(ulp16(got), ulp16(want)) + acc)[~masked]
+    assert np.all(err <= bound + 1e-12), (err - bound).max()
+    want = O.fused_attention_kernel(q, k, v, pkh, pqh, c2p, p2c, key_mask, scale)
+    got = host(fk().fused_attention(dev(q), dev(k), dev(v), dev(pkh), dev(pqh), dev(c2p), dev(p2c), dev(key_mask),
+                                    scale, B, H, L, 64, P))
+    assert got.shape == (B, L, H, 64)
+    assert np.max(np.abs(got - want)) <= 2e-3
+    # the fully masked row: the plain mean of V over every key
+    np.testing.assert_allclose(got[2], np.broadcast_to(v[2].astype(np.float64).mean(axis=1)[None], (L, H, 64)),
+                               atol=2e-3)
+
+
+def test_general_index_kernels_clamp_out_of_range_indices():
+    """Indices outside [0, P) read the nearest table row (the per-query
+    kernels' rule, kept by the matrix-core kernels)."""
+    B, H, L, P = 2, 2, 64, 200
+    r = np.random.default_rng(77)
+    q, k, v = (r.standard_normal((B, H, L, 64)).astype(np.float16) for _ in range(3))
+    pkh, pqh = (r.standard_normal((H, P, 64)).astype(np.float16) for _ in range(2))
+    c2p = r.integers(-40, P + 40, size=(H, L, L)).astype(np.int32)
+    p2c = r.integers(-40, P + 40, size=(H, L, L)).astype(np.int32)
+    key_mask = np.zeros((B, L), np.float16)
+    scale = O.scale_f32(64)
+    c2pc, p2cc = np.clip(c2p, 0, P - 1), np.clip(p2c, 0, P - 1)
+    want = O.relative_bias_kernel(q, k, pkh, pqh, c2pc, p2cc, key_mask, scale)
+    got = host(fk().relative_bias(dev(q), dev(k), dev(pkh), dev(pqh), dev(c2p), dev(p2c), dev(key_mask), scale, B, H,
+                                  L, 64, P))
+    acc = 4.0 * 8.0 * 2.0 ** -24 * O.relative_bias_kernel(np.abs(q), np.abs(k), np.abs(pkh), np.abs(pqh), c2pc, p2cc,
+                                                            key_mask, scale, round16=False)
+    assert np.all(np.abs(got - want) <= np.maximum(ulp16(got), ulp16(want)) + acc + 1e-12)
+    want = O.fused_attention_kernel(q, k, v, pkh, pqh, c2pc, p2cc, key_mask, scale)
+    got = host(fk().fused_attention(dev(q), dev(k), dev(v), dev(pkh), dev(pqh), dev(c2p), dev(p2c), dev(key_mask),
+                                    scale, B, H, L, 64, P))
+    assert np.max(np.abs(got - want)) <= 2e-3
+
+
 def test_attention_rejects_bias_output_on_chains_without_a_bias():
     from gliner_decide import GlinerDecideError
     q, k, v, pk, pq, mask = _attn_case(7, 1, 1, 32)
