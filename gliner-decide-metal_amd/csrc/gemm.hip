@@ -294,15 +294,17 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
   static_assert(S % 2 == 0, "fragment sets alternate per slice");
   static_assert(NSTAGE >= 2 && NSTAGE <= 5, "pipeline depth");
   static_assert(NSTAGE * STAGE * 2 <= 160 * 1024, "LDS budget");
-  static_assert(RPA % 32 == 0 && NSTAGE * RPA >= BM, "epilogue staging must fit in the stage buffers");
+  static_assert(RPA % 32 == 0 && (EPI == GD_EPI_BIAS_GELU || NSTAGE * RPA >= BM),
+                "epilogue staging must fit in the stage buffers");
   static_assert((NSTAGE - 1) * LPS < 64, "vmcnt range");
 
   // The GELU epilogue reads the correctly rounded table from LDS: with two
   // stages st1 is sized for all of it; with more, its first STAGE entries go
   // to st1 and the rest to st2.  C then goes through st0 in passes of RPA
   // rows, each wave's WM rows inside one pass.
-  constexpr bool GELU_TABLE = EPI == GD_EPI_BIAS_GELU && RPA % WM == 0 &&
+  constexpr bool GELU_TABLE = EPI == GD_EPI_BIAS_GELU && (RPA % WM == 0 || WAVES_M * 32 <= RPA) &&
                               (NSTAGE == 2 || 2 * STAGE >= kGeluEntries);
+  static_assert(EPI != GD_EPI_BIAS_GELU || GELU_TABLE || NSTAGE * RPA >= BM, "GELU epilogue staging");
   constexpr int TAB1 = NSTAGE == 2 || kGeluEntries <= STAGE ? kGeluEntries : STAGE;  // entries in st1
   __shared__ __attribute__((aligned(1024))) half_t st0[STAGE];
   __shared__ __attribute__((aligned(1024)))
@@ -335,27 +337,29 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int lr = lane & 31, lk = lane >> 5;
 
-  // Source pointers of this lane's 16-byte pieces (fixed across K).
-  const half_t* a_src[A_BLK];
-  const half_t* b_src[B_BLK];
+  // Element offsets of this lane's 16-byte pieces from A and W (fixed across
+  // K), 32-bit: the launchers keep both operands within 2^31 elements, so a
+  // piece is addressed as the uniform base plus one VGPR.
+  uint32_t a_off[A_BLK], b_off[B_BLK];
 #pragma unroll
   for (int j = 0; j < A_BLK; ++j) {
     const int blk = wave * A_BLK + j;
     int m = tile_m * BM + blk * Lay::kRowsPerBlock + lane / Lay::kChunks;
     m = m < M ? m : M - 1;
-    a_src[j] = A + (int64_t)m * lda + Lay::dma_chunk(lane, blk) * 8;
+    a_off[j] = (uint32_t)((int64_t)m * lda + Lay::dma_chunk(lane, blk) * 8);
   }
 #pragma unroll
   for (int j = 0; j < B_BLK; ++j) {
     const int blk = wave * B_BLK + j;
     const int n = tile_n * BN + blk * Lay::kRowsPerBlock + lane / Lay::kChunks;
-    b_src[j] = W + (int64_t)n * K + Lay::dma_chunk(lane, blk) * 8;
+    b_off[j] = (uint32_t)((int64_t)n * K + Lay::dma_chunk(lane, blk) * 8);
   }
   auto issue = [&](half_t* st, int k0) {
 #pragma unroll
-    for (int j = 0; j < A_BLK; ++j) load_lds16(a_src[j] + k0, st + (wave * A_BLK + j) * 512);
+    for (int j = 0; j < A_BLK; ++j) load_lds16(A + (a_off[j] + (uint32_t)k0), st + (wave * A_BLK + j) * 512);
 #pragma unroll
-    for (int j = 0; j < B_BLK; ++j) load_lds16(b_src[j] + k0, st + BM * BK + (wave * B_BLK + j) * 512);
+    for (int j = 0; j < B_BLK; ++j)
+      load_lds16(W + (b_off[j] + (uint32_t)k0), st + BM * BK + (wave * B_BLK + j) * 512);
   };
 
   float16_t acc[TM][TN];
@@ -368,13 +372,19 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
 
   // Fragment sets: fa[set][i] = A rows of MFMA tile i, fb[set][j] = W rows of tile j.
   half8_t fa[2][TM], fb[2][TN];
+  // Every fragment row is wm * WM + i * 32 + lr (or wn * WN + j * 32 + lr),
+  // congruent to lr modulo 16, so its swizzle term is the lane's own and
+  // Lay::offset(row, 2 s + lk) = row_base * BK + (lane_off ^ 16 s): one lane
+  // offset per operand, fragments apart by constants, slices by an XOR.
+  static_assert(BK == 64 && WM % 16 == 0 && WN % 16 == 0, "fragment address form");
+  const int lane_off = lr * BK + 8 * (lk ^ ((lr >> 1) & 1)) + 16 * ((lr >> 2) & 3);
+  const int a_frag0 = wm * WM * BK, b_frag0 = BM * BK + wn * WN * BK;
   auto read_frags = [&](const half_t* st, int slice, int set) {
+    const int lo = lane_off ^ (16 * slice);
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
-      fa[set][i] = *reinterpret_cast<const half8_t*>(st + Lay::offset(wm * WM + i * 32 + lr, 2 * slice + lk));
+    for (int i = 0; i < TM; ++i) fa[set][i] = *reinterpret_cast<const half8_t*>(st + a_frag0 + i * 32 * BK + lo);
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
-      fb[set][j] = *reinterpret_cast<const half8_t*>(st + BM * BK + Lay::offset(wn * WN + j * 32 + lr, 2 * slice + lk));
+    for (int j = 0; j < TN; ++j) fb[set][j] = *reinterpret_cast<const half8_t*>(st + b_frag0 + j * 32 * BK + lo);
   };
   // W rows as the MFMA A operand and A rows as B: lane (lr, lk) of tile (i, j)
   // accumulates C row i * 32 + lr at columns j * 32 + 8 q + 4 lk + e % 4
@@ -503,34 +513,57 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
     }
     __syncthreads();
     const half_t* tab2 = stage(ic<2 % NSTAGE>{});
-    half4_t res[TM][TN][4];
+    auto gelu_of = [&](int i, int j, int q) {
+      half4_t r;
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+      for (int e = 0; e < 4; ++e)
+        r[e] = gelu_from_table((half_t)(acc[i][j][4 * q + e] + bq[j][q][e]), st1, tab2, (uint32_t)TAB1);
+      return r;
+    };
+    if constexpr (RPA % WM == 0) {
+      half4_t res[TM][TN][4];
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            res[i][j][q][e] = gelu_from_table((half_t)(acc[i][j][4 * q + e] + bq[j][q][e]), st1, tab2, (uint32_t)TAB1);
-    constexpr int NPASS = (BM + RPA - 1) / RPA;
+          for (int q = 0; q < 4; ++q) res[i][j][q] = gelu_of(i, j, q);
+      constexpr int NPASS = (BM + RPA - 1) / RPA;
 #pragma unroll
-    for (int pass = 0; pass < NPASS; ++pass) {
-      const int row_lo = wm * WM - pass * RPA;  // this wave's first row within the pass
-      if (row_lo >= 0 && row_lo < RPA) {
+      for (int pass = 0; pass < NPASS; ++pass) {
+        const int row_lo = wm * WM - pass * RPA;  // this wave's first row within the pass
+        if (row_lo >= 0 && row_lo < RPA) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+          for (int i = 0; i < TM; ++i)
 #pragma unroll
-          for (int j = 0; j < TN; ++j)
+            for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-              *reinterpret_cast<half4_t*>(st0 + (row_lo + i * 32 + lr) * BN + 4 * (unit_of(j, q) ^ (lr & 15))) =
-                  res[i][j][q];
+              for (int q = 0; q < 4; ++q)
+                *reinterpret_cast<half4_t*>(st0 + (row_lo + i * 32 + lr) * BN + 4 * (unit_of(j, q) ^ (lr & 15))) =
+                    res[i][j][q];
+        }
+        __syncthreads();
+        const int pass_rows = BM - pass * RPA < RPA ? BM - pass * RPA : RPA;
+        store_rows(pass * RPA, pass_rows, [&](int r) { return st0 + r * BN; });
+        __syncthreads();
       }
-      __syncthreads();
-      const int pass_rows = BM - pass * RPA < RPA ? BM - pass * RPA : RPA;
-      store_rows(pass * RPA, pass_rows, [&](int r) { return st0 + r * BN; });
-      __syncthreads();
+    } else {
+      // A wave's rows do not fit one pass (320-row tiles): pass i takes the
+      // i-th 32-row group of every wave row, WAVES_M x 32 rows through st0,
+      // its GELU evaluated in the pass.
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<half4_t*>(st0 + (wm * 32 + lr) * BN + 4 * (unit_of(j, q) ^ (lr & 15))) = gelu_of(i, j, q);
+        __syncthreads();
+#pragma unroll
+        for (int g = 0; g < WAVES_M; ++g)
+          store_rows(g * WM + i * 32, 32, [&](int r) { return st0 + (g * 32 + r) * BN; });
+        __syncthreads();
+      }
     }
     return;
   }
@@ -580,6 +613,18 @@ int launch_lds_tile(const half_t* A, const half_t* W, const half_t* bias, half_t
     default: GD_LDS_GEMM(GD_EPI_BIAS_RELU); break;
   }
 #undef GD_LDS_GEMM
+  GD_LAUNCH_CHECK();
+  return GD_OK;
+}
+
+// 320 x 256 tiles (two 64-deep stages, 144 KiB), GELU epilogue only: one
+// round over up to 320 rows per tile row where 256-row tiles need a second.
+int launch_lds_tile_gelu320(const half_t* A, const half_t* W, const half_t* bias, half_t* C, int M, int N, int K,
+                            int64_t lda, int64_t ldc, hipStream_t stream) {
+  const int tiles_m = (M + 319) / 320;
+  const int tiles_n = N / 256;
+  hipLaunchKernelGGL((gemm_nt_lds_kernel<320, 256, 2, 64, 2, GD_EPI_BIAS_GELU, 8>), dim3(tiles_m * tiles_n), dim3(512),
+                     0, stream, A, W, bias, C, M, N, K, lda, ldc, tiles_m, tiles_n);
   GD_LAUNCH_CHECK();
   return GD_OK;
 }
@@ -686,14 +731,23 @@ int launch_linear(const void* a, const void* w, const void* bias, void* c, int64
     if (M >= 1024) return launch_tile<128, 128, true>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
     return launch_tile<64, 128, true>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
   }
+  // The DMA tile kernels address A and W by 32-bit element offsets; larger
+  // operands take the register-staged kernel (same accumulation order).
+  if ((int64_t)(M - 1) * lda + K >= (int64_t{1} << 31) || (int64_t)N * K >= (int64_t{1} << 31))
+    return launch_tile<128, 128, false>(A, Wt, Bv, Cm, M, N, K, lda, ldc, nullptr, 0, epilogue_kind, stream);
   if (M >= 2048 && N % 256 == 0) {
     // Whole rounds of 256 x 256 tiles (one tile per CU) over the first rows
     // and, when the rows left over fit one round of 128 x 128 tiles, those in
     // a second launch: a last round of a few large tiles is slower than one
-    // of many small ones (FFN-up at 4,896 rows: 44 + 18.5 us against 71.5 us).
-    // Both kernels accumulate in the same order and read the GELU table.
+    // of many small ones (FFN-up at 4,896 rows: 44 + 18.5 us against 71.5 us;
+    // with GELU, one round of 320 x 256 tiles: 55.5 us).  Every kernel
+    // accumulates in the same order and reads the GELU table.
     const int64_t cus = gemm_cu_count();
     const int64_t m_tiles_round = cus / (N / 256);
+    // GELU (FFN-up) on up to 320 rows per tile row: one round of 320 x 256
+    // tiles where 256 x 256 tiles would need a second (FFN-up at 4,896 rows).
+    if (epilogue_kind == GD_EPI_BIAS_GELU && M > m_tiles_round * 256 && M <= m_tiles_round * 320 && K % 64 == 0)
+      return launch_lds_tile_gelu320(A, Wt, Bv, Cm, M, N, K, lda, ldc, stream);
     const int64_t full_rows = m_tiles_round > 0 ? M / (m_tiles_round * 256) * (m_tiles_round * 256) : 0;
     const int64_t rest = M - full_rows;
     if (full_rows > 0 && rest > 0 && (rest + 127) / 128 * (N / 128) <= cus) {

@@ -182,12 +182,13 @@ def check_linear(out, x, w, b, epi):
 @pytest.mark.parametrize("epi,n", [("bias", 4096), ("gelu", 4096), ("bias", 1024)])
 def test_linear_rows_do_not_depend_on_m(epi, n):
     """Every GEMM kernel accumulates an element over the same K slices in the
-    same order and rounds it the same way: the first rows of a 4096-row
-    product (256 x 256 tiles at N = 4096, 192 x 128 at N = 1024) equal, bit
-    for bit, the same rows computed alone (160 rows: the 64 x 64 tiles;
-    1500: 128 x 128 tiles at N = 4096, 64 x 64 at N = 1024)."""
+    same order and rounds it the same way: the first rows of an 8192-row
+    product (256 x 256 tiles at N = 4096, 256-row tiles at N = 1024) equal,
+    bit for bit, the same rows computed alone (160 rows: the 64 x 64 tiles;
+    1500: 128 x 128 tiles at N = 4096, 64 x 64 at N = 1024; 4896: 320 x 256
+    tiles with GELU, 256 x 256 + 128 x 128 without, 192 x 128 at N = 1024)."""
     r = np.random.default_rng(21)
-    x = r.standard_normal((4096, 1024)).astype(np.float16)
+    x = r.standard_normal((8192, 1024)).astype(np.float16)
     w = (r.standard_normal((n, 1024)) / 32).astype(np.float16)
     b = r.standard_normal(n).astype(np.float16)
     def bits(t):
@@ -195,7 +196,7 @@ def test_linear_rows_do_not_depend_on_m(epi, n):
         return t.cpu().numpy().view(np.uint16)
 
     full = bits(fk().linear(dev(x), dev(w), dev(b), epilogue=epi))
-    for m in (160, 1500):
+    for m in (160, 1500, 4896):
         np.testing.assert_array_equal(bits(fk().linear(dev(x[:m]), dev(w), dev(b), epilogue=epi)), full[:m])
 
 
@@ -220,7 +221,7 @@ def _ordered16(a):
 def test_gelu_epilogue_every_fp16_input(m, n):
     """x @ I^T + 0 reproduces x exactly, so the GELU epilogue sees every finite
     fp16 value once (63488 = 248 x 256).  Every kernel (the small-M tiles at
-    M = 248, 256x128 at M = 2048 and 4896, 256x256 at 8192) reads the
+    M = 248, 256x128 at M = 2048, 320x256 at 4896, 256x256 at 8192) reads the
     correctly rounded table: exact everywhere."""
     vals = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
     vals = vals[np.isfinite(vals)]
