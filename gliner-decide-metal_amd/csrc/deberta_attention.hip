@@ -95,25 +95,30 @@ constexpr int kSchedMaxPairs = 2048;
 __global__ __launch_bounds__(1024) void attention_schedule_kernel(const int32_t* __restrict__ row_len, int B, int H,
                                                                   int L, int G, int32_t* __restrict__ sched,
                                                                   int n_slots) {
+  // An item's cost depends on its batch row only, so the rank of pair
+  // i = b H + h in the order (cost descending, index ascending) over all
+  // B H pairs is H (rows of higher cost + earlier rows of equal cost) + h.
   __shared__ int cost[kSchedMaxPairs];
   const int t = threadIdx.x;
   const int ntq = (L + kQT - 1) / kQT;
   const int n = B * H;
-  for (int i = t; i < n; i += 1024) {
-    const int len = row_len[i / H];
+  for (int b = t; b < B; b += 1024) {
+    const int len = row_len[b];
     int c = 0;
     for (int qt = 0; qt < ntq; ++qt) c += attention_item_cost(len, qt);
-    cost[i] = c;
+    cost[b] = c;
   }
   for (int s = t; s < n_slots; s += 1024) sched[s] = -1;
   __syncthreads();  // costs complete; the -1 stores land before any item store below
   for (int i = t; i < n; i += 1024) {
-    const int ci = cost[i];
-    int rank = 0;
-    for (int j = 0; j < n; ++j) {
+    const int b = i / H;
+    const int cb = cost[b];
+    int before = 0;
+    for (int j = 0; j < B; ++j) {
       const int cj = cost[j];
-      rank += (cj > ci) || (cj == ci && j < i);
+      before += (cj > cb) || (cj == cb && j < b);
     }
+    const int rank = before * H + (i - b * H);
     if (ntq == 2) {
       const int P = G >> 1;  // CU pairs
       const int r = rank / P, pp = rank - r * P;
