@@ -138,7 +138,8 @@ def test_embedding_layer_norm():
 @pytest.mark.parametrize("m,n,k", [(1, 128, 64), (65, 256, 128), (300, 1024, 1024), (1000, 384, 192),
                                    (160, 1024, 4096), (160, 4096, 1024), (37, 2048, 1024),
                                    (4096, 1024, 256), (8192, 3072, 1024), (8192, 4096, 1024),
-                                   (4896, 4096, 256), (5500, 3072, 256)])  # split: whole rounds + 128x128 rest
+                                   (4896, 4096, 256), (5500, 3072, 256),  # split: whole rounds + 128x128 rest
+                                   (4100, 4096, 128), (5120, 4096, 128)])  # GELU: one round of 320x256 tiles
 @pytest.mark.parametrize("epi", ["bias", "gelu", "relu", "none"])
 def test_linear(m, n, k, epi):
     r = np.random.default_rng(m + n + k)
