@@ -376,8 +376,9 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
   // congruent to lr modulo 16, so its swizzle term is the lane's own and
   // Lay::offset(row, 2 s + lk) = row_base * BK + (lane_off ^ 16 s): one lane
   // offset per operand, fragments apart by constants, slices by an XOR.
-  static_assert(BK == 64 && WM % 16 == 0 && WN % 16 == 0, "fragment address form");
-  const int lane_off = lr * BK + 8 * (lk ^ ((lr >> 1) & 1)) + 16 * ((lr >> 2) & 3);
+  static_assert(WM % 16 == 0 && WN % 16 == 0 && 16 % Lay::kRowsPer256 == 0, "fragment address form");
+  const int swz = (lr / Lay::kRowsPer256) & (Lay::kChunks - 1);  // the rows' swizzle term
+  const int lane_off = lr * BK + 8 * (lk ^ (swz & 1)) + 16 * (swz >> 1);
   const int a_frag0 = wm * WM * BK, b_frag0 = BM * BK + wn * WN * BK;
   auto read_frags = [&](const half_t* st, int slice, int set) {
     const int lo = lane_off ^ (16 * slice);
