@@ -8,6 +8,8 @@
 // staged kernel of deberta_attention.hip, which derives the indices from the
 // bucket function directly.
 #include <cmath>
+#include <cstdint>
+#include <initializer_list>
 
 #include "gd_common.hpp"
 #include "gd_kernels.hpp"
@@ -482,6 +484,16 @@ __global__ void relative_index_table_kernel(int32_t* __restrict__ out, int n, in
   if (i < 2 * n - 1) out[i] = relative_index(i - (n - 1), bucket_size, max_position);
 }
 
+// The matrix-core kernels read q, k, v and the table rows in 16-byte pieces,
+// the c2p indices four at a time and store half4 pieces of the output.
+bool general_mfma_ok(int64_t D, int64_t L, int64_t P, const int32_t* error_flag,
+                     std::initializer_list<const void*> ptrs) {
+  if (D != 64 || L % 16 != 0 || L > 512 || P > 65536 || error_flag != nullptr) return false;
+  for (const void* p : ptrs)
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return false;
+  return true;
+}
+
 }  // namespace
 
 int launch_relative_bias_general(const void* q, const void* k, const void* pos_key, const void* pos_query,
@@ -490,7 +502,7 @@ int launch_relative_bias_general(const void* q, const void* k, const void* pos_k
                                  hipStream_t stream) {
   if (B * H * L == 0) return GD_OK;
   // Indices travel packed in 16 bits, so the tables hold at most 65536 rows.
-  if (D == 64 && L % 16 == 0 && L <= 512 && P <= 65536 && error_flag == nullptr) {
+  if (general_mfma_ok(D, L, P, error_flag, {q, k, pos_key, pos_query, c2p, p2c, out})) {
     const dim3 grid((unsigned)(B * H * ((L + 63) / 64) * ((L / 16 + kGenKeyBlocks - 1) / kGenKeyBlocks)));
     hipLaunchKernelGGL(general_mfma_kernel<false>, grid, dim3(256), 0, stream, static_cast<const half_t*>(q),
                        static_cast<const half_t*>(k), nullptr, static_cast<const half_t*>(pos_key),
@@ -514,7 +526,7 @@ int launch_fused_attention_general(const void* q, const void* k, const void* v, 
                                    int32_t* error_flag, hipStream_t stream) {
   if (B * H * L == 0) return GD_OK;
   // Indices travel packed in 16 bits, so the tables hold at most 65536 rows.
-  if (D == 64 && L % 16 == 0 && L <= 512 && P <= 65536 && error_flag == nullptr) {
+  if (general_mfma_ok(D, L, P, error_flag, {q, k, v, pos_key, pos_query, c2p, p2c, out})) {
     const dim3 grid((unsigned)(B * H * ((L + 63) / 64)));
     hipLaunchKernelGGL(general_mfma_kernel<true>, grid, dim3(256), 0, stream, static_cast<const half_t*>(q),
                        static_cast<const half_t*>(k), static_cast<const half_t*>(v),

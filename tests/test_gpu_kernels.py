@@ -628,6 +628,40 @@ def test_general_index_kernels_clamp_out_of_range_indices():
     assert np.max(np.abs(got - want)) <= 2e-3
 
 
+def test_general_index_kernels_misaligned_indices():
+    """Index tensors 4 bytes off a 16-byte boundary take the per-query
+    kernels (the matrix-core kernels read indices four at a time): same
+    results as the aligned call, to the oracle's bounds."""
+    B, H, L, P = 1, 2, 32, 512
+    r = np.random.default_rng(78)
+    q, k, v = (r.standard_normal((B, H, L, 64)).astype(np.float16) for _ in range(3))
+    pkh, pqh = (r.standard_normal((H, P, 64)).astype(np.float16) for _ in range(2))
+    c2p = r.integers(0, P, size=(H, L, L)).astype(np.int32)
+    p2c = r.integers(0, P, size=(H, L, L)).astype(np.int32)
+    key_mask = np.zeros((B, L), np.float16)
+    key_mask[0, -3:] = -65504.0
+    scale = O.scale_f32(64)
+
+    def off4(a):  # the same values starting 4 bytes into a 16-byte aligned allocation
+        buf = torch.empty(a.size + 1, dtype=torch.int32, device="cuda")
+        buf[1:] = torch.from_numpy(a.reshape(-1)).cuda()
+        t = buf[1:].view(a.shape)
+        assert t.data_ptr() % 16 == 4
+        return t
+
+    want = O.relative_bias_kernel(q, k, pkh, pqh, c2p, p2c, key_mask, scale)
+    acc = 4.0 * 8.0 * 2.0 ** -24 * O.relative_bias_kernel(np.abs(q), np.abs(k), np.abs(pkh), np.abs(pqh), c2p, p2c,
+                                                            np.zeros_like(key_mask), scale, round16=False)
+    for c, p in ((dev(c2p), dev(p2c)), (off4(c2p), off4(p2c))):
+        got = host(fk().relative_bias(dev(q), dev(k), dev(pkh), dev(pqh), c, p, dev(key_mask), scale, B, H, L, 64, P))
+        assert np.all(np.abs(got - want) <= np.maximum(ulp16(got), ulp16(want)) + acc + 1e-12)
+    want = O.fused_attention_kernel(q, k, v, pkh, pqh, c2p, p2c, key_mask, scale)
+    for c, p in ((dev(c2p), dev(p2c)), (off4(c2p), off4(p2c))):
+        got = host(fk().fused_attention(dev(q), dev(k), dev(v), dev(pkh), dev(pqh), c, p, dev(key_mask), scale, B,
+                                        H, L, 64, P))
+        assert np.max(np.abs(got - want)) <= 2e-3
+
+
 def test_attention_rejects_bias_output_on_chains_without_a_bias():
     from gliner_decide import GlinerDecideError
     q, k, v, pk, pq, mask = _attn_case(7, 1, 1, 32)
