@@ -139,7 +139,8 @@ def test_embedding_layer_norm():
                                    (160, 1024, 4096), (160, 4096, 1024), (37, 2048, 1024),
                                    (4096, 1024, 256), (8192, 3072, 1024), (8192, 4096, 1024),
                                    (4896, 4096, 256), (5500, 3072, 256),  # split: whole rounds + 128x128 rest
-                                   (4100, 4096, 128), (5120, 4096, 128)])  # GELU: one round of 320x256 tiles
+                                   (4100, 4096, 128), (5120, 4096, 128),  # GELU: one round of 320x256 tiles
+                                   (32, 3072, 1024), (7, 4096, 1024)])  # one short sequence (64 x 64 tiles)
 @pytest.mark.parametrize("epi", ["bias", "gelu", "relu", "none"])
 def test_linear(m, n, k, epi):
     r = np.random.default_rng(m + n + k)
@@ -185,9 +186,10 @@ def test_linear_rows_do_not_depend_on_m(epi, n):
     """Every GEMM kernel accumulates an element over the same K slices in the
     same order and rounds it the same way: the first rows of an 8192-row
     product (256 x 256 tiles at N = 4096, 256-row tiles at N = 1024) equal,
-    bit for bit, the same rows computed alone (160 rows: the 64 x 64 tiles;
-    1500: 128 x 128 tiles at N = 4096, 64 x 64 at N = 1024; 4896: 320 x 256
-    tiles with GELU, 256 x 256 + 128 x 128 without, 192 x 128 at N = 1024)."""
+    bit for bit, the same rows computed alone (7, 32 and 160 rows: the
+    64 x 64 tiles; 1500: 128 x 128 tiles at N = 4096, 64 x 64 at N = 1024;
+    4896: 320 x 256 tiles with GELU, 256 x 256 + 128 x 128 without, 192 x 128
+    at N = 1024)."""
     r = np.random.default_rng(21)
     x = r.standard_normal((8192, 1024)).astype(np.float16)
     w = (r.standard_normal((n, 1024)) / 32).astype(np.float16)
@@ -197,7 +199,7 @@ def test_linear_rows_do_not_depend_on_m(epi, n):
         return t.cpu().numpy().view(np.uint16)
 
     full = bits(fk().linear(dev(x), dev(w), dev(b), epilogue=epi))
-    for m in (160, 1500, 4896):
+    for m in (7, 32, 160, 1500, 4896):
         np.testing.assert_array_equal(bits(fk().linear(dev(x[:m]), dev(w), dev(b), epilogue=epi)), full[:m])
 
 
