@@ -201,14 +201,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   auto clampi = [&](int x) { return x < 0 ? 0 : (x >= P ? P - 1 : x); };
   auto unpack = [](const uint32_t (&w)[2], int j) -> int { return (int)((w[j >> 1] >> (16 * (j & 1))) & 0xFFFFu); };
 
-  // Steps of a key block: 0 .. np - 1 gather c2p (posK rows), np .. 2 np - 1
-  // p2c (posQ rows), step p over table rows [128 (p mod np), + 128) (rows
-  // past P repeat row P - 1); the fused kernel's step 2 np brings the key
-  // block's V rows.  A step's rows are read into registers during the step
-  // before (the first step of a key block repeats the first step of every
-  // key block, so it is fetched once up front and again during the V step).
-  const int np = (P + kGenPass - 1) / kGenPass;
-  const int nsteps = 2 * np + (FUSED ? 1 : 0);
+  // Steps of a key block: the passes over the posK rows that hold any c2p
+  // index of the key block (passes c_lo .. c_lo + nc - 1), then the passes
+  // over the posQ rows that hold any of its p2c indices (p_lo .. p_lo + npp
+  // - 1); pass p covers table rows [128 p, + 128) (rows past P repeat row
+  // P - 1).  A pass holding no index of the block adds nothing, so it is not
+  // run (relative-position indices of a 64 x 128 tile span about 190 rows:
+  // 2 or 3 passes of each table instead of all of them).  The fused kernel's
+  // last step brings the key block's V rows.  A step's rows are read into
+  // registers during the step before.
+  __shared__ int pass_range[4][4];  // per wave: least / greatest c2p and p2c index
+  int c_lo = 0, nc = 0, p_lo = 0, npp = 0;
   constexpr int kPieces = kGenPass * 8 / 256;  // 16-byte pieces per thread
   half8_t pre[kPieces];
   auto fetch_rows = [&](int step, int ky_) {
@@ -216,9 +219,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int it = 0; it < kPieces; ++it) {
       const int i = t + 256 * it;
       const int row = i >> 3, ch = i & 7;
-      if (step < 2 * np) {
-        const int prow0 = (step < np ? step : step - np) * kGenPass + row;
-        const half_t* src = (step < np ? pkh : pqh) + (int64_t)(prow0 < P ? prow0 : P - 1) * 64;
+      if (step < nc + npp) {
+        const int prow0 = (step < nc ? c_lo + step : p_lo + step - nc) * kGenPass + row;
+        const half_t* src = (step < nc ? pkh : pqh) + (int64_t)(prow0 < P ? prow0 : P - 1) * 64;
         pre[it] = *reinterpret_cast<const half8_t*>(src + ch * 8);
       } else {
         // V rows of keys past L are zeros (their probabilities are 0 too)
@@ -237,7 +240,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   for (int dt = 0; dt < 4; ++dt) o[dt] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
   if (t < 64) tab[t * kGenStride + kGenPass] = -0.0f;  // visible after the first step's barriers
-  fetch_rows(0, 0);
   for (int kyi = 0; kyi < (FUSED ? nky : 1); ++kyi) {  // uniform
     const int kyb = FUSED ? kyi : ky;
     const int kb0 = kGenKeyBlocks * kyb;  // first 16-key block of this key block
@@ -245,6 +247,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // This lane's indices, clamped and packed two per register: c2p of keys
     // 16 kb + 4 g + j at query qg, p2c of query qg at those keys.
     uint32_t c2pk[MAXKB][2], p2ck[MAXKB][2];
+    int cmn = P, cmx = -1, pmn = P, pmx = -1;  // this lane's index range (valid scores only)
 #pragma unroll
     for (int kb = 0; kb < MAXKB; ++kb) {
       const bool ok = qg < L && kb < nkb;
@@ -255,11 +258,44 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int j = 0; j < 4; ++j) pi[j] = p2ch[(int64_t)(16 * (kb0 + kb) + 4 * g + j) * L + qg];
       }
-      c2pk[kb][0] = (uint32_t)clampi(ci.x) | ((uint32_t)clampi(ci.y) << 16);
-      c2pk[kb][1] = (uint32_t)clampi(ci.z) | ((uint32_t)clampi(ci.w) << 16);
-      p2ck[kb][0] = (uint32_t)clampi(pi[0]) | ((uint32_t)clampi(pi[1]) << 16);
-      p2ck[kb][1] = (uint32_t)clampi(pi[2]) | ((uint32_t)clampi(pi[3]) << 16);
+      const int c[4] = {clampi(ci.x), clampi(ci.y), clampi(ci.z), clampi(ci.w)};
+      const int pc[4] = {clampi(pi[0]), clampi(pi[1]), clampi(pi[2]), clampi(pi[3])};
+      c2pk[kb][0] = (uint32_t)c[0] | ((uint32_t)c[1] << 16);
+      c2pk[kb][1] = (uint32_t)c[2] | ((uint32_t)c[3] << 16);
+      p2ck[kb][0] = (uint32_t)pc[0] | ((uint32_t)pc[1] << 16);
+      p2ck[kb][1] = (uint32_t)pc[2] | ((uint32_t)pc[3] << 16);
+      if (ok) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          cmn = min(cmn, c[j]), cmx = max(cmx, c[j]);
+          pmn = min(pmn, pc[j]), pmx = max(pmx, pc[j]);
+        }
+      }
     }
+    // The workgroup's index range: wave reductions, then the four waves'
+    // through LDS (the previous key block read pass_range before its steps).
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      cmn = min(cmn, __shfl_xor(cmn, off, 64)), cmx = max(cmx, __shfl_xor(cmx, off, 64));
+      pmn = min(pmn, __shfl_xor(pmn, off, 64)), pmx = max(pmx, __shfl_xor(pmx, off, 64));
+    }
+    if (lane == 0) {
+      pass_range[wave][0] = cmn, pass_range[wave][1] = cmx;
+      pass_range[wave][2] = pmn, pass_range[wave][3] = pmx;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      cmn = min(cmn, pass_range[w][0]), cmx = max(cmx, pass_range[w][1]);
+      pmn = min(pmn, pass_range[w][2]), pmx = max(pmx, pass_range[w][3]);
+    }
+    // (wave 0's queries exist and nkb >= 1, so both ranges are non-empty)
+    c_lo = __builtin_amdgcn_readfirstlane(cmn / kGenPass);
+    nc = __builtin_amdgcn_readfirstlane(cmx / kGenPass) - c_lo + 1;
+    p_lo = __builtin_amdgcn_readfirstlane(pmn / kGenPass);
+    npp = __builtin_amdgcn_readfirstlane(pmx / kGenPass) - p_lo + 1;
+    const int nsteps = nc + npp + (FUSED ? 1 : 0);
+    fetch_rows(0, kyb);  // lands while the K rows load
     // The key block's K rows (clamped to L - 1) into LDS.  The previous key
     // block's last reads of krows came before its V step's barriers.
 #pragma unroll
@@ -292,7 +328,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 
     float* const p2c64 = tab;  // p2c steps: P2C of 64 keys [key][kGenStride] in the C2P table's space
-    for (int step = 0; step < 2 * np; ++step) {  // uniform
+    for (int step = 0; step < nc + npp; ++step) {  // uniform
       __syncthreads();  // the previous step is done with `rows` and the tables
 #pragma unroll
       for (int it = 0; it < kPieces; ++it) {
@@ -301,8 +337,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       __syncthreads();
       if (step + 1 < nsteps) fetch_rows(step + 1, kyb);  // lands during this step
-      const int base = (step < np ? step : step - np) * kGenPass;
-      if (step < np) {
+      const int base = (step < nc ? c_lo + step : p_lo + step - nc) * kGenPass;
+      if (step < nc) {
         // ---- c2p: C2P of this wave's queries, gathered by the wave itself ----
         if (active) {
 #pragma unroll 4
@@ -413,7 +449,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         *reinterpret_cast<half8_t*>(rows + gen_swz(i >> 3, i & 7)) = pre[it];
       }
       __syncthreads();
-      if (kyi + 1 < nky) fetch_rows(0, 0);  // the next key block's first step
       if (active) {
         // ds_read_b64_tr_b16: in each 16-lane group, source lane s names 4
         // consecutive halfs and lane j receives element j % 4 of source lanes
