@@ -140,6 +140,7 @@ def test_embedding_layer_norm():
                                    (4096, 1024, 256), (8192, 3072, 1024), (8192, 4096, 1024),
                                    (4896, 4096, 256), (5500, 3072, 256),  # split: whole rounds + 128x128 rest
                                    (4100, 4096, 128), (5120, 4096, 128),  # GELU: one round of 320x256 tiles
+                                   (4896, 4096, 64), (4200, 4096, 192),  # ... one and three K steps
                                    (32, 3072, 1024), (7, 4096, 1024)])  # one short sequence (64 x 64 tiles)
 @pytest.mark.parametrize("epi", ["bias", "gelu", "relu", "none"])
 def test_linear(m, n, k, epi):
