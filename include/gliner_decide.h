@@ -154,7 +154,10 @@ int gd_linear(const void* a, const void* w, const void* bias, void* c, int64_t m
  * c2p_indices = p2c_indices = NULL selects the closed-form indices the
  * classifier builds (c2p[h,q,k] = p2c[h,k,q] = clip(bucket(q - k) + 256, 0,
  * 511), DeBERTa.swift:498-519) and runs them on the MFMA attention kernel
- * (D = 64, P = 512, L a multiple of 16 in [16, 512]).
+ * (D = 64, P = 512, L a multiple of 16 in [16, 512]).  Index tensors run on
+ * the matrix cores too when D = 64, L is a multiple of 16 up to 512,
+ * P <= 65536 and every operand is 16-byte aligned; otherwise on per-query
+ * kernels.  Indices outside [0, P) read the nearest table row.
  * Replaces FusedKernels.relativeBias (FusedKernels.swift:83-123, 214-258). */
 int gd_relative_bias(const void* q, const void* k, const void* pos_key, const void* pos_query,
                      const int32_t* c2p_indices, const int32_t* p2c_indices, const void* key_mask,
@@ -165,7 +168,8 @@ int gd_relative_bias(const void* q, const void* k, const void* pos_key, const vo
  * score = (q.k + q.pos_key[c2p] + k.pos_query[p2c]) * scale (fp32), masked
  * keys := -65504, softmax, out[b, q, h, :] = sum_k w v  -> [B, L, H, D] fp16.
  * NULL index tensors select the closed-form indices, as for
- * gd_relative_bias, on the MFMA attention kernel.
+ * gd_relative_bias, on the MFMA attention kernel; index tensors take the
+ * matrix cores under gd_relative_bias's conditions.
  * Replaces FusedKernels.fusedAttention (FusedKernels.swift:13-81, 160-210). */
 int gd_fused_attention(const void* q, const void* k, const void* v, const void* pos_key,
                        const void* pos_query, const int32_t* c2p_indices,
