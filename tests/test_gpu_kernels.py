@@ -631,6 +631,34 @@ def test_general_index_kernels_clamp_out_of_range_indices():
     assert np.max(np.abs(got - want)) <= 2e-3
 
 
+@pytest.mark.parametrize("L,P", [(16, 512), (32, 65536), (32, 65537)])
+def test_general_index_kernels_size_limits(L, P):
+    """The shortest sequence (one 16-key block, one active wave), the largest
+    table the matrix-core kernels' 16-bit packed indices address (P = 65536,
+    indices up to 65535) and one row more (the per-query kernels)."""
+    B, H = 2, 1
+    r = np.random.default_rng(P + L)
+    q, k, v = (r.standard_normal((B, H, L, 64)).astype(np.float16) for _ in range(3))
+    pkh, pqh = (r.standard_normal((H, P, 64)).astype(np.float16) for _ in range(2))
+    c2p = r.integers(0, P, size=(H, L, L)).astype(np.int32)
+    p2c = r.integers(0, P, size=(H, L, L)).astype(np.int32)
+    c2p[0, 0, :2] = [0, P - 1]  # both ends of the table
+    p2c[0, :2, 0] = [P - 1, 0]
+    key_mask = np.zeros((B, L), np.float16)
+    key_mask[1, L // 2:] = -65504.0
+    scale = O.scale_f32(64)
+    want = O.relative_bias_kernel(q, k, pkh, pqh, c2p, p2c, key_mask, scale)
+    got = host(fk().relative_bias(dev(q), dev(k), dev(pkh), dev(pqh), dev(c2p), dev(p2c), dev(key_mask), scale, B, H,
+                                  L, 64, P))
+    acc = 4.0 * 8.0 * 2.0 ** -24 * O.relative_bias_kernel(np.abs(q), np.abs(k), np.abs(pkh), np.abs(pqh), c2p, p2c,
+                                                            np.zeros_like(key_mask), scale, round16=False)
+    assert np.all(np.abs(got - want) <= np.maximum(ulp16(got), ulp16(want)) + acc + 1e-12)
+    want = O.fused_attention_kernel(q, k, v, pkh, pqh, c2p, p2c, key_mask, scale)
+    got = host(fk().fused_attention(dev(q), dev(k), dev(v), dev(pkh), dev(pqh), dev(c2p), dev(p2c), dev(key_mask),
+                                    scale, B, H, L, 64, P))
+    assert np.max(np.abs(got - want)) <= 2e-3
+
+
 def test_general_index_kernels_misaligned_indices():
     """Index tensors 4 bytes off a 16-byte boundary take the per-query
     kernels (the matrix-core kernels read indices four at a time): same
