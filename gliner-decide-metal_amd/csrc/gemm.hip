@@ -78,6 +78,12 @@ __device__ __forceinline__ half_t gelu_from_table(half_t y, const half_t* tab, c
   return mag < (uint32_t)kGeluHalf ? small : big;
 }
 
+// The correctly rounded GELU of every fp16 bit pattern (65,536 entries,
+// 128 KiB), filled on the device from the lookup below, so each entry is
+// exactly what that lookup returns (NaN payloads included): tiles whose
+// stage buffers hold it replace the lookup's arithmetic by one read.
+__device__ __attribute__((aligned(16))) half_t g_gelu_full[65536];
+
 // The same lookup in the global copy of the table.
 __device__ __forceinline__ half_t gelu_from_global_table(half_t y) {
   const uint32_t u = __builtin_bit_cast(uint16_t, y);
@@ -86,6 +92,11 @@ __device__ __forceinline__ half_t gelu_from_global_table(half_t y) {
   const half_t big = (u >> 15) ? (half_t)(y * (half_t)0) : y;
   const half_t small = g_gelu_table[idx];
   return mag < (uint32_t)kGeluHalf ? small : big;
+}
+
+__global__ __launch_bounds__(256) void gelu_full_table_kernel() {
+  const int u = blockIdx.x * 256 + threadIdx.x;
+  g_gelu_full[u] = gelu_from_global_table(__builtin_bit_cast(half_t, (uint16_t)u));
 }
 
 // Epilogue of one output element: the fp16 addMM output (acc + bias rounded
@@ -311,17 +322,24 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
   constexpr bool GELU_TABLE = EPI == GD_EPI_BIAS_GELU && (RPA % WM == 0 || WAVES_M * 32 <= RPA) &&
                               (NSTAGE == 2 || 2 * STAGE >= kGeluEntries);
   static_assert(EPI != GD_EPI_BIAS_GELU || GELU_TABLE || NSTAGE * RPA >= BM, "GELU epilogue staging");
+  // Tiles whose stage buffers hold 128 KiB (and whose GELU values all fit
+  // the registers before C is staged) read the full 65,536-entry table:
+  // the stages are then one array, the table lands in it after the K loop.
+  constexpr bool FULLTAB = GELU_TABLE && BM != 320 && RPA % WM == 0 && NSTAGE * STAGE >= 65536;
   constexpr bool TAB0 = GELU_TABLE && NSTAGE == 2 && BM == 320;  // the table in st0, DMA'd under the K loop
   constexpr int TAB1 = NSTAGE == 2 || kGeluEntries <= STAGE ? kGeluEntries : STAGE;  // entries in st1
-  __shared__ __attribute__((aligned(1024))) half_t st0[TAB0 && kGeluEntries > STAGE ? kGeluEntries : STAGE];
-  __shared__ __attribute__((aligned(1024)))
-  half_t st1[GELU_TABLE && !TAB0 && NSTAGE == 2 && kGeluEntries > STAGE ? kGeluEntries : STAGE];
-  __shared__ __attribute__((aligned(1024))) half_t st2[NSTAGE > 2 ? STAGE : 8];
-  __shared__ __attribute__((aligned(1024))) half_t st3[NSTAGE > 3 ? STAGE : 8];
-  __shared__ __attribute__((aligned(1024))) half_t st4[NSTAGE > 4 ? STAGE : 8];
+  constexpr int kA = FULLTAB ? 16 : 1024;  // alignment of the separate buffers (unused with FULLTAB)
+  __shared__ __attribute__((aligned(1024))) half_t stall[FULLTAB ? NSTAGE * STAGE : 8];
+  __shared__ __attribute__((aligned(kA))) half_t st0[FULLTAB ? 8 : (TAB0 && kGeluEntries > STAGE ? kGeluEntries : STAGE)];
+  __shared__ __attribute__((aligned(kA)))
+  half_t st1[FULLTAB ? 8 : (GELU_TABLE && !TAB0 && NSTAGE == 2 && kGeluEntries > STAGE ? kGeluEntries : STAGE)];
+  __shared__ __attribute__((aligned(kA))) half_t st2[NSTAGE > 2 && !FULLTAB ? STAGE : 8];
+  __shared__ __attribute__((aligned(kA))) half_t st3[NSTAGE > 3 && !FULLTAB ? STAGE : 8];
+  __shared__ __attribute__((aligned(kA))) half_t st4[NSTAGE > 4 && !FULLTAB ? STAGE : 8];
   auto stage = [&](auto b) -> half_t* {
     constexpr int B = decltype(b)::value;
-    if constexpr (B == 0) return st0;
+    if constexpr (FULLTAB) return stall + B * STAGE;
+    else if constexpr (B == 0) return st0;
     else if constexpr (B == 1) return st1;
     else if constexpr (B == 2) return st2;
     else if constexpr (B == 3) return st3;
@@ -518,11 +536,17 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
   if constexpr (GELU_TABLE) {
     // ---- GELU epilogue: the table in st0 (two stages) or st1 + st2, C
     // through the other buffer in passes ----
-    const half_t* tab = TAB0 ? st0 : st1;
+    const half_t* tab = FULLTAB ? stall : (TAB0 ? st0 : st1);
     const half_t* tab2 = stage(ic<2 % NSTAGE>{});
     constexpr uint32_t kSplit = TAB0 ? kGeluEntries : TAB1;
-    half_t* const cst = TAB0 ? st1 : st0;
-    if constexpr (!TAB0) {
+    half_t* const cst = FULLTAB ? stall : (TAB0 ? st1 : st0);
+    if constexpr (FULLTAB) {
+      // the full table by DMA into the stage buffers (all read: the K loop's
+      // last barrier), wave w taking 1 KiB blocks w, w + NW, ...
+      for (int j = wave; j < 65536 / 512; j += NW) load_lds16(g_gelu_full + j * 512 + lane * 8, stall + j * 512);
+      wait_vmcnt<0>();
+      __syncthreads();
+    } else if constexpr (!TAB0) {
       // All of this thread's table pieces are loaded before any is stored,
       // so the L2 latency is paid once.
       constexpr int kPieces = kGeluEntries / 8;
@@ -544,8 +568,13 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
     auto gelu_of = [&](int i, int j, int q) {
       half4_t r;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        r[e] = gelu_from_table((half_t)(acc[i][j][4 * q + e] + bq[j][q][e]), tab, tab2, kSplit);
+      for (int e = 0; e < 4; ++e) {
+        const half_t y = (half_t)(acc[i][j][4 * q + e] + bq[j][q][e]);
+        if constexpr (FULLTAB)
+          r[e] = tab[__builtin_bit_cast(uint16_t, y)];
+        else
+          r[e] = gelu_from_table(y, tab, tab2, kSplit);
+      }
       return r;
     };
     if constexpr (RPA % WM == 0) {
@@ -556,6 +585,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
         for (int j = 0; j < TN; ++j)
 #pragma unroll
           for (int q = 0; q < 4; ++q) res[i][j][q] = gelu_of(i, j, q);
+      if constexpr (FULLTAB) __syncthreads();  // every wave's table reads precede the staging writes
       constexpr int NPASS = (BM + RPA - 1) / RPA;
 #pragma unroll
       for (int pass = 0; pass < NPASS; ++pass) {
@@ -725,6 +755,10 @@ int ensure_gelu_table(hipStream_t stream) {
   }
   const std::vector<uint16_t>& tab = gelu_table_host();
   GD_HIP_CHECK(hipMemcpyToSymbol(HIP_SYMBOL(g_gelu_table), tab.data(), tab.size() * sizeof(uint16_t)));
+  // the full table from the compact one, before any stream can read it
+  hipLaunchKernelGGL(gelu_full_table_kernel, dim3(256), dim3(256), 0, stream);
+  GD_LAUNCH_CHECK();
+  GD_HIP_CHECK(hipStreamSynchronize(stream));
   ready[dev] = true;
   return GD_OK;
 }
