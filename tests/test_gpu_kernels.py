@@ -137,7 +137,8 @@ def test_embedding_layer_norm():
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("m,n,k", [(1, 128, 64), (65, 256, 128), (300, 1024, 1024), (1000, 384, 192),
                                    (160, 1024, 4096), (160, 4096, 1024), (37, 2048, 1024),
-                                   (4096, 1024, 256), (8192, 3072, 1024), (8192, 4096, 1024),
+                                   (4096, 1024, 256), (4896, 1024, 4096),  # one round of 160x128 tiles
+                                   (8192, 3072, 1024), (8192, 4096, 1024),
                                    (4896, 4096, 256), (5500, 3072, 256),  # split: whole rounds + 128x128 rest
                                    (4100, 4096, 128), (5120, 4096, 128),  # GELU: one round of 320x256 tiles
                                    (4896, 4096, 64), (4200, 4096, 192),  # ... one and three K steps
@@ -189,7 +190,7 @@ def test_linear_rows_do_not_depend_on_m(epi, n):
     product (256 x 256 tiles at N = 4096, 256-row tiles at N = 1024) equal,
     bit for bit, the same rows computed alone (7, 32 and 160 rows: the
     64 x 64 tiles; 1500: 128 x 128 tiles at N = 4096, 64 x 64 at N = 1024;
-    4896: 320 x 256 tiles with GELU, 256 x 256 + 128 x 128 without, 192 x 128
+    4896: 320 x 256 tiles with GELU, 256 x 256 + 128 x 128 without, 160 x 128
     at N = 1024)."""
     r = np.random.default_rng(21)
     x = r.standard_normal((8192, 1024)).astype(np.float16)
