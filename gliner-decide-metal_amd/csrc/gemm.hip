@@ -528,14 +528,19 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
   // workgroups still re-read (1-2 us less per launch on the 8,192-row
   // projections, +1% on the whole classify step; the LayerNorm and
   // attention outputs measured slower the same way and keep plain stores).
+  // The full-GELU-table tiles are the exception: plain stores take 2.5-3 us
+  // off FFN-up at 8,192 rows.
   auto store_rows = [&](int row0, int nrows, auto&& buf) {
 #pragma unroll 4
     for (int idx = t; idx < nrows * UPR; idx += NT) {
       const int r = idx / UPR, u = idx - r * UPR;
       const int row = tile_m * BM + row0 + r;
-      if (row < M)
-        __builtin_nontemporal_store(*reinterpret_cast<const half4_t*>(buf(r) + 4 * (u ^ (r & 15))),
-                                    reinterpret_cast<half4_t*>(C + (int64_t)row * ldc + tile_n * BN + 4 * u));
+      if (row < M) {
+        const half4_t v = *reinterpret_cast<const half4_t*>(buf(r) + 4 * (u ^ (r & 15)));
+        half4_t* dst = reinterpret_cast<half4_t*>(C + (int64_t)row * ldc + tile_n * BN + 4 * u);
+        if constexpr (FULLTAB) *dst = v;
+        else __builtin_nontemporal_store(v, dst);
+      }
     }
   };
   if constexpr (GELU_TABLE) {
