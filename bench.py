@@ -65,16 +65,21 @@ def parse():
 # ---------------------------------------------------------------------------
 # live kernel timing
 # ---------------------------------------------------------------------------
-def gemm_tile(M, N, cus=256):
-    """The tile launch_linear picks for M >= 2048 rows (gemm.hip): whole
-    rounds of 256x256 plus a 128x128 remainder, or the fewest rounds of
-    tiles weighted by their relative cost."""
+def gemm_tile(M, N, gelu=False, cus=256):
+    """The tile launch_linear picks for M >= 2048 rows (gemm.hip): one round
+    of 320x256 (GELU) or 160x128 (four waves, no GELU) tiles where it fits,
+    whole rounds of 256x256 plus a 128x128 remainder, or the fewest rounds
+    of tiles weighted by their relative cost."""
     if N % 256 == 0:
         per_round = cus // (N // 256)
+        if gelu and per_round * 256 < M <= per_round * 320:
+            return "320,256"
         full = M // (per_round * 256) * (per_round * 256) if per_round else 0
         rest = M - full
         if full > 0 and rest > 0 and (rest + 127) // 128 * (N // 128) <= cus:
             return "256,256 + 128,128"
+    if not gelu and -(-M // 160) * (N // 128) <= cus:
+        return "160,128"
 
     def rounds(bm, bn):
         return -(-(-(-M // bm) * (N // bn)) // cus)
@@ -268,7 +273,7 @@ def measure_kernels(model_cfg, iters, only=None):
 
         us = time_launches(lin, [0], iters)
         flops = 2 * T * n * k
-        out[name] = dict(kernel=f"gemm_nt_lds_kernel<{gemm_tile(T, n)}>", shape=[T, n, k], us=us, flops=flops,
+        out[name] = dict(kernel=f"gemm_nt_lds_kernel<{gemm_tile(T, n, epi == 'gelu')}>", shape=[T, n, k], us=us, flops=flops,
                          tflops=flops / us / 1e6, bound="mfma", launches_per_step=24,
                          bytes=(T * k + n * k + T * n) * 2)
         del a, w, c
