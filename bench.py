@@ -30,7 +30,10 @@ for _p in (str(ROOT), str(ROOT / "gliner-decide-metal_amd")):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
-ROOFLINE_KERNEL = "ffn_up_gelu"  # the kernel with the largest share of the step (profiles/e2e_classify_b32_l256.md)
+# FFN-up + GELU: the single product with the largest share of the step
+# (24.3% in profiles/e2e_classify_b32_l256.md; out-proj and FFN-down together
+# take 30.6% through one kernel, each less than FFN-up)
+ROOFLINE_KERNEL = "ffn_up_gelu"
 FP16_DENSE_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
 ROTATE_BYTES = 600 << 20  # > 2x the 256 MB MALL
 
