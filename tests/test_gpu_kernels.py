@@ -183,18 +183,19 @@ def check_linear(out, x, w, b, epi):
         assert np.mean(out != O.f16(y)) < 5e-3
 
 
-@pytest.mark.parametrize("epi,n", [("bias", 4096), ("gelu", 4096), ("bias", 1024)])
-def test_linear_rows_do_not_depend_on_m(epi, n):
+@pytest.mark.parametrize("epi,n,k", [("bias", 4096, 1024), ("gelu", 4096, 1024), ("bias", 1024, 1024),
+                                     ("bias", 1024, 4096)])
+def test_linear_rows_do_not_depend_on_m(epi, n, k):
     """Every GEMM kernel accumulates an element over the same K slices in the
     same order and rounds it the same way: the first rows of an 8192-row
     product (256 x 256 tiles at N = 4096, 256-row tiles at N = 1024) equal,
     bit for bit, the same rows computed alone (7, 32 and 160 rows: the
     64 x 64 tiles; 1500: 128 x 128 tiles at N = 4096, 64 x 64 at N = 1024;
     4896: 320 x 256 tiles with GELU, 256 x 256 + 128 x 128 without, 160 x 128
-    at N = 1024)."""
+    at N = 1024, also at K = 4096: the FFN-down shape)."""
     r = np.random.default_rng(21)
-    x = r.standard_normal((8192, 1024)).astype(np.float16)
-    w = (r.standard_normal((n, 1024)) / 32).astype(np.float16)
+    x = r.standard_normal((8192, k)).astype(np.float16)
+    w = (r.standard_normal((n, k)) / np.sqrt(k)).astype(np.float16)
     b = r.standard_normal(n).astype(np.float16)
     def bits(t):
         torch.cuda.synchronize()
