@@ -43,6 +43,14 @@ constexpr size_t kStaticWorkspaceBytes = size_t(48) << 20;
 static __device__ __align__(256) unsigned char scratch[kStaticWorkspaceBytes];
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[64] = {};  // device address of `scratch`, per device
+// Orders the static-workspace calls on one GPU: each call's first launch
+// waits for the event the previous call recorded after its last launch, on
+// whatever stream that call used, and the mutex keeps a call's wait, launches
+// and record together.  Calls from two streams or threads then run one after
+// the other in the order they were made, instead of overwriting each other's
+// activations.
+std::mutex g_static_call_mu[64];
+hipEvent_t g_static_event[64] = {};
 
 struct HipDeviceGuard {
   int prev = -1;
@@ -291,6 +299,9 @@ int Classifier::init_static_workspace() {
   if (!g_scratch_ptr[device_]) {
     void* p = nullptr;
     GD_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    hipEvent_t ev = nullptr;
+    GD_HIP_CHECK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    g_static_event[device_] = ev;
     g_scratch_ptr[device_] = p;
   }
   static_ws_base_ = g_scratch_ptr[device_];
@@ -342,7 +353,18 @@ int Classifier::classify_static(const int32_t* ids, const void* mask, const int3
     return GD_ERR_SHAPE;
   }
   carve_workspace(w, static_cast<uint8_t*>(static_ws_base_), T, M, B, slots);
-  return forward(w, ids, mask, markers, marker_mask, B, L, Hh, O, logits, stream, nullptr, packed_tokens);
+  // Eager calls are ordered through the device's event.  Under graph capture
+  // the wait and record are left out (an event recorded outside the capture
+  // cannot join it): replays are ordered by whoever launches them.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  const bool capturing = hipStreamIsCapturing(stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone;
+  std::lock_guard<std::mutex> lock(g_static_call_mu[device_]);
+  hipEvent_t ev = g_static_event[device_];
+  if (!capturing) GD_HIP_CHECK(hipStreamWaitEvent(stream, ev, 0));
+  const int st = forward(w, ids, mask, markers, marker_mask, B, L, Hh, O, logits, stream, nullptr, packed_tokens);
+  // recorded after a failed call too: later calls wait for what it enqueued
+  if (!capturing) GD_HIP_CHECK(hipEventRecord(ev, stream));
+  return st;
 }
 
 // One encoder layer (DeBERTa.swift:296-428).

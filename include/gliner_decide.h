@@ -352,8 +352,13 @@ int gd_classifier_classify_packed(gd_classifier* model, const int32_t* input_ids
  * packed total) with up to 1024 marker slots (B*Hh*O); larger calls return
  * GD_ERR_SHAPE.  The array (one per GPU, held from the library's first use on
  * that GPU until the process ends) is shared by every context on that GPU
- * and keeps the last call's contents: calls that overlap on one GPU (two
- * streams, threads or contexts) race. */
+ * and keeps the last call's contents.  Calls on one GPU are ordered: each
+ * waits, on its stream, for the work of the call made before it (a per-GPU
+ * event), so calls from two streams, threads or contexts run one after the
+ * other in the order they were made.  A call made during graph capture
+ * records no such wait: replays of that graph race with other calls on the
+ * same GPU unless the caller orders them.  The call captures cleanly once
+ * the context exists (its tables are filled at creation). */
 int gd_classifier_classify_static(gd_classifier* model, const int32_t* input_ids, const void* attention_mask,
                                   const int32_t* marker_indices, const float* marker_mask, int64_t batch,
                                   int64_t seq_len, int64_t max_heads, int64_t max_options, int64_t total_tokens,
