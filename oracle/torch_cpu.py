@@ -10,6 +10,15 @@ DeBERTa.swift:274-447 with the relative bias of :374-379 and SDPA of
 rounding points, with torch's multithreaded CPU kernels -- the fastest
 faithful CPU evaluation available in this environment.  Every row is
 computed at the full bucket length L, as the reference does.
+
+With round16=True the same graph rounds to fp16 wherever the reference
+writes an fp16 array (the rounding points of `oracle.deberta`: every addMM
+output, c2pRaw / p2cRaw, their sum and its division by fp16(sqrt(3D)), the
+bias + key-mask add, the attention output, the residual sums, LayerNorm and
+GELU outputs, the classifier's logits) and evaluates between them in fp32:
+a second restatement of the GPU's rounding chain, fast enough to check whole
+batches at the label-probability bar.  It is pinned against the numpy
+oracle (float64 and float32, same rounding points) in tests/test_oracle.py.
 """
 
 from __future__ import annotations
@@ -27,8 +36,10 @@ def _t(a) -> torch.Tensor:
 class TorchCPUModel:
     """`GLiNERDecideClassifier` (default flags) on torch CPU tensors, fp32."""
 
-    def __init__(self, weights: dict, config: O.Config):
+    def __init__(self, weights: dict, config: O.Config, round16: bool = False):
         self.c = config
+        self.round16 = round16
+        r = self._r
         C, H = config.hidden_size, config.num_attention_heads
         self.H, self.D = H, C // H
         w = O.ModelWeights.from_store(weights, config)
@@ -37,10 +48,10 @@ class TorchCPUModel:
         self.layers = []
         eps = config.layer_norm_eps
         # relative precompute (DeBERTa.swift:204-227)
-        rel_n = torch.nn.functional.layer_norm(_t(w.rel_embeddings), (C,), _t(w.rel_ln_g), _t(w.rel_ln_b), eps)
+        rel_n = r(torch.nn.functional.layer_norm(_t(w.rel_embeddings), (C,), _t(w.rel_ln_g), _t(w.rel_ln_b), eps))
         for lw in w.layers:
             qkv_w, qkv_b = _t(lw.qkv_w), _t(lw.qkv_b)
-            pos = (rel_n @ qkv_w[: 2 * C].T + qkv_b[: 2 * C]).view(O.POSITION_COUNT, 2, H, self.D)
+            pos = r(rel_n @ qkv_w[: 2 * C].T + qkv_b[: 2 * C]).view(O.POSITION_COUNT, 2, H, self.D)
             self.layers.append(dict(
                 qkv_w=qkv_w, qkv_b=qkv_b, pos_q=pos[:, 0].permute(1, 0, 2).contiguous(),
                 pos_k=pos[:, 1].permute(1, 0, 2).contiguous(), out_w=_t(lw.out_w), out_b=_t(lw.out_b),
@@ -49,6 +60,10 @@ class TorchCPUModel:
         self.cls0_w, self.cls0_b = _t(w.cls0_w), _t(w.cls0_b)
         self.cls2_w, self.cls2_b = _t(w.cls2_w), _t(w.cls2_b)
         self._idx = {}
+
+    def _r(self, t: torch.Tensor) -> torch.Tensor:
+        """An fp16 rounding point (identity unless round16)."""
+        return t.half().float() if self.round16 else t
 
     def _indices(self, L: int):
         if L not in self._idx:
@@ -59,13 +74,27 @@ class TorchCPUModel:
     @torch.no_grad()
     def forward(self, ids, attention_mask, marker_indices, marker_mask) -> torch.Tensor:
         """Logits [B, Hh, O] (fp32) for host arrays of one batch."""
+        r = self._r
+        x = self.encode(ids, attention_mask)
+        B, L, C = x.shape
+        mi = torch.from_numpy(np.asarray(marker_indices, np.int64))  # :430-444
+        flat = (mi + (torch.arange(B) * L)[:, None, None]).reshape(-1)
+        m = x.reshape(B * L, C)[flat]
+        val = r(torch.relu(r(m @ self.cls0_w.T + self.cls0_b)) @ self.cls2_w.T + self.cls2_b)[:, 0].view(mi.shape)
+        mm = _t(marker_mask)
+        return r(torch.where(mm > 0, val, torch.tensor(O.LOGIT_FILL)))
+
+    @torch.no_grad()
+    def encode(self, ids, attention_mask) -> torch.Tensor:
+        """Final hidden states [B, L, C] (fp32) for host arrays of one batch."""
         c, H, D = self.c, self.H, self.D
         C, eps = c.hidden_size, c.layer_norm_eps
+        r = self._r
         ids = torch.from_numpy(np.asarray(ids, np.int64))
         mask = _t(attention_mask)
         B, L = ids.shape
         ln = torch.nn.functional.layer_norm
-        x = ln(self.emb[ids], (C,), self.emb_g, self.emb_b, eps) * mask[..., None]  # :285-292
+        x = r(r(ln(self.emb[ids], (C,), self.emb_g, self.emb_b, eps)) * mask[..., None])  # :285-292
         c2p_idx, p2c_idx = self._indices(L)
         ci = c2p_idx.expand(B, H, L, L)
         pi = p2c_idx.expand(B, H, L, L)
@@ -73,22 +102,20 @@ class TorchCPUModel:
         bias_scale = O.scale_f16(D)  # fp16(sqrt(3D)) (:323-326)
         qk_scale = O.scale_f32(D)  # 1 / sqrt(3D) (:390)
         for p in self.layers:
-            qkv = (x @ p["qkv_w"].T + p["qkv_b"]).view(B, L, 3, H, D)  # :298-320
+            qkv = r(x @ p["qkv_w"].T + p["qkv_b"]).view(B, L, 3, H, D)  # :298-320
             q, k, v = (qkv[:, :, i].permute(0, 2, 1, 3) for i in range(3))
-            c2p = torch.gather(q @ p["pos_k"].transpose(-1, -2), -1, ci)  # :374-375
-            p2c = torch.gather(k @ p["pos_q"].transpose(-1, -2), -1, pi).transpose(-1, -2)  # :376-378
-            bias = (c2p + p2c) / bias_scale  # :379
-            scores = q @ k.transpose(-1, -2) * qk_scale + bias + key_mask  # :383-392
-            ctx = (torch.softmax(scores, -1) @ v).permute(0, 2, 1, 3).reshape(B, L, C)
-            x = ln(ctx @ p["out_w"].T + p["out_b"] + x, (C,), p["ln1_g"], p["ln1_b"], eps)  # :412-418
-            inter = torch.nn.functional.gelu(x @ p["inter_w"].T + p["inter_b"])  # :420-421
-            x = ln(inter @ p["ffn_w"].T + p["ffn_b"] + x, (C,), p["ln2_g"], p["ln2_b"], eps)  # :422-427
-        mi = torch.from_numpy(np.asarray(marker_indices, np.int64))  # :430-444
-        flat = (mi + (torch.arange(B) * L)[:, None, None]).reshape(-1)
-        m = x.reshape(B * L, C)[flat]
-        val = (torch.relu(m @ self.cls0_w.T + self.cls0_b) @ self.cls2_w.T + self.cls2_b)[:, 0].view(mi.shape)
-        mm = _t(marker_mask)
-        return torch.where(mm > 0, val, torch.tensor(O.LOGIT_FILL))
+            c2p = torch.gather(r(q @ p["pos_k"].transpose(-1, -2)), -1, ci)  # :374-375
+            p2c = torch.gather(r(k @ p["pos_q"].transpose(-1, -2)), -1, pi).transpose(-1, -2)  # :376-378
+            bias = r(r(c2p + p2c) / bias_scale)  # :379
+            del c2p, p2c
+            scores = q @ k.transpose(-1, -2) * qk_scale + r(bias + key_mask)  # :383-392
+            del bias
+            ctx = r((torch.softmax(scores, -1) @ v).permute(0, 2, 1, 3).reshape(B, L, C))
+            del scores
+            x = r(ln(r(r(ctx @ p["out_w"].T + p["out_b"]) + x), (C,), p["ln1_g"], p["ln1_b"], eps))  # :412-418
+            inter = r(torch.nn.functional.gelu(r(x @ p["inter_w"].T + p["inter_b"])))  # :420-421
+            x = r(ln(r(r(inter @ p["ffn_w"].T + p["ffn_b"]) + x), (C,), p["ln2_g"], p["ln2_b"], eps))  # :422-427
+        return x
 
     @staticmethod
     def flops(B: int, L: int, config: O.Config) -> float:
