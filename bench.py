@@ -543,12 +543,17 @@ def main():
     _, Hh, O_ = markers.shape
     model.reserve(B, L, Hh, O_)
     logits = torch.empty((B, Hh, O_), dtype=torch.float16, device=ids.device)
+    # The step ends with the logits in host memory (main.swift:247-279 reads
+    # them back): an asynchronous copy into pinned memory on the forward's
+    # stream, so the next step's forward queues behind it without a host wait.
+    logits_host = torch.empty((B, Hh, O_), dtype=torch.float16, pin_memory=True)
 
     def step():
         # the packed forward's token count comes from the host copy of the
         # batch (what a tokenizer knows), every step
         total = int(row_extents(host["attention_mask"], host["marker_indices"], host["marker_mask"]).sum())
         model.classify_device(ids, mask, markers, mmask, logits, total_tokens=total)
+        logits_host.copy_(logits, non_blocking=True)
 
     def timed(fn, steps):
         torch.cuda.synchronize()
@@ -564,8 +569,9 @@ def main():
     ms = elapsed * 1000 / args.steps
     rows_s = B * args.steps / elapsed
     assert torch.isfinite(logits.float()).all()
+    assert torch.equal(logits_host, logits.cpu())
     packed_logits = logits.clone()  # the headline forward's output
-    log(f"e2e: {ms:.3f} ms/step, {rows_s:.1f} rows/s (packed rows)")
+    log(f"e2e: {ms:.3f} ms/step, {rows_s:.1f} rows/s (packed rows, logits read back to pinned host memory)")
     padded_logits = torch.empty_like(logits)
     padded = lambda: model.classify_device(ids, mask, markers, mmask, padded_logits)  # noqa: E731
     for _ in range(args.warmup):
@@ -632,7 +638,8 @@ def main():
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic (seeded ids/lengths; random-init N(0,0.02) fp16 weights of DeBERTa-v3-large + GLiNER head)",
-        "config": dict(wl, parallelism="single GPU", compiled_graph=args.compiled, rows="packed"),
+        "config": dict(wl, parallelism="single GPU", compiled_graph=args.compiled, rows="packed",
+                       step="forward + classifier + logits D2H into pinned host memory"),
         "roofline": roof,
         "cpu_baseline": cpu,
         "kernels": {k: dict({kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()},
