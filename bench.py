@@ -3,16 +3,19 @@ MI355X, B=32 rows of L=256 tokens per step (synthetic seeded inputs and
 random-init fp16 weights of the real architecture).
 
 One step = one `classify` of a 32-row batch (embedding, 24 layers, classifier)
-with inputs resident in HBM.  Prints ONE JSON line on stdout (logs on stderr):
-rows/s over exactly --steps timed steps, the roofline of the dominant kernel
-(measured live with HIP events on the launch stream, first thing in the
-process: the same launch sequence as `--profile-kernel`, whose rocprofv3
-summary is committed under profiles/), a CPU baseline (the batched torch fp32
+with inputs resident in HBM, ending with the logits copied to pinned host
+memory.  Prints ONE JSON line on stdout (logs on stderr): rows/s over exactly
+--steps timed steps, the roofline of the dominant kernel (measured live with
+HIP events on the launch stream, first thing in the process after a warm-up
+of the same launches: the launch sequence of `--profile-kernel`, whose
+rocprofv3 summary is committed under profiles/), a CPU baseline (the batched torch fp32
 restatement of the reference graph on this host's cores), the single layer at
 B=1 L=32 and the long-context batch (B=64, L=512).
 
 Kernel timings use rotating buffer sets larger than the 256 MB Infinity Cache
-so that HBM, not the cache, serves the reads.
+so that HBM, not the cache, serves the reads, and time each kernel after
+0.1 s (at most 2000 launches) of its own launches (the clocks of an idle GPU
+ramp up under load).
 """
 
 from __future__ import annotations
@@ -96,12 +99,25 @@ def gemm_tile(M, N, gelu=False, cus=256):
     return tile
 
 
-def time_launches(fn, sets, iters):
+WARM_S, WARM_MAX = 0.1, 2000  # untimed launches before a kernel is timed: 0.1 s, at most 2000
+
+
+def time_launches(fn, sets, iters, warm_s=WARM_S):
     """Average duration (us) of fn(set) over `iters` launches cycling through
-    the buffer sets, between two events on the launch stream."""
+    the buffer sets, between two events on the launch stream, after `warm_s`
+    seconds (at most WARM_MAX launches) of the same launches untimed: the
+    GPU's clocks ramp up under load
+    (FFN-up at 8192 rows: 87.7 us over its first 60 launches from idle,
+    78.5-79 us sustained, 93 us after 2 s idle), so the timed launches run at
+    the clocks a busy GPU holds.  The warm-up synchronises every 32 launches,
+    so its wall time follows the GPU's."""
     import torch
-    for s in sets[:2]:
-        fn(s)
+    i, t_end = 0, time.perf_counter() + warm_s
+    while i < 2 or (time.perf_counter() < t_end and i < WARM_MAX):
+        fn(sets[i % len(sets)])
+        i += 1
+        if i % 32 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
@@ -380,8 +396,8 @@ def roofline_of(name, best, iters):
     traffic, source = profiled_traffic(name)
     return dict(kernel=name, bound=best["bound"], achieved=round(ach, 2), peak=peak, unit=unit,
                 frac=round(ach / peak, 4), traffic=traffic, traffic_source=source, avg_us=round(best["us"], 2),
-                launches=iters, measured="first in the process, the launch sequence of "
-                                        f"`bench.py --profile-kernel {name} --kernel-iters {iters}`",
+                launches=iters, measured="first in the process after a warm-up of the same launches, the launch "
+                                        f"sequence of `bench.py --profile-kernel {name} --kernel-iters {iters}`",
                 algorithmic_per_launch=best["bytes"] if best["bound"] == "hbm" else best["flops"])
 
 
