@@ -117,7 +117,9 @@ __global__ __launch_bounds__(64) void fused_attention_general_kernel(
 // L <= 512, P <= 65536).  A workgroup of 4 waves owns (b, h, 64 queries),
 // wave w queries q0 + 16 w .. + 15, and takes the keys in blocks of 128: the
 // relative bias gives each key block a workgroup of its own, the fused
-// attention walks all of them.  66 KB of LDS, so two workgroups share a CU.
+// attention walks all of them.  The bias kernel takes 49 KB of LDS and 158
+// VGPRs, so three workgroups share a CU; the fused kernel, which also stages
+// K rows in LDS and carries the softmax state, two.
 // For a key block, every pass over 128 positions of the tables computes
 // C2P = Q . posK[pass]^T (v_mfma_f32_16x16x32_f16, fp32) into an LDS table
 // [query][position], or per 16-key block P2C = K . posQ[pass]^T into a table
@@ -149,14 +151,14 @@ typedef __attribute__((address_space(3))) gen_short4_t gen_lds_short4_t;
 __device__ __forceinline__ int gen_swz(int row, int chunk) { return row * 64 + ((chunk ^ ((row >> 1) & 7)) << 3); }
 
 template <bool FUSED>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void general_mfma_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FUSED ? 2 : 3, FUSED ? 2 : 3))) void general_mfma_kernel(
     const half_t* __restrict__ q, const half_t* __restrict__ k, const half_t* __restrict__ v,
     const half_t* __restrict__ pos_key, const half_t* __restrict__ pos_query, const int32_t* __restrict__ c2p_idx,
     const int32_t* __restrict__ p2c_idx, const half_t* __restrict__ key_mask, float scale, int H, int L, int P,
     half_t* __restrict__ out) {
   __shared__ __attribute__((aligned(16))) float tab[64 * kGenStride];          // C2P [query][position]
   __shared__ __attribute__((aligned(16))) half_t rows[kGenPass * 64];          // a pass's table rows (fused: V rows)
-  __shared__ __attribute__((aligned(16))) half_t krows[16 * kGenKeyBlocks * 64];  // the key block's K rows
+  __shared__ __attribute__((aligned(16))) half_t krows[FUSED ? 16 * kGenKeyBlocks * 64 : 8];  // fused: the key block's K rows
   // Workgroup -> (b, h, query block qb, key block ky; the fused kernel takes
   // every key block).  Workgroups go to the 8 XCDs round-robin; with H a
   // multiple of 8, XCD x takes heads x H / 8 .. (x + 1) H / 8 - 1 only, so
@@ -196,8 +198,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int32_t* p2ch = p2c_idx + (int64_t)h * L * L;
   const half_t* mrow = key_mask + (int64_t)b * L;
   const int qr = qg < L ? qg : L - 1;
-  const half8_t qf0 = *reinterpret_cast<const half8_t*>(qbase + (int64_t)qr * 64 + 8 * g);
-  const half8_t qf1 = *reinterpret_cast<const half8_t*>(qbase + (int64_t)qr * 64 + 32 + 8 * g);
+  const half8_t qf0 = *reinterpret_cast<const half8_t*>(qbase + (qr * 64 + 8 * g));
+  const half8_t qf1 = *reinterpret_cast<const half8_t*>(qbase + (qr * 64 + 32 + 8 * g));
   auto clampi = [&](int x) { return x < 0 ? 0 : (x >= P ? P - 1 : x); };
   auto unpack = [](const uint32_t (&w)[2], int j) -> int { return (int)((w[j >> 1] >> (16 * (j & 1))) & 0xFFFFu); };
 
@@ -221,13 +223,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const int row = i >> 3, ch = i & 7;
       if (step < nc + npp) {
         const int prow0 = (step < nc ? c_lo + step : p_lo + step - nc) * kGenPass + row;
-        const half_t* src = (step < nc ? pkh : pqh) + (int64_t)(prow0 < P ? prow0 : P - 1) * 64;
+        const half_t* src = (step < nc ? pkh : pqh) + (prow0 < P ? prow0 : P - 1) * 64;
         pre[it] = *reinterpret_cast<const half8_t*>(src + ch * 8);
       } else {
         // V rows of keys past L are zeros (their probabilities are 0 too)
         const int key = 16 * kGenKeyBlocks * ky_ + row;
         pre[it] = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
-        if (key < L) pre[it] = *reinterpret_cast<const half8_t*>(v + ((int64_t)bh * L + key) * 64 + ch * 8);
+        if (key < L) pre[it] = *reinterpret_cast<const half8_t*>(v + (int64_t)bh * L * 64 + (key * 64 + ch * 8));
       }
     }
   };
@@ -249,15 +251,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     uint32_t c2pk[MAXKB][2], p2ck[MAXKB][2];
     int cmn = P, cmx = -1, pmn = P, pmx = -1;  // this lane's index range (valid scores only)
 #pragma unroll
+    // L is a multiple of 16, so a wave's queries all exist or none does: `ok`
+    // is uniform.  Blocks past nkb and waves past L load the indices of block
+    // nkb - 1 / query lc, in bounds and never used.
     for (int kb = 0; kb < MAXKB; ++kb) {
-      const bool ok = qg < L && kb < nkb;
-      int4 ci = {0, 0, 0, 0};
-      int pi[4] = {0, 0, 0, 0};
-      if (ok) {
-        ci = *reinterpret_cast<const int4*>(c2ph + (int64_t)qg * L + 16 * (kb0 + kb) + 4 * g);
+      const bool ok = active && kb < nkb;
+      const int kbc = kb < nkb ? kb : nkb - 1, qc = active ? qg : lc;
+      int pi[4];
+      const int4 ci = *reinterpret_cast<const int4*>(c2ph + (qc * L + 16 * (kb0 + kbc) + 4 * g));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) pi[j] = p2ch[(int64_t)(16 * (kb0 + kb) + 4 * g + j) * L + qg];
-      }
+      for (int j = 0; j < 4; ++j) pi[j] = p2ch[(16 * (kb0 + kbc) + 4 * g + j) * L + qc];
       const int c[4] = {clampi(ci.x), clampi(ci.y), clampi(ci.z), clampi(ci.w)};
       const int pc[4] = {clampi(pi[0]), clampi(pi[1]), clampi(pi[2]), clampi(pi[3])};
       c2pk[kb][0] = (uint32_t)c[0] | ((uint32_t)c[1] << 16);
@@ -295,19 +298,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     p_lo = __builtin_amdgcn_readfirstlane(pmn / kGenPass);
     npp = __builtin_amdgcn_readfirstlane(pmx / kGenPass) - p_lo + 1;
     const int nsteps = nc + npp + (FUSED ? 1 : 0);
-    fetch_rows(0, kyb);  // lands while the K rows load
-    // The key block's K rows (clamped to L - 1) into LDS.  The previous key
-    // block's last reads of krows came before its V step's barriers.
-#pragma unroll
-    for (int it = 0; it < 16 * kGenKeyBlocks * 8 / 256; ++it) {
-      const int i = t + 256 * it;
-      const int row = i >> 3, ch = i & 7;
-      const int key = 16 * kb0 + row < L ? 16 * kb0 + row : L - 1;
-      *reinterpret_cast<half8_t*>(krows + gen_swz(row, ch)) =
-          *reinterpret_cast<const half8_t*>(kbase + (int64_t)key * 64 + ch * 8);
-    }
+    fetch_rows(0, kyb);  // lands during the K loads and q.k
+    // K of the key block (keys past L clamped to L - 1).  The bias kernel
+    // keeps the fragments of its wave's p2c keys (16 kb + lc, kb = 4 kg +
+    // wave) in registers, straight from global memory; the fused kernel,
+    // whose q.k needs every key in every wave, stages the key block's K rows
+    // in LDS (the previous key block's last reads of krows came before its
+    // V step's barriers, this block's writes come after its pass_range
+    // barrier).
+    half8_t kp[MAXKB / 4][2];
     float acc[MAXKB][4];
     if constexpr (FUSED) {
+#pragma unroll
+      for (int it = 0; it < 16 * kGenKeyBlocks * 8 / 256; ++it) {
+        const int i = t + 256 * it;
+        const int row = i >> 3, ch = i & 7;
+        const int key = 16 * kb0 + row < L ? 16 * kb0 + row : L - 1;
+        *reinterpret_cast<half8_t*>(krows + gen_swz(row, ch)) =
+            *reinterpret_cast<const half8_t*>(kbase + (key * 64 + ch * 8));
+      }
       __syncthreads();  // K rows visible
       // q.k of this wave's queries (lane: query lc, keys 16 kb + 4 g + i)
 #pragma unroll
@@ -321,6 +330,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int j = 0; j < 4; ++j) acc[kb][j] = r[j];
       }
     } else {
+#pragma unroll
+      for (int kg = 0; kg < MAXKB / 4; ++kg) {
+        const int key = 16 * (kb0 + 4 * kg + wave) + lc < L ? 16 * (kb0 + 4 * kg + wave) + lc : L - 1;
+        kp[kg][0] = *reinterpret_cast<const half8_t*>(kbase + (key * 64 + 8 * g));
+        kp[kg][1] = *reinterpret_cast<const half8_t*>(kbase + (key * 64 + 32 + 8 * g));
+      }
 #pragma unroll
       for (int kb = 0; kb < MAXKB; ++kb)
 #pragma unroll
@@ -337,11 +352,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       __syncthreads();
       if (step + 1 < nsteps) fetch_rows(step + 1, kyb);  // lands during this step
+      // The packed indices stay packed across steps: unpacking them once,
+      // outside the loop, would take 32 more registers.
+#pragma unroll
+      for (int kb = 0; kb < MAXKB; ++kb) {
+        asm volatile("" : "+v"(c2pk[kb][0]), "+v"(c2pk[kb][1]), "+v"(p2ck[kb][0]), "+v"(p2ck[kb][1]));
+      }
       const int base = (step < nc ? c_lo + step : p_lo + step - nc) * kGenPass;
       if (step < nc) {
         // ---- c2p: C2P of this wave's queries, gathered by the wave itself ----
         if (active) {
-#pragma unroll 4
+#pragma unroll
           for (int tp = 0; tp < kGenPass / 16; ++tp) {
             const half8_t a0 = *reinterpret_cast<const half8_t*>(rows + gen_swz(16 * tp + lc, g));
             const half8_t a1 = *reinterpret_cast<const half8_t*>(rows + gen_swz(16 * tp + lc, 4 + g));
@@ -366,10 +387,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int kg = 0; kg < MAXKB / 4; ++kg) {
           if (4 * kg >= nkb) continue;  // uniform
           {
-            const int kb = 4 * kg + wave;  // rows past nkb hold clamped keys; never read
-            const half8_t kf0 = *reinterpret_cast<const half8_t*>(krows + gen_swz(16 * kb + lc, g));
-            const half8_t kf1 = *reinterpret_cast<const half8_t*>(krows + gen_swz(16 * kb + lc, 4 + g));
-#pragma unroll 4
+            // (blocks past nkb hold clamped keys; their P2C rows are never read)
+            half8_t kf0, kf1;
+            if constexpr (FUSED) {
+              kf0 = *reinterpret_cast<const half8_t*>(krows + gen_swz(16 * (4 * kg + wave) + lc, g));
+              kf1 = *reinterpret_cast<const half8_t*>(krows + gen_swz(16 * (4 * kg + wave) + lc, 4 + g));
+            } else {
+              kf0 = kp[kg][0], kf1 = kp[kg][1];
+            }
+#pragma unroll
             for (int tp = 0; tp < kGenPass / 16; ++tp) {
               const half8_t a0 = *reinterpret_cast<const half8_t*>(rows + gen_swz(16 * tp + lc, g));
               const half8_t a1 = *reinterpret_cast<const half8_t*>(rows + gen_swz(16 * tp + lc, 4 + g));
@@ -394,19 +420,43 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
     if constexpr (!FUSED) {
       // ---- scores: (c2p + p2c) * scale, masked keys -65504 ----
-      if (active && qg < L) {
-        half_t* orow = out + ((int64_t)bh * L + qg) * L;
+      if (active) {  // (uniform: every lane of the wave takes part in the row swaps)
+        half_t* orow = out + (int64_t)bh * L * L + qg * L;
+        // Lane (g, query lc) holds keys 4 g .. 4 g + 3 of each 16-key block.
+        // Per group of four blocks a 4 x 4 transpose across the wave's four
+        // 16-lane rows (v_permlane32_swap, then v_permlane16_swap) leaves row
+        // g with all 16 keys of block 4 m + g, stored as one 32-byte piece.
 #pragma unroll
-        for (int kb = 0; kb < MAXKB; ++kb) {
-          if (kb >= nkb) continue;
-          half4_t sv;
+        for (int m = 0; m < MAXKB / 4; ++m) {
+          if (4 * m >= nkb) continue;  // uniform
+          uint32_t x[4][2];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int key = 16 * (kb0 + kb) + 4 * g + j;
-            const float sc = acc[kb][j] * scale;
-            sv[j] = (float)mrow[key] < -60000.f ? (half_t)-65504.f : (half_t)sc;
+          for (int u = 0; u < 4; ++u) {
+            const int kb = 4 * m + u, kbc = kb < nkb ? kb : nkb - 1;  // blocks past nkb: in bounds, never stored
+            const half4_t mk = *reinterpret_cast<const half4_t*>(mrow + 16 * (kb0 + kbc) + 4 * g);
+            half4_t sv;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const float sc = acc[kb][j] * scale;
+              sv[j] = (float)mk[j] < -60000.f ? (half_t)-65504.f : (half_t)sc;
+            }
+            const uint2 w = __builtin_bit_cast(uint2, sv);
+            x[u][0] = w.x, x[u][1] = w.y;
           }
-          __builtin_nontemporal_store(sv, reinterpret_cast<half4_t*>(orow + 16 * (kb0 + kb) + 4 * g));
+#pragma unroll
+          for (int d = 0; d < 2; ++d) {
+            const auto s02 = __builtin_amdgcn_permlane32_swap(x[0][d], x[2][d], false, false);
+            const auto s13 = __builtin_amdgcn_permlane32_swap(x[1][d], x[3][d], false, false);
+            const uint32_t z0 = s02[0], z2 = s02[1], z1 = s13[0], z3 = s13[1];
+            const auto s01 = __builtin_amdgcn_permlane16_swap(z0, z1, false, false);
+            const auto s23 = __builtin_amdgcn_permlane16_swap(z2, z3, false, false);
+            x[0][d] = s01[0], x[1][d] = s01[1], x[2][d] = s23[0], x[3][d] = s23[1];
+          }
+          if (4 * m + g < nkb) {
+            half_t* dst = orow + 16 * (kb0 + 4 * m + g);
+            *reinterpret_cast<uint4*>(dst) = uint4{x[0][0], x[0][1], x[1][0], x[1][1]};
+            *reinterpret_cast<uint4*>(dst + 8) = uint4{x[2][0], x[2][1], x[3][0], x[3][1]};
+          }
         }
       }
     } else {
@@ -494,9 +544,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           }
         }
       }
-      // the next key block writes krows and `rows` only after its own
-      // barriers; this one's V reads end before the next step's first barrier
-      __syncthreads();
+      // The next key block writes pass_range and `rows` only after barriers
+      // that every wave reaches after its V reads here.
     }
   }
   if constexpr (FUSED) {
@@ -537,7 +586,7 @@ int launch_relative_bias_general(const void* q, const void* k, const void* pos_k
                                  hipStream_t stream) {
   if (B * H * L == 0) return GD_OK;
   // Indices travel packed in 16 bits, so the tables hold at most 65536 rows.
-  if (general_mfma_ok(D, L, P, error_flag, {q, k, pos_key, pos_query, c2p, p2c, out})) {
+  if (general_mfma_ok(D, L, P, error_flag, {q, k, pos_key, pos_query, c2p, p2c, key_mask, out})) {
     const dim3 grid((unsigned)(B * H * ((L + 63) / 64) * ((L / 16 + kGenKeyBlocks - 1) / kGenKeyBlocks)));
     hipLaunchKernelGGL(general_mfma_kernel<false>, grid, dim3(256), 0, stream, static_cast<const half_t*>(q),
                        static_cast<const half_t*>(k), nullptr, static_cast<const half_t*>(pos_key),
