@@ -592,14 +592,16 @@ def test_fused_attention_closed_form_indices(L):
     assert np.max(np.abs(got - want)) <= 2e-3
 
 
-@pytest.mark.parametrize("L,P,H", [(32, 512, 2), (144, 300, 2), (256, 512, 8), (512, 512, 1)])
+@pytest.mark.parametrize("L,P,H", [(32, 512, 2), (48, 200, 3), (144, 300, 2), (256, 512, 8), (512, 512, 1)])
 def test_general_index_kernels_random_indices(L, P, H):
     """gd_relative_bias and gd_fused_attention with arbitrary index tensors
     (the matrix-core kernels: D = 64, L a multiple of 16) against the
     oracle's restatement of the Metal kernels.  Per-head random indices;
     L = 144 leaves a partial key block (one 16-key block) and a query block
-    with one active wave, P = 300 a partial table pass; the last batch row
-    has every key masked (the reference's uniform softmax over -65504)."""
+    with one active wave, L = 48 three 16-key blocks (a partial group of the
+    bias kernel's four-block store transpose) and three active waves, P = 300
+    a partial table pass; the last batch row has every key masked (the
+    reference's uniform softmax over -65504)."""
     B = 3
     r = np.random.default_rng(900 + L)
     q, k, v = (r.standard_normal((B, H, L, 64)).astype(np.float16) for _ in range(3))
