@@ -115,12 +115,13 @@ __global__ __launch_bounds__(64) void fused_attention_general_kernel(
 // ---------------------------------------------------------------------------
 // The general-index kernels on the matrix cores (D = 64, L a multiple of 16,
 // L <= 512, P <= 65536).  A workgroup of 4 waves owns (b, h, 64 queries),
-// wave w queries q0 + 16 w .. + 15, and takes the keys in blocks of 128: the
+// wave w queries q0 + 16 w .. + 15, and takes the keys in blocks of 64: the
 // relative bias gives each key block a workgroup of its own, the fused
-// attention walks all of them.  The bias kernel takes 49 KB of LDS and 158
-// VGPRs, so three workgroups share a CU; the fused kernel, which also stages
-// K rows in LDS and carries the softmax state, two.
-// For a key block, every pass over 128 positions of the tables computes
+// attention walks all of them.  25 KB of LDS per workgroup; the bias kernel's
+// 86 VGPRs let five workgroups share a CU, the fused kernel's 127 (it also
+// carries the softmax state and the output) four.  Time follows occupancy:
+// the passes below are chains of LDS round trips and barriers.
+// For a key block, every pass over 64 positions of the tables computes
 // C2P = Q . posK[pass]^T (v_mfma_f32_16x16x32_f16, fp32) into an LDS table
 // [query][position], or per 16-key block P2C = K . posQ[pass]^T into a table
 // [key][position]; each score takes its two terms from the tables at its
@@ -136,12 +137,14 @@ __global__ __launch_bounds__(64) void fused_attention_general_kernel(
 // fp16 hi + lo (V rows in LDS, read transposed by ds_read_b64_tr_b16); the
 // output row is divided by the row's sum at the end.
 // ---------------------------------------------------------------------------
-constexpr int kGenPass = 128;              // table positions per pass
+constexpr int kGenPass = 64;               // table positions per pass
 constexpr int kGenStride = kGenPass + 4;   // fp32 row stride: float4 stores of 8 lanes hit 32 distinct banks
 // Column kGenPass of every table row holds -0, the term of a position outside
 // the pass (x + -0 = x for every fp32 x, signed zeros included).
 __device__ __forceinline__ int gen_col(int c) { return (unsigned)c < (unsigned)kGenPass ? c : kGenPass; }
-constexpr int kGenKeyBlocks = 8;           // 16-key blocks per key block (128 keys)
+constexpr int kGenKeyBlocks = 4;           // 16-key blocks per key block (64 keys)
+// The table-rows buffer also holds the fused kernel's K rows and V rows of a key block.
+static_assert(16 * kGenKeyBlocks == kGenPass, "a key block's K / V rows fill the table-rows buffer");
 
 typedef __attribute__((address_space(3))) void gen_lds_void_t;
 typedef __attribute__((address_space(3))) half_t gen_lds_half_t;
@@ -151,19 +154,19 @@ typedef __attribute__((address_space(3))) gen_short4_t gen_lds_short4_t;
 __device__ __forceinline__ int gen_swz(int row, int chunk) { return row * 64 + ((chunk ^ ((row >> 1) & 7)) << 3); }
 
 template <bool FUSED>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FUSED ? 2 : 3, FUSED ? 2 : 3))) void general_mfma_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FUSED ? 4 : 5, FUSED ? 4 : 5))) void general_mfma_kernel(
     const half_t* __restrict__ q, const half_t* __restrict__ k, const half_t* __restrict__ v,
     const half_t* __restrict__ pos_key, const half_t* __restrict__ pos_query, const int32_t* __restrict__ c2p_idx,
     const int32_t* __restrict__ p2c_idx, const half_t* __restrict__ key_mask, float scale, int H, int L, int P,
     half_t* __restrict__ out) {
   __shared__ __attribute__((aligned(16))) float tab[64 * kGenStride];          // C2P [query][position]
   __shared__ __attribute__((aligned(16))) half_t rows[kGenPass * 64];          // a pass's table rows (fused: V rows)
-  __shared__ __attribute__((aligned(16))) half_t krows[FUSED ? 16 * kGenKeyBlocks * 64 : 8];  // fused: the key block's K rows
   // Workgroup -> (b, h, query block qb, key block ky; the fused kernel takes
   // every key block).  Workgroups go to the 8 XCDs round-robin; with H a
   // multiple of 8, XCD x takes heads x H / 8 .. (x + 1) H / 8 - 1 only, so
   // its L2 holds just those heads' index tensors and position tables.
-  const int nqb = (L + 63) / 64, nky = (L / 16 + kGenKeyBlocks - 1) / kGenKeyBlocks;
+  constexpr int MAXKB = kGenKeyBlocks;
+  const int nqb = (L + 63) / 64, nky = (L / 16 + MAXKB - 1) / MAXKB;
   const int nky_wg = FUSED ? 1 : nky;
   int h, qb, ky, b;
   {
@@ -189,7 +192,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FUSED ? 2 :
   const int qw = qb * 64 + 16 * wave;  // the wave's first query
   const bool active = qw < L;          // uniform
   const int qg = qw + lc;              // this lane's query in the score tile (keys 4 g .. 4 g + 3 of a block)
-  constexpr int MAXKB = kGenKeyBlocks;
   const half_t* qbase = q + (int64_t)bh * L * 64;
   const half_t* kbase = k + (int64_t)bh * L * 64;
   const half_t* pkh = pos_key + (int64_t)h * P * 64;
@@ -206,9 +208,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FUSED ? 2 :
   // Steps of a key block: the passes over the posK rows that hold any c2p
   // index of the key block (passes c_lo .. c_lo + nc - 1), then the passes
   // over the posQ rows that hold any of its p2c indices (p_lo .. p_lo + npp
-  // - 1); pass p covers table rows [128 p, + 128) (rows past P repeat row
+  // - 1); pass p covers table rows [64 p, + 64) (rows past P repeat row
   // P - 1).  A pass holding no index of the block adds nothing, so it is not
-  // run (relative-position indices of a 64 x 128 tile span about 190 rows:
+  // run (relative-position indices of a 64 x 64 tile span at most 127 rows:
   // 2 or 3 passes of each table instead of all of them).  The fused kernel's
   // last step brings the key block's V rows.  A step's rows are read into
   // registers during the step before.
@@ -227,7 +229,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FUSED ? 2 :
         pre[it] = *reinterpret_cast<const half8_t*>(src + ch * 8);
       } else {
         // V rows of keys past L are zeros (their probabilities are 0 too)
-        const int key = 16 * kGenKeyBlocks * ky_ + row;
+        const int key = 16 * MAXKB * ky_ + row;
         pre[it] = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
         if (key < L) pre[it] = *reinterpret_cast<const half8_t*>(v + (int64_t)bh * L * 64 + (key * 64 + ch * 8));
       }
@@ -244,8 +246,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FUSED ? 2 :
   if (t < 64) tab[t * kGenStride + kGenPass] = -0.0f;  // visible after the first step's barriers
   for (int kyi = 0; kyi < (FUSED ? nky : 1); ++kyi) {  // uniform
     const int kyb = FUSED ? kyi : ky;
-    const int kb0 = kGenKeyBlocks * kyb;  // first 16-key block of this key block
-    const int nkb = L / 16 - kb0 < kGenKeyBlocks ? L / 16 - kb0 : kGenKeyBlocks;
+    const int kb0 = MAXKB * kyb;  // first 16-key block of this key block
+    const int nkb = L / 16 - kb0 < MAXKB ? L / 16 - kb0 : MAXKB;
     // This lane's indices, clamped and packed two per register: c2p of keys
     // 16 kb + 4 g + j at query qg, p2c of query qg at those keys.
     uint32_t c2pk[MAXKB][2], p2ck[MAXKB][2];
@@ -299,35 +301,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FUSED ? 2 :
     npp = __builtin_amdgcn_readfirstlane(pmx / kGenPass) - p_lo + 1;
     const int nsteps = nc + npp + (FUSED ? 1 : 0);
     fetch_rows(0, kyb);  // lands during the K loads and q.k
-    // K of the key block (keys past L clamped to L - 1).  The bias kernel
-    // keeps the fragments of its wave's p2c keys (16 kb + lc, kb = 4 kg +
-    // wave) in registers, straight from global memory; the fused kernel,
-    // whose q.k needs every key in every wave, stages the key block's K rows
-    // in LDS (the previous key block's last reads of krows came before its
-    // V step's barriers, this block's writes come after its pass_range
-    // barrier).
+    // K of the key block (keys past L clamped to L - 1).  Each wave keeps
+    // the fragments of its p2c keys (16 kb + lc, kb = 4 kg + wave) in
+    // registers: the bias kernel loads them from global memory; the fused
+    // kernel, whose q.k needs every key in every wave, stages the key block's
+    // K rows in the table-rows buffer first (the previous key block's last
+    // reads of that buffer, its V rows, came before this block's pass_range
+    // barrier; the first step's barrier follows these reads).
     half8_t kp[MAXKB / 4][2];
     float acc[MAXKB][4];
     if constexpr (FUSED) {
 #pragma unroll
-      for (int it = 0; it < 16 * kGenKeyBlocks * 8 / 256; ++it) {
+      for (int it = 0; it < 16 * MAXKB * 8 / 256; ++it) {
         const int i = t + 256 * it;
         const int row = i >> 3, ch = i & 7;
         const int key = 16 * kb0 + row < L ? 16 * kb0 + row : L - 1;
-        *reinterpret_cast<half8_t*>(krows + gen_swz(row, ch)) =
+        *reinterpret_cast<half8_t*>(rows + gen_swz(row, ch)) =
             *reinterpret_cast<const half8_t*>(kbase + (key * 64 + ch * 8));
       }
       __syncthreads();  // K rows visible
       // q.k of this wave's queries (lane: query lc, keys 16 kb + 4 g + i)
 #pragma unroll
       for (int kb = 0; kb < MAXKB; ++kb) {
-        const half8_t kf0 = *reinterpret_cast<const half8_t*>(krows + gen_swz(16 * kb + lc, g));
-        const half8_t kf1 = *reinterpret_cast<const half8_t*>(krows + gen_swz(16 * kb + lc, 4 + g));
+        const half8_t kf0 = *reinterpret_cast<const half8_t*>(rows + gen_swz(16 * kb + lc, g));
+        const half8_t kf1 = *reinterpret_cast<const half8_t*>(rows + gen_swz(16 * kb + lc, 4 + g));
         float4_t r = {0.f, 0.f, 0.f, 0.f};
         r = mfma16x16x32(kf0, qf0, r);
         r = mfma16x16x32(kf1, qf1, r);
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[kb][j] = r[j];
+      }
+#pragma unroll
+      for (int kg = 0; kg < MAXKB / 4; ++kg) {
+        kp[kg][0] = *reinterpret_cast<const half8_t*>(rows + gen_swz(16 * (4 * kg + wave) + lc, g));
+        kp[kg][1] = *reinterpret_cast<const half8_t*>(rows + gen_swz(16 * (4 * kg + wave) + lc, 4 + g));
       }
     } else {
 #pragma unroll
@@ -388,13 +395,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FUSED ? 2 :
           if (4 * kg >= nkb) continue;  // uniform
           {
             // (blocks past nkb hold clamped keys; their P2C rows are never read)
-            half8_t kf0, kf1;
-            if constexpr (FUSED) {
-              kf0 = *reinterpret_cast<const half8_t*>(krows + gen_swz(16 * (4 * kg + wave) + lc, g));
-              kf1 = *reinterpret_cast<const half8_t*>(krows + gen_swz(16 * (4 * kg + wave) + lc, 4 + g));
-            } else {
-              kf0 = kp[kg][0], kf1 = kp[kg][1];
-            }
+            const half8_t kf0 = kp[kg][0], kf1 = kp[kg][1];
 #pragma unroll
             for (int tp = 0; tp < kGenPass / 16; ++tp) {
               const half8_t a0 = *reinterpret_cast<const half8_t*>(rows + gen_swz(16 * tp + lc, g));
