@@ -725,6 +725,169 @@ int launch_tile(const half_t* A, const half_t* W, const half_t* bias, half_t* C,
   return GD_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Skinny products: at most 32 rows (one short sequence, a few marker rows).
+// The time of such a product is the chain of dependent MFMAs per accumulator
+// (K / 16 of them) plus how fast the workgroups stream W; the tile kernels
+// above give N / 64 workgroups with one 32 x 32 accumulator per wave.  Here
+// a workgroup of two waves owns a 32 x 16 tile (N / 16 workgroups), wave w
+// rows 16 w .. 16 w + 15 in one v_mfma_f32_16x16x16_f16 chain, and keeps
+// eight 128-deep stages of A and W in flight (96 KiB).  The 16 x 16 x 16 MFMA
+// sums the same 16 products per K slice as the 32 x 32 x 16 form, bit for bit
+// (checked on the device over wide-range and cancelling operands), and the
+// slices run in the same order, so each element has the bits the tile
+// kernels give it.
+//
+// Stage layout: rows of 128 halfs (256 B), A rows 0..31 then W rows 32..47;
+// the 16-byte chunk index is XORed with the row's low four bits, so the 16
+// rows of a fragment read at one logical chunk cover the 64 banks once.
+// ---------------------------------------------------------------------------
+constexpr int kSkBK = 128;                        // K per stage
+constexpr int kSkStages = 8;
+constexpr int kSkRows = 48;                       // 32 A rows + 16 W rows
+constexpr int kSkStage = kSkRows * kSkBK;         // halfs per stage
+constexpr int kSkLoads = kSkStage * 2 / 1024 / 2;  // 1 KiB DMA blocks per wave per stage (6)
+static_assert((kSkStages - 1) * kSkLoads < 64, "vmcnt range");
+
+__device__ __forceinline__ int sk_offset(int row, int chunk) { return row * kSkBK + ((chunk ^ (row & 15)) << 3); }
+
+template <int EPI>
+__global__ __launch_bounds__(128) void gemm_skinny_kernel(const half_t* __restrict__ A, const half_t* __restrict__ W,
+                                                         const half_t* __restrict__ bias, half_t* __restrict__ C,
+                                                         int M, int N, int K, int64_t lda, int64_t ldc) {
+  // One named array per stage: every LDS read names its buffer at compile
+  // time, so the compiler's waits cover only the DMA into that buffer.
+  __shared__ __attribute__((aligned(1024))) half_t sk0[kSkStage];
+  __shared__ __attribute__((aligned(1024))) half_t sk1[kSkStage];
+  __shared__ __attribute__((aligned(1024))) half_t sk2[kSkStage];
+  __shared__ __attribute__((aligned(1024))) half_t sk3[kSkStage];
+  __shared__ __attribute__((aligned(1024))) half_t sk4[kSkStage];
+  __shared__ __attribute__((aligned(1024))) half_t sk5[kSkStage];
+  __shared__ __attribute__((aligned(1024))) half_t sk6[kSkStage];
+  __shared__ __attribute__((aligned(1024))) half_t sk7[kSkStage];
+  static_assert(kSkStages == 8, "one named buffer per stage");
+  auto stage = [&](auto b) -> half_t* {
+    constexpr int B = decltype(b)::value;
+    if constexpr (B == 0) return sk0;
+    else if constexpr (B == 1) return sk1;
+    else if constexpr (B == 2) return sk2;
+    else if constexpr (B == 3) return sk3;
+    else if constexpr (B == 4) return sk4;
+    else if constexpr (B == 5) return sk5;
+    else if constexpr (B == 6) return sk6;
+    else return sk7;
+  };
+
+  const int tile_n = blockIdx.x;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int g = lane >> 4, r = lane & 15;
+
+  // This lane's 16-byte pieces: block j of the wave (stage block 6 w + j)
+  // holds rows 4 blk .. 4 blk + 3, lane l row 4 blk + l / 16 at physical
+  // chunk l % 16, which is logical chunk (l % 16) ^ (row & 15).  Rows past M
+  // repeat row M - 1 (never stored).  Offsets in elements, 32-bit.
+  uint32_t off[kSkLoads];
+  bool is_w[kSkLoads];
+#pragma unroll
+  for (int j = 0; j < kSkLoads; ++j) {
+    const int blk = wave * kSkLoads + j;
+    const int row = 4 * blk + (lane >> 4);
+    const int chunk = (lane & 15) ^ (row & 15);
+    is_w[j] = row >= 32;
+    if (row < 32) {
+      const int m = row < M ? row : M - 1;
+      off[j] = (uint32_t)((int64_t)m * lda + chunk * 8);
+    } else {
+      off[j] = (uint32_t)((int64_t)(tile_n * 16 + row - 32) * K + chunk * 8);
+    }
+  }
+  auto issue = [&](half_t* st, int k0) {
+#pragma unroll
+    for (int j = 0; j < kSkLoads; ++j)
+      load_lds16((is_w[j] ? W : A) + (off[j] + (uint32_t)k0), st + (wave * kSkLoads + j) * 512);
+  };
+
+  // Fragments of K slice s of a stage: lane (g, r) holds k = 16 s + 4 g ..
+  // + 3 of A row 16 w + r and of W row r; W is the MFMA A operand, so the
+  // lane accumulates C row 16 w + r at columns 4 g .. 4 g + 3 of the tile.
+  half4_t fa[2][kSkBK / 16], fw[2][kSkBK / 16];
+  auto read_frags = [&](const half_t* st, int set) {
+#pragma unroll
+    for (int s = 0; s < kSkBK / 16; ++s) {
+      const int chunk = 2 * s + (g >> 1), sub = 4 * (g & 1);
+      fa[set][s] = *reinterpret_cast<const half4_t*>(st + sk_offset(16 * wave + r, chunk) + sub);
+      fw[set][s] = *reinterpret_cast<const half4_t*>(st + sk_offset(32 + r, chunk) + sub);
+    }
+  };
+  float4_t acc = {0.f, 0.f, 0.f, 0.f};
+
+  // Every step issues exactly one stage (past the end of K the last stage is
+  // fetched again into a buffer nobody reads), so each wait is a plain
+  // vmcnt(N).
+  const int nk = K / kSkBK;
+  const int last_k0 = (nk - 1) * kSkBK;
+  // (the eight buffers as compile-time constants, in order)
+  auto each_buffer = [&](auto&& f) {
+    f(ic<0>{}), f(ic<1>{}), f(ic<2>{}), f(ic<3>{}), f(ic<4>{}), f(ic<5>{}), f(ic<6>{}), f(ic<7>{});
+  };
+  each_buffer([&](auto b) { issue(stage(b), min(decltype(b)::value * kSkBK, last_k0)); });
+  wait_vmcnt<(kSkStages - 1) * kSkLoads>();  // stage 0 landed
+  stage_barrier();
+  read_frags(stage(ic<0>{}), 0);
+
+  // Step kt on buffer B: stage kt + 1 landed everywhere and every wave is
+  // done with buffer B (its fragments were read a step earlier); B is
+  // refilled with stage kt + 8; the fragments of stage kt + 1 are read, and
+  // their LDS latency passes under the MFMA chain of stage kt, whose
+  // fragments are already in registers.
+  auto step = [&](auto b, int kt) {
+    constexpr int B = decltype(b)::value;
+    wait_vmcnt<(kSkStages - 2) * kSkLoads>();
+    stage_barrier();
+    issue(stage(b), min((kt + kSkStages) * kSkBK, last_k0));
+    read_frags(stage(ic<(B + 1) % kSkStages>{}), (B + 1) & 1);  // unused after the last step
+    // (the scheduler would otherwise pull each MFMA up to the fragment read
+    // it needs next and wait for that read inside the chain)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < kSkBK / 16; ++s)
+      acc = __builtin_amdgcn_mfma_f32_16x16x16f16(fw[B & 1][s], fa[B & 1][s], acc, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  int kt = 0;
+  for (; kt + kSkStages <= nk; kt += kSkStages) each_buffer([&](auto b) { step(b, kt + decltype(b)::value); });
+  each_buffer([&](auto b) {
+    if (kt + decltype(b)::value < nk) step(b, kt + decltype(b)::value);
+  });
+  wait_vmcnt<0>();  // every DMA landed before the workgroup's LDS is released
+
+  const int row = 16 * wave + r;
+  if (row < M) {
+    const int col = tile_n * 16 + 4 * g;
+    half4_t v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = epilogue<EPI>(acc[e], EPI != GD_EPI_NONE ? (float)bias[col + e] : 0.f);
+    *reinterpret_cast<half4_t*>(C + (int64_t)row * ldc + col) = v;
+  }
+}
+
+int launch_skinny(const half_t* A, const half_t* W, const half_t* bias, half_t* C, int M, int N, int K, int64_t lda,
+                  int64_t ldc, int epi, hipStream_t stream) {
+  const dim3 grid(N / 16), block(128);
+#define GD_SKINNY(E) \
+  hipLaunchKernelGGL((gemm_skinny_kernel<E>), grid, block, 0, stream, A, W, bias, C, M, N, K, lda, ldc)
+  switch (epi) {
+    case GD_EPI_NONE: GD_SKINNY(GD_EPI_NONE); break;
+    case GD_EPI_BIAS: GD_SKINNY(GD_EPI_BIAS); break;
+    case GD_EPI_BIAS_GELU: GD_SKINNY(GD_EPI_BIAS_GELU); break;
+    default: GD_SKINNY(GD_EPI_BIAS_RELU); break;
+  }
+#undef GD_SKINNY
+  GD_LAUNCH_CHECK();
+  return GD_OK;
+}
+
 // Correctly rounded fp16 GELU of every table entry (host, double precision).
 const std::vector<uint16_t>& gelu_table_host() {
   static const std::vector<uint16_t> tab = [] {
@@ -807,6 +970,10 @@ int launch_linear(const void* a, const void* w, const void* bias, void* c, int64
   // operands take the register-staged kernel (same accumulation order).
   if ((int64_t)(M - 1) * lda + K >= (int64_t{1} << 31) || (int64_t)N * K >= (int64_t{1} << 31))
     return launch_tile<128, 128, false>(A, Wt, Bv, Cm, M, N, K, lda, ldc, nullptr, 0, epilogue_kind, stream);
+  // At most 32 rows: 32 x 16 tiles, one MFMA chain per wave, eight stages in
+  // flight.
+  if (M <= 32 && N % 16 == 0 && K % kSkBK == 0)
+    return launch_skinny(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
   if (M >= 2048 && N % 256 == 0) {
     // Whole rounds of 256 x 256 tiles (one tile per CU) over the first rows
     // and, when the rows left over fit one round of 128 x 128 tiles, those in

@@ -142,7 +142,8 @@ def test_embedding_layer_norm():
                                    (4896, 4096, 256), (5500, 3072, 256),  # split: whole rounds + 128x128 rest
                                    (4100, 4096, 128), (5120, 4096, 128),  # GELU: one round of 320x256 tiles
                                    (4896, 4096, 64), (4200, 4096, 192),  # ... one and three K steps
-                                   (32, 3072, 1024), (7, 4096, 1024)])  # one short sequence (64 x 64 tiles)
+                                   (32, 3072, 1024), (7, 4096, 1024),  # one short sequence (32 x 16 tiles)
+                                   (17, 1024, 4096), (32, 128, 128), (5, 256, 384)])  # ... one and three K stages
 @pytest.mark.parametrize("epi", ["bias", "gelu", "relu", "none"])
 def test_linear(m, n, k, epi):
     r = np.random.default_rng(m + n + k)
@@ -189,8 +190,9 @@ def test_linear_rows_do_not_depend_on_m(epi, n, k):
     """Every GEMM kernel accumulates an element over the same K slices in the
     same order and rounds it the same way: the first rows of an 8192-row
     product (256 x 256 tiles at N = 4096, 256-row tiles at N = 1024) equal,
-    bit for bit, the same rows computed alone (7, 32 and 160 rows: the
-    64 x 64 tiles; 1500: 128 x 128 tiles at N = 4096, 64 x 64 at N = 1024;
+    bit for bit, the same rows computed alone (7 and 32 rows: the 32 x 16
+    tiles on 16 x 16 x 16 MFMAs; 160 rows: the 64 x 64 tiles; 1500: 128 x 128
+    tiles at N = 4096, 64 x 64 at N = 1024;
     4896: 320 x 256 tiles with GELU, 256 x 256 + 128 x 128 without, 160 x 128
     at N = 1024, also at K = 4096: the FFN-down shape)."""
     r = np.random.default_rng(21)
@@ -223,12 +225,12 @@ def _ordered16(a):
     return np.where(i < 0, -(i & 0x7FFF), i)
 
 
-@pytest.mark.parametrize("m,n", [(248, 256), (2048, 256), (4896, 4096), (8192, 4096)])
+@pytest.mark.parametrize("m,n", [(32, 2048), (248, 256), (2048, 256), (4896, 4096), (8192, 4096)])
 def test_gelu_epilogue_every_fp16_input(m, n):
     """x @ I^T + 0 reproduces x exactly, so the GELU epilogue sees every finite
-    fp16 value once (63488 = 248 x 256).  Every kernel (the small-M tiles at
-    M = 248, 256x128 at M = 2048, 320x256 at 4896, 256x256 at 8192) reads the
-    correctly rounded table: exact everywhere."""
+    fp16 value once (63488 = 248 x 256).  Every kernel (the 32 x 16 tiles at
+    M = 32, the small-M tiles at M = 248, 256x128 at M = 2048, 320x256 at 4896,
+    256x256 at 8192) reads the correctly rounded table: exact everywhere."""
     vals = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
     vals = vals[np.isfinite(vals)]
     x = np.zeros((m, n), np.float16)
