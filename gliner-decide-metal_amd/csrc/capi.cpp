@@ -262,6 +262,14 @@ int gd_stream_probe_add(const void* a, const void* b, void* c, int64_t n, void* 
   return launch_stream_probe_add(a, b, c, n, as_stream(stream));
 }
 
+int gd_diag_mfma_forms(const void* a, const void* w, const float* c0, float* d32, float* d16, int64_t tiles,
+                       void* stream) {
+  clear_error();
+  GD_CHECK_ARG(tiles == 0 || (a && w && c0 && d32 && d16), "null tensor pointer");
+  GD_CHECK_SHAPE(tiles >= 0 && tiles <= (int64_t{1} << 20), "tiles must be in [0, 2^20]");
+  return launch_mfma_forms(a, w, c0, d32, d16, tiles, as_stream(stream));
+}
+
 int gd_relative_index_table(int32_t* out, int32_t n, int32_t bucket_size, int32_t max_position, void* stream) {
   clear_error();
   GD_CHECK_ARG(out, "null output");

@@ -14,6 +14,10 @@ int device_cu_count();
 // Streaming reference kernel (gd_stream_probe_add): c = a + b, n fp16.
 int launch_stream_probe_add(const void* a, const void* b, void* c, int64_t n, hipStream_t stream);
 
+// gd_diag_mfma_forms: 32 x 32 x 16 and 16 x 16 x 16 MFMA forms on the same tiles.
+int launch_mfma_forms(const void* a, const void* w, const float* c0, float* d32, float* d16, int64_t tiles,
+                      hipStream_t stream);
+
 int launch_residual_layer_norm(const void* x, const void* residual, const void* gamma, const void* beta, void* out,
                                int64_t rows, int64_t cols, float eps, uint32_t flags, hipStream_t stream);
 

@@ -734,7 +734,8 @@ int launch_tile(const half_t* A, const half_t* W, const half_t* bias, half_t* C,
 // rows 16 w .. 16 w + 15 in one v_mfma_f32_16x16x16_f16 chain, and keeps
 // eight 128-deep stages of A and W in flight (96 KiB).  The 16 x 16 x 16 MFMA
 // sums the same 16 products per K slice as the 32 x 32 x 16 form, bit for bit
-// (checked on the device over wide-range and cancelling operands), and the
+// (gd_diag_mfma_forms runs both on the device; a GPU test compares them over
+// wide-range, cancelling and large-accumulator operands), and the
 // slices run in the same order, so each element has the bits the tile
 // kernels give it.
 //
@@ -1043,6 +1044,74 @@ int launch_linear(const void* a, const void* w, const void* bias, void* c, int64
   }
   if (M >= 1024) return launch_tile<128, 128, false>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
   return launch_tile<64, 128, false>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
+}
+
+
+// ---------------------------------------------------------------------------
+// gd_diag_mfma_forms: the two MFMA forms the GEMM kernels use for the same
+// 16-product K slice, one 32 x 32 output tile per wave: d32 through one
+// v_mfma_f32_32x32x16_f16, d16 through four v_mfma_f32_16x16x16_f16.  The
+// skinny GEMM is bit-identical to the tile kernels only if these agree.
+// A [t][32][16], W [t][32][16] fp16 (C = A W^T, as in gd_linear), C0 and the
+// outputs [t][32][32] fp32, row-major.
+// ---------------------------------------------------------------------------
+namespace {
+__global__ __launch_bounds__(64) void mfma_form32_kernel(const half_t* __restrict__ A, const half_t* __restrict__ W,
+                                                        const float* __restrict__ C0, float* __restrict__ D) {
+  const int64_t t = blockIdx.x;
+  const int l = threadIdx.x;
+  const half_t* a = A + t * 512;
+  const half_t* w = W + t * 512;
+  half8_t fa, fw;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    fa[i] = a[(l & 31) * 16 + 8 * (l >> 5) + i];
+    fw[i] = w[(l & 31) * 16 + 8 * (l >> 5) + i];
+  }
+  float16_t c;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) c[e] = C0[t * 1024 + (8 * (e >> 2) + 4 * (l >> 5) + (e & 3)) * 32 + (l & 31)];
+  c = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa, fw, c, 0, 0, 0);
+#pragma unroll
+  for (int e = 0; e < 16; ++e) D[t * 1024 + (8 * (e >> 2) + 4 * (l >> 5) + (e & 3)) * 32 + (l & 31)] = c[e];
+}
+
+__global__ __launch_bounds__(64) void mfma_form16_kernel(const half_t* __restrict__ A, const half_t* __restrict__ W,
+                                                        const float* __restrict__ C0, float* __restrict__ D) {
+  const int64_t t = blockIdx.x;
+  const int l = threadIdx.x;
+  const half_t* a = A + t * 512;
+  const half_t* w = W + t * 512;
+#pragma unroll
+  for (int rm = 0; rm < 2; ++rm)
+#pragma unroll
+    for (int cn = 0; cn < 2; ++cn) {
+      half4_t fa, fw;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        fa[i] = a[(16 * rm + (l & 15)) * 16 + 4 * (l >> 4) + i];
+        fw[i] = w[(16 * cn + (l & 15)) * 16 + 4 * (l >> 4) + i];
+      }
+      float4_t c;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) c[e] = C0[t * 1024 + (16 * rm + 4 * (l >> 4) + e) * 32 + 16 * cn + (l & 15)];
+      c = __builtin_amdgcn_mfma_f32_16x16x16f16(fa, fw, c, 0, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) D[t * 1024 + (16 * rm + 4 * (l >> 4) + e) * 32 + 16 * cn + (l & 15)] = c[e];
+    }
+}
+}  // namespace
+
+int launch_mfma_forms(const void* a, const void* w, const float* c0, float* d32, float* d16, int64_t tiles,
+                      hipStream_t stream) {
+  if (tiles == 0) return GD_OK;
+  hipLaunchKernelGGL(mfma_form32_kernel, dim3((unsigned)tiles), dim3(64), 0, stream, static_cast<const half_t*>(a),
+                     static_cast<const half_t*>(w), c0, d32);
+  GD_LAUNCH_CHECK();
+  hipLaunchKernelGGL(mfma_form16_kernel, dim3((unsigned)tiles), dim3(64), 0, stream, static_cast<const half_t*>(a),
+                     static_cast<const half_t*>(w), c0, d16);
+  GD_LAUNCH_CHECK();
+  return GD_OK;
 }
 
 }  // namespace gd

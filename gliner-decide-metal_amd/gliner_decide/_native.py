@@ -109,6 +109,7 @@ _SIGNATURES = {
                                        i32, i32, vp, i64, vp]),
     "gd_relative_index_table": (C.c_int, [vp, i32, i32, i32, vp]),
     "gd_stream_probe_add": (C.c_int, [vp, vp, vp, i64, vp]),
+    "gd_diag_mfma_forms": (C.c_int, [vp, vp, vp, vp, vp, i64, vp]),
     "gd_weight_store_create": (C.c_int, [C.POINTER(vp)]),
     "gd_weight_store_destroy": (None, [vp]),
     "gd_weight_store_add": (C.c_int, [vp, C.c_char_p, vp, i32, C.POINTER(i64), i32]),

@@ -25,6 +25,15 @@ extern "C" {
  * the output written once) on this device. */
 int gd_stream_probe_add(const void* a, const void* b, void* c, int64_t n, void* stream);
 
+/* The two MFMA forms of one 16-product K slice, per 32 x 32 tile t
+ * (0 <= tiles <= 2^20): d32[t] = A[t] W[t]^T + C0[t] through one
+ * v_mfma_f32_32x32x16_f16 and d16[t] through four v_mfma_f32_16x16x16_f16.
+ * a, w: fp16 [tiles][32][16]; c0, d32, d16: fp32 [tiles][32][32], row-major.
+ * The GEMM for at most 32 rows uses the second form and the tile kernels the
+ * first; their rows agree bit for bit only if d32 and d16 do. */
+int gd_diag_mfma_forms(const void* a, const void* w, const float* c0, float* d32, float* d16, int64_t tiles,
+                       void* stream);
+
 #if defined(__GNUC__)
 #pragma GCC visibility pop
 #endif

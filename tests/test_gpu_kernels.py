@@ -728,6 +728,49 @@ def test_attention_rejects_bias_output_on_chains_without_a_bias():
             fk().deberta_attention(dev(q), dev(k), dev(v), gpk, gpq, dev(mask), output="bias", score=score)
 
 
+def test_mfma_forms_agree_bit_for_bit():
+    """The GEMM for at most 32 rows runs v_mfma_f32_16x16x16_f16, the tile
+    kernels v_mfma_f32_32x32x16_f16; a row's bits do not depend on M only if
+    both forms give the same fp32 result for the same 16 products and
+    accumulator.  Checked over normal operands, exponents spread over 2^+-12,
+    pairs of products that cancel to a few ulps, and accumulators far larger
+    than the products; the 32 x 32 form is also held to the fp64 value within
+    the fp32 summation bound (so a wrong operand layout in either form
+    fails)."""
+    from gliner_decide import _native as N
+    from gliner_decide.device import stream_handle
+    r = np.random.default_rng(17)
+    T = 2048
+    a = r.standard_normal((T, 32, 16))
+    w = r.standard_normal((T, 32, 16))
+    c0 = r.standard_normal((T, 32, 32))
+    kind = np.arange(T) % 4
+    wide = kind == 1
+    a[wide] *= np.exp2(r.integers(-12, 13, size=a[wide].shape))
+    w[wide] *= np.exp2(r.integers(-12, 13, size=w[wide].shape))
+    c0[wide] *= np.exp2(r.integers(-12, 13, size=c0[wide].shape))
+    cancel = kind == 2  # product k + 8 = -(product k) (1 + ~2^-9): the slice sums to a few ulps
+    a[cancel, :, 8:] = -a[cancel, :, :8] * (1 + np.exp2(-9) * r.standard_normal((cancel.sum(), 32, 8)))
+    w[cancel, :, 8:] = w[cancel, :, :8]
+    c0[kind == 3] *= 2.0 ** 14
+    a16, w16, c32 = a.astype(np.float16), w.astype(np.float16), c0.astype(np.float32)
+    da, dw, dc = dev(a16), dev(w16), dev(c32)
+    d32 = torch.empty((T, 32, 32), dtype=torch.float32, device="cuda")
+    d16 = torch.empty_like(d32)
+    N.check(N.lib().gd_diag_mfma_forms(da.data_ptr(), dw.data_ptr(), dc.data_ptr(), d32.data_ptr(), d16.data_ptr(),
+                                       T, stream_handle()))
+    torch.cuda.synchronize()
+    g32, g16 = d32.cpu().numpy(), d16.cpu().numpy()
+    np.testing.assert_array_equal(g32.view(np.uint32), g16.view(np.uint32))
+    exact = np.einsum("tik,tjk->tij", a16.astype(np.float64), w16.astype(np.float64)) + c32.astype(np.float64)
+    scale = np.einsum("tik,tjk->tij", np.abs(a16.astype(np.float64)), np.abs(w16.astype(np.float64))) + np.abs(c32)
+    # (an fp32 sum of 17 terms: at most 17 roundings of 2^-24 relative; a
+    # wrong operand layout is off by the size of the terms)
+    err = np.abs(g32 - exact) / scale
+    print(f"mfma forms: max error {err.max() * 2.0 ** 24:.2f} units of 2^-24 of the terms' sum")
+    assert err.max() <= 17 * 2.0 ** -24
+
+
 def test_stream_probe_adds():
     """The streaming-ceiling diagnostic computes what it claims (c = a + b,
     fp16), including a tail shorter than one block."""
