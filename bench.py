@@ -62,6 +62,10 @@ def parse():
                             "general_fused_attention"],
                    help="only run this kernel (--kernel-iters launches on rotating buffers) followed by a 256 MiB "
                         "torch copy, for rocprofv3 counter runs; prints the kernel table, no JSON line")
+    p.add_argument("--profile-layer", action="store_true",
+                   help="only time one encoder layer at B=1, L=32 (gd_classifier_layer_forward, 200 calls after 10 "
+                        "untimed, a one-layer model of the same shapes), for rocprofv3 kernel traces; prints its "
+                        "time, no JSON line")
     p.add_argument("--serving", action="store_true",
                    help="time the JSONL runner instead (4096 text examples: JSON parse, schema formatting and "
                         "tokenization, H2D, forward, D2H, decode) and print its own JSON line")
@@ -530,6 +534,11 @@ def main():
         nb = calibration_copy()
         for k, v in kernels.items():
             log(f"{k}: {v['us']:.2f} us per launch over {args.kernel_iters} launches; calibration copy {nb} B")
+        return
+    if args.profile_layer:
+        cfg1 = DeBERTaV2Configuration(vocab_size=128100, num_hidden_layers=1)
+        layer = single_layer_us(GLiNERDecideClassifier(synthetic_weights(cfg1, seed=4), cfg1))
+        log(f"single layer B=1 L=32: {layer['us']:.2f} us per call over {layer['iters']} calls")
         return
     t = time.perf_counter()
     weights = synthetic_weights(cfg, seed=4)
