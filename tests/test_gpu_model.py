@@ -142,6 +142,27 @@ def test_compact_last_layer_edges():
     fast.check_device_errors()
 
 
+def test_compact_last_layer_on_skinny_tiles():
+    """Ten marker rows: the last layer's products after the attention run on
+    the 32 x 16 skinny tiles (at most 32 rows), while GD_FULL_ROWS runs them
+    on all 64 token rows with the 64 x 64 tiles.  The logits agree bit for
+    bit: both kernels accumulate every element in the same order."""
+    from gliner_decide import DecisionInput
+    fast, full, _, _ = _small_pair(seed=29)
+    r = np.random.default_rng(37)
+    B, L, Hh, O = 2, 32, 1, 5
+    ids = r.integers(1000, 3000, size=(B, L)).astype(np.int32)
+    mask = np.ones((B, L), np.float16)
+    mi = r.integers(0, L, size=(B, Hh, O)).astype(np.int32)
+    mm = np.ones((B, Hh, O), np.float32)
+    inp = DecisionInput(ids, mask, mi, mm)
+    want = full.classify_device(*inp.to_device()).float().cpu().numpy()
+    got = fast.classify_device(*inp.to_device()).float().cpu().numpy()
+    assert np.all(np.isfinite(want))
+    np.testing.assert_array_equal(got, want)
+    fast.check_device_errors()
+
+
 @pytest.mark.parametrize("L", [128, 256, 512])
 def test_row_extents_leave_logits_unchanged(L):
     """classify stops each row's attention at its extent (last unmasked or
