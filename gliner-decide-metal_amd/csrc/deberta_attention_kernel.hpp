@@ -578,7 +578,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
             // - 4 g - i of keys 4 g + i.
             float4_t madd = {0.f, 0.f, 0.f, 0.f};
             if constexpr (!NOMASK) madd = *reinterpret_cast<const float4_t*>(mask_add + k0 + 4 * g);
-            half4_t c2p, p2c;
+            half4_t c2p = {}, p2c = {};  // (the fp32 chains use c2p32 / p2c32 only)
             float4_t c2p32, p2c32;
             if constexpr (B32) {
               const float* cp = c2pf + lc * kC2PF32Stride + 15 + lc - 4 * g;
