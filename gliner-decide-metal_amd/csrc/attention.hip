@@ -570,7 +570,9 @@ __global__ void relative_index_table_kernel(int32_t* __restrict__ out, int n, in
 }
 
 // The matrix-core kernels read q, k, v and the table rows in 16-byte pieces,
-// the c2p indices four at a time and store half4 pieces of the output.
+// the c2p indices and (the bias kernel) the key mask four at a time, and
+// store 8- or 16-byte pieces of the output; both entry points hold every
+// operand to 16-byte alignment, as the header states.
 bool general_mfma_ok(int64_t D, int64_t L, int64_t P, const int32_t* error_flag,
                      std::initializer_list<const void*> ptrs) {
   if (D != 64 || L % 16 != 0 || L > 512 || P > 65536 || error_flag != nullptr) return false;
@@ -611,7 +613,7 @@ int launch_fused_attention_general(const void* q, const void* k, const void* v, 
                                    int32_t* error_flag, hipStream_t stream) {
   if (B * H * L == 0) return GD_OK;
   // Indices travel packed in 16 bits, so the tables hold at most 65536 rows.
-  if (general_mfma_ok(D, L, P, error_flag, {q, k, v, pos_key, pos_query, c2p, p2c, out})) {
+  if (general_mfma_ok(D, L, P, error_flag, {q, k, v, pos_key, pos_query, c2p, p2c, key_mask, out})) {
     const dim3 grid((unsigned)(B * H * ((L + 63) / 64)));
     hipLaunchKernelGGL(general_mfma_kernel<true>, grid, dim3(256), 0, stream, static_cast<const half_t*>(q),
                        static_cast<const half_t*>(k), static_cast<const half_t*>(v),
