@@ -208,6 +208,29 @@ def test_linear_rows_do_not_depend_on_m(epi, n, k):
         np.testing.assert_array_equal(bits(fk().linear(dev(x[:m]), dev(w), dev(b), epilogue=epi)), full[:m])
 
 
+@pytest.mark.parametrize("m", [7, 32, 300])
+def test_linear_strided_operands(m):
+    """gd_linear with lda > k and ldc > n (the skinny tiles at 7 and 32 rows,
+    the 64 x 64 tiles at 300): the padding columns of A are never read into
+    the product and those of C are never written."""
+    from gliner_decide import _native as N
+    from gliner_decide.device import stream_handle
+    n, k, lda, ldc = 256, 256, 320, 288
+    r = np.random.default_rng(m)
+    x = r.standard_normal((m, lda)).astype(np.float16)
+    x[:, k:] = np.float16(np.nan)  # read into the product, these would poison it
+    w = (r.standard_normal((n, k)) / 16).astype(np.float16)
+    b = r.standard_normal(n).astype(np.float16)
+    dx, dw, db = dev(x), dev(w), dev(b)
+    c = torch.full((m, ldc), 7.0, dtype=torch.float16, device="cuda")
+    N.check(N.lib().gd_linear(dx.data_ptr(), dw.data_ptr(), db.data_ptr(), c.data_ptr(), m, n, k, lda, ldc, None, 0,
+                              N.GD_EPI_BIAS, stream_handle()))
+    torch.cuda.synchronize()
+    got = c.cpu().numpy()
+    assert np.all(got[:, n:] == np.float16(7.0))
+    check_linear(got[:, :n], np.ascontiguousarray(x[:, :k]), w, b, "bias")
+
+
 def test_linear_row_gather():
     r = np.random.default_rng(8)
     x = r.standard_normal((500, 1024)).astype(np.float16)
