@@ -142,6 +142,8 @@ def test_embedding_layer_norm():
                                    (4896, 4096, 256), (5500, 3072, 256),  # split: whole rounds + 128x128 rest
                                    (4100, 4096, 128), (5120, 4096, 128),  # GELU: one round of 320x256 tiles
                                    (4896, 4096, 64), (4200, 4096, 192),  # ... one and three K steps
+                                   (4096, 4096, 64), (4096, 4096, 128), (8192, 4096, 192),  # 256 x 256: 1-3 K steps
+                                   (8192, 3072, 64),  # 256 x 192, one K step
                                    (32, 3072, 1024), (7, 4096, 1024),  # one short sequence (32 x 16 tiles)
                                    (17, 1024, 4096), (32, 128, 128), (5, 256, 384)])  # ... one and three K stages
 @pytest.mark.parametrize("epi", ["bias", "gelu", "relu", "none"])
