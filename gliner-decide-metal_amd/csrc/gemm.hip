@@ -952,6 +952,47 @@ int64_t gemm_cu_count() {
 }
 }  // namespace
 
+namespace {
+// Tile choice for up to 4,096 rows: a cost model fitted to a sweep of every
+// tile kernel over 160 to 4,096 rows of the encoder's four products (N =
+// 1024, 3072, 4096; K = 1024 and 4096; bias and GELU epilogues; one MI355X,
+// each choice the measured fastest at every swept point).  A tile kernel
+// that holds one workgroup per CU takes ceil(tiles / CUs) rounds of
+// a + b K / 1024 (+ g with GELU) us; the 64 x 64 tiles run two workgroups
+// per CU, each round after the first adding the fraction `s` of one.  Every
+// kernel accumulates an element the same way, so the choice changes no bit.
+struct TileCost {
+  int bm, bn;
+  float a, b, g;
+};
+constexpr TileCost kTileCosts[] = {
+    {64, 64, 3.19f, 3.32f, 1.59f},    {128, 128, 1.53f, 9.37f, 3.39f}, {160, 128, 5.86f, 8.08f, 3.88f},
+    {192, 128, 5.63f, 8.79f, 3.20f},  {256, 128, 6.88f, 10.18f, 4.83f}, {256, 192, 10.0f, 12.6f, 4.42f},
+    {256, 256, 8.44f, 16.34f, 7.79f},
+};
+
+// Index into kTileCosts of the cheapest tile for an M x N x K product.
+int cheapest_tile(int M, int N, int K, bool gelu, int64_t cus) {
+  int best = 0;
+  double best_us = 1e30;
+  const double kk = K / 1024.0;
+  for (int i = 0; i < (int)(sizeof kTileCosts / sizeof kTileCosts[0]); ++i) {
+    const TileCost& t = kTileCosts[i];
+    if (N % t.bn) continue;
+    const int64_t tiles = (int64_t)((M + t.bm - 1) / t.bm) * (N / t.bn);
+    const double rounds = (double)((tiles + cus - 1) / cus);
+    const double per = t.a + t.b * kk + (gelu ? t.g : 0.0);
+    double us = per * rounds;
+    if (t.bm == 64) {
+      const double share = K <= 1024 ? 0.57 : (K >= 4096 ? 0.73 : 0.57 + 0.16 * (K - 1024) / 3072.0);
+      us = per * (1.0 + share * (rounds - 1.0));
+    }
+    if (us < best_us) best_us = us, best = i;
+  }
+  return best;
+}
+}  // namespace
+
 int launch_linear(const void* a, const void* w, const void* bias, void* c, int64_t m, int64_t n, int64_t k, int64_t lda,
                   int64_t ldc, const int32_t* a_rows, int64_t a_row_count, int epilogue_kind, hipStream_t stream) {
   if (m == 0) return GD_OK;
@@ -975,6 +1016,17 @@ int launch_linear(const void* a, const void* w, const void* bias, void* c, int64
   // flight.
   if (M <= 32 && N % 16 == 0 && K % kSkBK == 0)
     return launch_skinny(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
+  if (M <= 4096 && N % 128 == 0 && K % 64 == 0) {
+    switch (cheapest_tile(M, N, K, epilogue_kind == GD_EPI_BIAS_GELU, gemm_cu_count())) {
+      case 0: return launch_lds_tile<64, 64, 2, 64, 4, 4>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
+      case 1: return launch_lds_tile<128, 128, 2, 64, 2>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
+      case 2: return launch_lds_tile<160, 128, 1, 64, 3, 4>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
+      case 3: return launch_lds_tile<192, 128, 2, 64, 3>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
+      case 4: return launch_lds_tile<256, 128, 4, 64, 3>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
+      case 5: return launch_lds_tile<256, 192, 4, 64, 2>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
+      default: return launch_lds_tile<256, 256, 2, 64, 2>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
+    }
+  }
   if (M >= 2048 && N % 256 == 0) {
     // Whole rounds of 256 x 256 tiles (one tile per CU) over the first rows
     // and, when the rows left over fit one round of 128 x 128 tiles, those in
@@ -1031,17 +1083,12 @@ int launch_linear(const void* a, const void* w, const void* bias, void* c, int64
     if (bm == 192) return launch_lds_tile<192, 128, 2, 64, 3>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
     return launch_lds_tile<256, 128, 4, 64, 3>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
   }
-  // Short M (classifier head, the last layer's marker rows, short buckets):
-  // DMA-pipelined tiles -- 128 x 128 (two stages) when they fill a round,
-  // else 64 x 64 tiles of four waves with four 64-deep stages in flight (64
-  // KiB: two workgroups per CU).  The register-staged kernel keeps one K step
-  // in flight, which left a 160-row K = 4096 product waiting on global
-  // latency for 55 us.
-  if (N % 64 == 0 && K % 64 == 0) {
-    if (N % 128 == 0 && (int64_t)((M + 127) / 128) * (N / 128) >= gemm_cu_count())
-      return launch_lds_tile<128, 128, 2, 64, 2>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
+  // Widths that are a multiple of 64 but not of 128: 64 x 64 DMA-pipelined
+  // tiles of four waves with four 64-deep stages in flight (the
+  // register-staged kernel keeps one K step in flight, which left a 160-row
+  // K = 4096 product waiting on global latency for 55 us).
+  if (N % 64 == 0 && K % 64 == 0)
     return launch_lds_tile<64, 64, 2, 64, 4, 4>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
-  }
   if (M >= 1024) return launch_tile<128, 128, false>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
   return launch_tile<64, 128, false>(A, Wt, Bv, Cm, M, N, K, lda, ldc, a_rows, (int)a_row_count, epilogue_kind, stream);
 }

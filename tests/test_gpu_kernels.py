@@ -144,6 +144,9 @@ def test_embedding_layer_norm():
                                    (4896, 4096, 64), (4200, 4096, 192),  # ... one and three K steps
                                    (4096, 4096, 64), (4096, 4096, 128), (8192, 4096, 192),  # 256 x 256: 1-3 K steps
                                    (8192, 3072, 64),  # 256 x 192, one K step
+                                   (792, 3072, 1024), (1100, 4096, 1024), (1400, 3072, 1024),  # up to 4,096
+                                   (1800, 4096, 1024), (2300, 2048, 1024), (2600, 1024, 1024),  # rows: the
+                                   (3500, 3072, 1024),  # cost-model tile choice
                                    (32, 3072, 1024), (7, 4096, 1024),  # one short sequence (32 x 16 tiles)
                                    (17, 1024, 4096), (32, 128, 128), (5, 256, 384)])  # ... one and three K stages
 @pytest.mark.parametrize("epi", ["bias", "gelu", "relu", "none"])
@@ -193,10 +196,12 @@ def test_linear_rows_do_not_depend_on_m(epi, n, k):
     same order and rounds it the same way: the first rows of an 8192-row
     product (256 x 256 tiles at N = 4096, 256-row tiles at N = 1024) equal,
     bit for bit, the same rows computed alone (7 and 32 rows: the 32 x 16
-    tiles on 16 x 16 x 16 MFMAs; 160 rows: the 64 x 64 tiles; 1500: 128 x 128
-    tiles at N = 4096, 64 x 64 at N = 1024;
-    4896: 320 x 256 tiles with GELU, 256 x 256 + 128 x 128 without, 160 x 128
-    at N = 1024, also at K = 4096: the FFN-down shape)."""
+    tiles on 16 x 16 x 16 MFMAs; 160 rows: the 64 x 64 tiles; 792 to 3,500:
+    the tiles the cost model picks up to 4,096 rows -- at N = 4096 128 x 128,
+    160 x 128 or 192 x 128 (GELU), 192 x 128, 256 x 128 and 256 x 256, at N =
+    1024 64 x 64, 128 x 128 and 160 x 128; 4896: 320 x 256 tiles with GELU,
+    256 x 256 + 128 x 128 without, 160 x 128 at N = 1024, also at K = 4096:
+    the FFN-down shape)."""
     r = np.random.default_rng(21)
     x = r.standard_normal((8192, k)).astype(np.float16)
     w = (r.standard_normal((n, k)) / np.sqrt(k)).astype(np.float16)
@@ -206,7 +211,7 @@ def test_linear_rows_do_not_depend_on_m(epi, n, k):
         return t.cpu().numpy().view(np.uint16)
 
     full = bits(fk().linear(dev(x), dev(w), dev(b), epilogue=epi))
-    for m in (7, 32, 160, 1500, 4896):
+    for m in (7, 32, 160, 792, 1100, 1500, 1800, 2600, 3500, 4896):
         np.testing.assert_array_equal(bits(fk().linear(dev(x[:m]), dev(w), dev(b), epilogue=epi)), full[:m])
 
 
