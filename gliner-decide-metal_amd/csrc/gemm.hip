@@ -1029,11 +1029,14 @@ int launch_linear(const void* a, const void* w, const void* bias, void* c, int64
   }
   if (M >= 2048 && N % 256 == 0) {
     // Whole rounds of 256 x 256 tiles (one tile per CU) over the first rows
-    // and, when the rows left over fit one round of 128 x 128 tiles, those in
-    // a second launch: a last round of a few large tiles is slower than one
-    // of many small ones (FFN-up at 4,896 rows: 44 + 18.5 us against 71.5 us;
-    // with GELU, one round of 320 x 256 tiles: 55.5 us).  Every kernel
-    // accumulates in the same order and reads the GELU table.
+    // and, when the rows left over fit one round of 128 x 128 tiles and would
+    // cost the 256 x 256 launch a further round, those in a second launch: a
+    // last round of a few large tiles is slower than one of many small ones
+    // (FFN-up at 4,896 rows: 44 + 18.5 us against 71.5 us; with GELU, one
+    // round of 320 x 256 tiles: 55.5 us).  Where the rest adds no round
+    // (N = 3072 on 32,768 rows: 1,536 tiles, six rounds either way) the
+    // second launch only adds its own ramp (212 against 199 us).  Every
+    // kernel accumulates in the same order and reads the GELU table.
     const int64_t cus = gemm_cu_count();
     const int64_t m_tiles_round = cus / (N / 256);
     // GELU (FFN-up) on up to 320 rows per tile row: one round of 320 x 256
@@ -1042,7 +1045,8 @@ int launch_linear(const void* a, const void* w, const void* bias, void* c, int64
       return launch_lds_tile_gelu320(A, Wt, Bv, Cm, M, N, K, lda, ldc, stream);
     const int64_t full_rows = m_tiles_round > 0 ? M / (m_tiles_round * 256) * (m_tiles_round * 256) : 0;
     const int64_t rest = M - full_rows;
-    if (full_rows > 0 && rest > 0 && (rest + 127) / 128 * (N / 128) <= cus) {
+    auto rounds256 = [&](int64_t rows) { return ((rows + 255) / 256 * (N / 256) + cus - 1) / cus; };
+    if (full_rows > 0 && rest > 0 && (rest + 127) / 128 * (N / 128) <= cus && rounds256(full_rows) < rounds256(M)) {
       const int st =
           launch_lds_tile<256, 256, 2, 64, 2>(A, Wt, Bv, Cm, (int)full_rows, N, K, lda, ldc, epilogue_kind, stream);
       if (st != GD_OK) return st;
@@ -1054,8 +1058,9 @@ int launch_linear(const void* a, const void* w, const void* bias, void* c, int64
     // 256-row tiles: 256 x 256 (two 64-deep stages, 128 KiB of LDS), 256 x 192
     // (two stages, 112 KiB) or 256 x 128 (three stages, 144 KiB), whichever
     // finishes first: rounds of one tile per CU, each costing the tile's
-    // measured time relative to a 256 x 128 tile (1.9, 1.35, 1; K = 1024 and
-    // 4096 alike).  Ties keep the larger tile.
+    // measured time per round relative to a 256 x 128 tile (1.5, 1.35, 1; K =
+    // 1024 and 4096 alike, from a sweep of every tile kernel over 4,896 to
+    // 32,768 rows).  Ties keep the larger tile.
     const int64_t cus = gemm_cu_count();
     auto rounds = [&](int bm, int bn) { return (double)((((M + bm - 1) / bm) * (N / bn) + cus - 1) / cus); };
     // One round of 160 x 128 tiles of four waves (each wave 160 x 32, three
@@ -1077,7 +1082,16 @@ int launch_linear(const void* a, const void* w, const void* bias, void* c, int64
       bm = 256, bn = 192;
       best = rounds(256, 192) * 1.35;
     }
-    if (N % 256 == 0 && rounds(256, 256) * 1.9 <= best) bm = 256, bn = 256;
+    if (N % 256 == 0 && rounds(256, 256) * 1.5 <= best) {
+      bm = 256, bn = 256;
+      best = rounds(256, 256) * 1.5;
+    }
+    // With GELU, 320 x 256 tiles (two stages, 144 KiB, the table under the K
+    // loop) at about 1.95 of a 256 x 128 tile: FFN-up on 8,193 to 10,240
+    // rows takes two rounds of them against three of 256 x 256 (9,500 rows:
+    // 105.3 -> 93.6 us).
+    if (epilogue_kind == GD_EPI_BIAS_GELU && N % 256 == 0 && rounds(320, 256) * 1.95 < best)
+      return launch_lds_tile_gelu320(A, Wt, Bv, Cm, M, N, K, lda, ldc, stream);
     if (bn == 256) return launch_lds_tile<256, 256, 2, 64, 2>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
     if (bn == 192) return launch_lds_tile<256, 192, 4, 64, 2>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
     if (bm == 192) return launch_lds_tile<192, 128, 2, 64, 3>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);

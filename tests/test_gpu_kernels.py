@@ -147,6 +147,8 @@ def test_embedding_layer_norm():
                                    (792, 3072, 1024), (1100, 4096, 1024), (1400, 3072, 1024),  # up to 4,096
                                    (1800, 4096, 1024), (2300, 2048, 1024), (2600, 1024, 1024),  # rows: the
                                    (3500, 3072, 1024),  # cost-model tile choice
+                                   (9500, 4096, 1024), (11835, 1024, 4096),  # 320 x 256 (GELU) and
+                                   (16384, 3072, 1024),  # 256 x 256 tiles over several rounds
                                    (32, 3072, 1024), (7, 4096, 1024),  # one short sequence (32 x 16 tiles)
                                    (17, 1024, 4096), (32, 128, 128), (5, 256, 384)])  # ... one and three K stages
 @pytest.mark.parametrize("epi", ["bias", "gelu", "relu", "none"])
