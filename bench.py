@@ -54,6 +54,8 @@ def parse():
     p.add_argument("--compiled", action="store_true", help="replay a captured hipGraph per step")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-bucket-mix", action="store_true", help="skip the mixed-length throughput field")
+    p.add_argument("--bucket-mix", action="store_true",
+                   help="only the mixed-length workload (4096 rows over the L32..L512 buckets), its own JSON line")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--kernel-iters", type=int, default=60)
     p.add_argument("--profile-kernel", default=None,
@@ -554,6 +556,17 @@ def main():
         return
     model = GLiNERDecideClassifier(weights, cfg, use_compiled_graph=args.compiled)
     log(f"model on device: {model.device_bytes / 2**20:.0f} MiB")
+    if args.bucket_mix:
+        mix = bucket_mix_rate(model)
+        log(f"bucket mix: {mix}")
+        print(json.dumps({"metric": "rows/s, bucket mix (B=32 batches over L32..L512), 24L encoder + cls head",
+                          "value": mix["value"], "unit": "rows/s", "n_gpus": 1, "higher_is_better": True,
+                          "dtype": "f16", "data": "synthetic (seeded ids/lengths; random-init weights)",
+                          "config": {"workload": "bucket mix: 4096 rows, lengths exp(U(ln 8, ln 512)), 1-2 tasks x "
+                                                 "2-10 labels, packed rows", "batch": 32,
+                                     "compiled_graph": args.compiled},
+                          "bucket_mix": mix}), flush=True)
+        return
     if args.workload == "classify":
         batch = classification_batch(seed=4)
         wl = dict(workload="24L DeBERTa-v3-large encoder + GLiNER classifier head, B=32 L=256 "
