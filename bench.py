@@ -78,10 +78,13 @@ def parse():
 # live kernel timing
 # ---------------------------------------------------------------------------
 def gemm_tile(M, N, gelu=False, cus=256):
-    """The tile launch_linear picks for M >= 2048 rows (gemm.hip): one round
+    """The tile launch_linear picks above 4,096 rows (gemm.hip): one round
     of 320x256 (GELU) or 160x128 (four waves, no GELU) tiles where it fits,
-    whole rounds of 256x256 plus a 128x128 remainder, or the fewest rounds
-    of tiles weighted by their relative cost."""
+    whole rounds of 256x256 plus a 128x128 remainder where the remainder
+    would cost the 256x256 launch a further round, or the fewest rounds of
+    tiles weighted by their relative cost."""
+    def rounds(bm, bn):
+        return -(-(-(-M // bm) * (N // bn)) // cus)
     if N % 256 == 0:
         per_round = cus // (N // 256)
         if gelu and per_round * 256 < M <= per_round * 320:
@@ -89,19 +92,21 @@ def gemm_tile(M, N, gelu=False, cus=256):
         full = M // (per_round * 256) * (per_round * 256) if per_round else 0
         rest = M - full
         if full > 0 and rest > 0 and (rest + 127) // 128 * (N // 128) <= cus:
-            return "256,256 + 128,128"
+            def rounds256(rows):
+                return -(-(-(-rows // 256) * (N // 256)) // cus)
+            if rounds256(full) < rounds256(M):
+                return "256,256 + 128,128"
     if not gelu and -(-M // 160) * (N // 128) <= cus:
         return "160,128"
-
-    def rounds(bm, bn):
-        return -(-(-(-M // bm) * (N // bn)) // cus)
     tile, best = "256,128", rounds(256, 128)
     if rounds(192, 128) * 0.8 < best:
         tile, best = "192,128", rounds(192, 128) * 0.8
     if N % 192 == 0 and rounds(256, 192) * 1.35 <= best:
         tile, best = "256,192", rounds(256, 192) * 1.35
-    if N % 256 == 0 and rounds(256, 256) * 1.9 <= best:
-        tile = "256,256"
+    if N % 256 == 0 and rounds(256, 256) * 1.5 <= best:
+        tile, best = "256,256", rounds(256, 256) * 1.5
+    if gelu and N % 256 == 0 and rounds(320, 256) * 1.95 < best:
+        tile = "320,256"
     return tile
 
 
