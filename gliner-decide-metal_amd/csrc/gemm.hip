@@ -5,23 +5,30 @@
 // follow the intermediate and classifier projections (DeBERTa.swift:421,437).
 //
 // gfx950 design.  Both operands are K-contiguous (A is [M, K] row-major, W is
-// [N, K] row-major), so every MFMA fragment is one 16-byte row segment.  A
-// block of 256 threads (4 waves, 2 x 2) owns a BM x BN tile and walks K in
-// steps of 64:
-//   * global -> registers -> LDS, double-buffered: the loads of step k+1 are
-//     in flight while the MFMAs of step k run;
-//   * LDS rows are 128 B (64 halfs) with the 16-byte chunk index XOR-swizzled
-//     by bits 1..3 of the row, so a fragment read of 16 consecutive rows
-//     covers all 64 banks once (no conflicts on ds_read_b128);
-//   * each wave runs v_mfma_f32_32x32x16_f16 over a (BM/2) x (BN/2) sub-tile
-//     with fp32 accumulators;
-//   * the epilogue adds the bias, rounds to fp16 (the addMM output) and
-//     applies GELU (the correctly rounded fp16 GELU of that fp16 value, from a
-//     table) or ReLU -- the two fp16 rounding points of `gelu(linear(x))` in
-//     the reference graph.
-//   * workgroups are dispatched round-robin over the 8 XCDs; the tile order is
-//     remapped so each XCD works on a compact 4-tile-row band and its private
-//     L2 serves the A rows and W columns it shares.
+// [N, K] row-major), so every MFMA fragment is one 16-byte row segment, and
+// the epilogue adds the bias, rounds to fp16 (the addMM output) and applies
+// GELU (the correctly rounded fp16 GELU of that fp16 value, from a table) or
+// ReLU -- the two fp16 rounding points of `gelu(linear(x))` in the reference
+// graph.  Three kernel families:
+//   * gemm_nt_lds_kernel, the main path: tiles from 64 x 64 to 320 x 256 of
+//     4 or 8 waves, operands brought into LDS by direct-to-LDS DMA
+//     (global_load_lds_dwordx4) two to five 64-deep stages ahead, 128-byte
+//     LDS rows with an XOR swizzle (conflict-free ds_read_b128 fragments),
+//     v_mfma_f32_32x32x16_f16 with fp32 accumulators, the output staged
+//     through LDS into coalesced row segments;
+//   * gemm_skinny_kernel for at most 32 rows (one short sequence): 32 x 16
+//     tiles of two waves on v_mfma_f32_16x16x16_f16, eight 128-deep stages;
+//   * gemm_nt_kernel, register-staged (global -> registers -> LDS, one K step
+//     ahead): operands whose rows are gathered through an index list (the
+//     classifier's marker rows) or that exceed 32-bit element offsets.
+// Every kernel accumulates an element over the same 16-wide K slices in the
+// same order, so a row's bits do not depend on M or on the kernel chosen.
+// launch_linear chooses the kernel and tile: up to 4,096 rows by a cost model
+// fitted to a sweep of every tile kernel, above that by rounds of tiles per
+// CU weighted by each tile's measured cost.  Workgroups are dispatched
+// round-robin over the 8 XCDs; the tile order is remapped so each XCD works
+// on a compact 4-tile-row band and its private L2 serves the A rows and W
+// columns it shares.
 #include <atomic>
 #include <cmath>
 #include <cstring>
