@@ -119,6 +119,11 @@ __device__ __forceinline__ half_t epilogue(float acc, float b) {
   return y > (half_t)0 ? y : (half_t)0;
 }
 
+// Register-staged tiles: a block of 256 threads (4 waves, 2 x 2) owns a
+// BM x BN tile and walks K in steps of 64, global -> registers -> LDS double
+// buffered (the loads of step k + 1 in flight while the MFMAs of step k
+// run), each wave on a (BM/2) x (BN/2) sub-tile.  With GATHER, A row i is
+// row a_rows[i] of the operand (the classifier's marker rows).
 template <int BM, int BN, int EPI, bool GATHER>
 __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(const half_t* __restrict__ A, const half_t* __restrict__ W,
                                                            const half_t* __restrict__ bias, half_t* __restrict__ C,
