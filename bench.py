@@ -79,7 +79,7 @@ def parse():
 # ---------------------------------------------------------------------------
 def gemm_tile(M, N, gelu=False, cus=256):
     """The tile launch_linear picks above 4,096 rows (gemm.hip): one round
-    of 320x256 (GELU) or 160x128 (four waves, no GELU) tiles where it fits,
+    of 320x256 (GELU) or 160x128 (eight waves, no GELU) tiles where it fits,
     whole rounds of 256x256 plus a 128x128 remainder where the remainder
     would cost the 256x256 launch a further round, or the fewest rounds of
     tiles weighted by their relative cost."""
@@ -303,7 +303,9 @@ def measure_kernels(model_cfg, iters, only=None):
 
         us = time_launches(lin, [0], iters)
         flops = 2 * T * n * k
-        out[name] = dict(kernel=f"gemm_nt_lds_kernel<{gemm_tile(T, n, epi == 'gelu')}>", shape=[T, n, k], us=us, flops=flops,
+        tile = gemm_tile(T, n, epi == 'gelu')
+        kname = "gemm_lds_split160_kernel" if tile == "160,128" else f"gemm_nt_lds_kernel<{tile}>"
+        out[name] = dict(kernel=kname, shape=[T, n, k], us=us, flops=flops,
                          tflops=flops / us / 1e6, bound="mfma", launches_per_step=24,
                          bytes=(T * k + n * k + T * n) * 2)
         del a, w, c

@@ -15,7 +15,9 @@
 //     (global_load_lds_dwordx4) two to five 64-deep stages ahead, 128-byte
 //     LDS rows with an XOR swizzle (conflict-free ds_read_b128 fragments),
 //     v_mfma_f32_32x32x16_f16 with fp32 accumulators, the output staged
-//     through LDS into coalesced row segments;
+//     through LDS into coalesced row segments; gemm_lds_split160_kernel is
+//     its 160 x 128 tile on eight waves of unequal row counts (bias
+//     epilogues);
 //   * gemm_skinny_kernel for at most 32 rows (one short sequence): 32 x 16
 //     tiles of two waves on v_mfma_f32_16x16x16_f16, eight 128-deep stages;
 //   * gemm_nt_kernel, register-staged (global -> registers -> LDS, one K step
@@ -697,6 +699,203 @@ int launch_lds_tile(const half_t* A, const half_t* W, const half_t* bias, half_t
   return GD_OK;
 }
 
+// 160 x 128 tiles of eight waves (three 64-deep stages, 108 KiB) for the bias
+// epilogues: the rows split unevenly, a wave taking three or two 32-row groups
+// of one 32-column strip (rows 0-95 or 96-159), so that every SIMD holds one
+// wave of each kind and two waves cover each other's LDS and barrier waits,
+// where the four-wave form of the tile has one wave per SIMD.  Stage layout,
+// DMA order, fragment reads, K order and epilogue are gemm_nt_lds_kernel's.
+template <int EPI>
+__global__ __launch_bounds__(512) void gemm_lds_split160_kernel(const half_t* __restrict__ A,
+                                                               const half_t* __restrict__ W,
+                                                               const half_t* __restrict__ bias,
+                                                               half_t* __restrict__ C, int M, int N, int K,
+                                                               int64_t lda, int64_t ldc, int tiles_m, int tiles_n) {
+  constexpr int BM = 160, BN = 128, BK = 64, NSTAGE = 3, NT = 512;
+  using Lay = StageLayout<BK>;
+  constexpr int WN = 32, TN = 1;
+  constexpr int B_BLK = BN / Lay::kRowsPerBlock / 8;  // 1 KiB W blocks per wave per stage
+  constexpr int STAGE = (BM + BN) * BK;
+  constexpr int S = BK / 16;
+  constexpr int RPA = STAGE / BN / 32 * 32;  // epilogue rows per stage buffer
+  static_assert(EPI != GD_EPI_BIAS_GELU, "bias epilogues only");
+  static_assert(BM / Lay::kRowsPerBlock == 4 * 3 + 4 * 2 && B_BLK == 2, "A blocks: four waves take 3, four take 2");
+  static_assert(NSTAGE * RPA >= BM && RPA % 32 == 0, "epilogue staging must fit in the stage buffers");
+  __shared__ __attribute__((aligned(1024))) half_t st0[STAGE];
+  __shared__ __attribute__((aligned(1024))) half_t st1[STAGE];
+  __shared__ __attribute__((aligned(1024))) half_t st2[STAGE];
+  auto stage = [&](auto b) -> half_t* {
+    constexpr int B = decltype(b)::value;
+    if constexpr (B == 0) return st0;
+    else if constexpr (B == 1) return st1;
+    else return st2;
+  };
+
+  const int nwg = tiles_m * tiles_n;
+  int bid = blockIdx.x;
+  if ((nwg & 7) == 0) bid = (bid & 7) * (nwg >> 3) + (bid >> 3);
+  const int band = bid / (kGroupM * tiles_n);
+  const int first_m = band * kGroupM;
+  const int gm = min(kGroupM, tiles_m - first_m);
+  const int in_band = bid - band * kGroupM * tiles_n;
+  const int tile_m = first_m + in_band % gm;
+  const int tile_n = in_band / gm;
+
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wn = wave >> 1;  // column strip
+  const int lr = lane & 31, lk = lane >> 5;
+
+  // A wave of TM row groups from row wrow0, its A blocks a_blk0 .. a_blk0 + TM - 1.
+  auto run = [&](auto tm_c, const int wrow0, const int a_blk0) {
+    constexpr int TM = decltype(tm_c)::value;
+    constexpr int A_BLK = TM;
+    constexpr int LPS = A_BLK + B_BLK;
+    uint32_t a_off[A_BLK], b_off[B_BLK];
+#pragma unroll
+    for (int j = 0; j < A_BLK; ++j) {
+      const int blk = a_blk0 + j;
+      int m = tile_m * BM + blk * Lay::kRowsPerBlock + lane / Lay::kChunks;
+      m = m < M ? m : M - 1;
+      a_off[j] = (uint32_t)((int64_t)m * lda + Lay::dma_chunk(lane, blk) * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < B_BLK; ++j) {
+      const int blk = wave * B_BLK + j;
+      const int n = tile_n * BN + blk * Lay::kRowsPerBlock + lane / Lay::kChunks;
+      b_off[j] = (uint32_t)((int64_t)n * K + Lay::dma_chunk(lane, blk) * 8);
+    }
+    auto issue = [&](half_t* st, int k0) {
+#pragma unroll
+      for (int j = 0; j < A_BLK; ++j) load_lds16(A + (a_off[j] + (uint32_t)k0), st + (a_blk0 + j) * 512);
+#pragma unroll
+      for (int j = 0; j < B_BLK; ++j)
+        load_lds16(W + (b_off[j] + (uint32_t)k0), st + BM * BK + (wave * B_BLK + j) * 512);
+    };
+
+    float16_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][0][e] = 0.f;
+    half8_t fa[2][TM], fb[2][TN];
+    const int swz = (lr / Lay::kRowsPer256) & (Lay::kChunks - 1);
+    const int lane_off = lr * BK + 8 * (lk ^ (swz & 1)) + 16 * (swz >> 1);
+    const int a_frag0 = wrow0 * BK, b_frag0 = BM * BK + wn * WN * BK;
+    auto read_frags = [&](const half_t* st, int slice, int set) {
+      const int lo = lane_off ^ (16 * slice);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[set][i] = *reinterpret_cast<const half8_t*>(st + a_frag0 + i * 32 * BK + lo);
+      fb[set][0] = *reinterpret_cast<const half8_t*>(st + b_frag0 + lo);
+    };
+    auto mma = [&](int set) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) acc[i][0] = mfma32x32x16(fb[set][0], fa[set][i], acc[i][0]);
+    };
+    auto interleave = [&]() {
+#pragma unroll
+      for (int r = 0; r < TM + TN; ++r) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    };
+
+    const int nk = K / BK;
+    const int last_k0 = (nk - 1) * BK;
+    issue(st0, 0);
+    issue(st1, min(BK, last_k0));
+    issue(st2, min(2 * BK, last_k0));
+    wait_vmcnt<(NSTAGE - 1) * LPS>();  // stage 0 landed
+    stage_barrier();
+    read_frags(st0, 0, 0);
+    auto step = [&](auto b, int kt) {
+      constexpr int B = decltype(b)::value;
+#pragma unroll
+      for (int s = 0; s + 1 < S; ++s) {
+        read_frags(stage(b), s + 1, (s + 1) & 1);
+        mma(s & 1);
+        interleave();
+      }
+      wait_vmcnt<(NSTAGE - 2) * LPS>();
+      stage_barrier();
+      issue(stage(b), min((kt + NSTAGE) * BK, last_k0));
+      read_frags(stage(ic<(B + 1) % NSTAGE>{}), 0, 0);
+      mma((S - 1) & 1);
+      interleave();
+    };
+    int kt = 0;
+    for (; kt + NSTAGE <= nk; kt += NSTAGE) {
+      step(ic<0>{}, kt);
+      step(ic<1>{}, kt + 1);
+      step(ic<2>{}, kt + 2);
+    }
+    if (kt < nk) step(ic<0>{}, kt);
+    if (kt + 1 < nk) step(ic<1>{}, kt + 1);
+    wait_vmcnt<0>();
+    __syncthreads();
+
+    // Epilogue as in gemm_nt_lds_kernel: rows [p RPA, (p + 1) RPA) of the
+    // tile staged in stage buffer p, 8-byte unit u of row r at u ^ (r & 15).
+    constexpr int UPR = BN / 4;
+    auto unit_of = [&](int q) { return (wn * WN) / 4 + 2 * q + lk; };
+    float bq[4][4];
+    if constexpr (EPI != GD_EPI_NONE) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bq[q][e] = (float)bias[tile_n * BN + 4 * unit_of(q) + e];
+    }
+    auto rows_of = [&](int p) -> half_t* { return p == 0 ? st0 : (p == 1 ? st1 : st2); };
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int rb = wrow0 + i * 32;
+      half_t* Cs = rows_of(rb / RPA) + (rb % RPA + lr) * BN;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        half4_t v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = epilogue<EPI>(acc[i][0][4 * q + e], EPI != GD_EPI_NONE ? bq[q][e] : 0.f);
+        *reinterpret_cast<half4_t*>(Cs + 4 * (unit_of(q) ^ (lr & 15))) = v;
+      }
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int idx = t; idx < BM * UPR; idx += NT) {
+      const int r = idx / UPR, u = idx - r * UPR;
+      const int row = tile_m * BM + r;
+      if (row < M) {
+        const half4_t v = *reinterpret_cast<const half4_t*>(rows_of(r / RPA) + (r % RPA) * BN + 4 * (u ^ (r & 15)));
+        __builtin_nontemporal_store(v, reinterpret_cast<half4_t*>(C + (int64_t)row * ldc + tile_n * BN + 4 * u));
+      }
+    }
+  };
+  // Waves 0, 2, 5 and 7 take three row groups, 1, 3, 4 and 6 two: one of each
+  // on a SIMD whether a workgroup's waves are dealt to the SIMDs in turn or in
+  // pairs.
+  if (((wave ^ (wave >> 2)) & 1) == 0) run(ic<3>{}, 0, 5 * wn);
+  else run(ic<2>{}, 96, 5 * wn + 3);
+}
+
+int launch_lds_split160(const half_t* A, const half_t* W, const half_t* bias, half_t* C, int M, int N, int K,
+                        int64_t lda, int64_t ldc, int epi, hipStream_t stream) {
+  const int tiles_m = (M + 159) / 160;
+  const int tiles_n = N / 128;
+  const dim3 grid(tiles_m * tiles_n), block(512);
+#define GD_SPLIT_GEMM(E)                                                                                 \
+  hipLaunchKernelGGL((gemm_lds_split160_kernel<E>), grid, block, 0, stream, A, W, bias, C, M, N, K, lda, ldc, \
+                     tiles_m, tiles_n)
+  switch (epi) {
+    case GD_EPI_NONE: GD_SPLIT_GEMM(GD_EPI_NONE); break;
+    case GD_EPI_BIAS: GD_SPLIT_GEMM(GD_EPI_BIAS); break;
+    default: GD_SPLIT_GEMM(GD_EPI_BIAS_RELU); break;
+  }
+#undef GD_SPLIT_GEMM
+  GD_LAUNCH_CHECK();
+  return GD_OK;
+}
+
 // 320 x 256 tiles (two 64-deep stages, 144 KiB), GELU epilogue only: one
 // round over up to 320 rows per tile row where 256-row tiles need a second.
 int launch_lds_tile_gelu320(const half_t* A, const half_t* W, const half_t* bias, half_t* C, int M, int N, int K,
@@ -1035,7 +1234,9 @@ int launch_linear(const void* a, const void* w, const void* bias, void* c, int64
     switch (cheapest_tile(M, N, K, epilogue_kind == GD_EPI_BIAS_GELU, gemm_cu_count())) {
       case 0: return launch_lds_tile<64, 64, 2, 64, 4, 4>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
       case 1: return launch_lds_tile<128, 128, 2, 64, 2>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
-      case 2: return launch_lds_tile<160, 128, 1, 64, 3, 4>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
+      case 2:
+        if (epilogue_kind != GD_EPI_BIAS_GELU) return launch_lds_split160(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
+        return launch_lds_tile<160, 128, 1, 64, 3, 4>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
       case 3: return launch_lds_tile<192, 128, 2, 64, 3>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
       case 4: return launch_lds_tile<256, 128, 4, 64, 3>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
       case 5: return launch_lds_tile<256, 192, 4, 64, 2>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
@@ -1078,12 +1279,13 @@ int launch_linear(const void* a, const void* w, const void* bias, void* c, int64
     // 32,768 rows).  Ties keep the larger tile.
     const int64_t cus = gemm_cu_count();
     auto rounds = [&](int bm, int bn) { return (double)((((M + bm - 1) / bm) * (N / bn) + cus - 1) / cus); };
-    // One round of 160 x 128 tiles of four waves (each wave 160 x 32, three
-    // stages, 108 KiB) where it fits: out-proj and FFN-down on up to 5,120
-    // packed rows run 248 tiles instead of 208 larger ones (FFN-down at
-    // 4,896 rows 49.6 -> 47.0 us, out-proj 16.2 -> 15.9 us).
+    // One round of 160 x 128 tiles (three stages, 108 KiB) where it fits:
+    // out-proj and FFN-down on up to 5,120 packed rows run 248 tiles instead
+    // of 208 larger ones (FFN-down at 4,896 rows 49.6 -> 47.0 us, out-proj
+    // 16.2 -> 15.9 us with four waves; eight waves, rows split 96 / 64:
+    // out-proj 15.2 us, FFN-down at 2,600 and 3,500 rows 3% less).
     if (epilogue_kind != GD_EPI_BIAS_GELU && N % 128 == 0 && (M + 159) / 160 * (N / 128) <= cus)
-      return launch_lds_tile<160, 128, 1, 64, 3, 4>(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
+      return launch_lds_split160(A, Wt, Bv, Cm, M, N, K, lda, ldc, epilogue_kind, stream);
     int bm = 256, bn = 128;
     double best = rounds(256, 128);
     // 192 x 128 tiles (three stages, 120 KiB) fill a round that 256-row

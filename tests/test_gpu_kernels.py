@@ -138,6 +138,7 @@ def test_embedding_layer_norm():
 @pytest.mark.parametrize("m,n,k", [(1, 128, 64), (65, 256, 128), (300, 1024, 1024), (1000, 384, 192),
                                    (160, 1024, 4096), (160, 4096, 1024), (37, 2048, 1024),
                                    (4096, 1024, 256), (4896, 1024, 4096),  # one round of 160x128 tiles
+                                   (5000, 1024, 64), (4920, 1024, 128),  # ... 1-2 K steps, partial last tiles
                                    (8192, 3072, 1024), (8192, 4096, 1024),
                                    (4896, 4096, 256), (5500, 3072, 256),  # split: whole rounds + 128x128 rest
                                    (4100, 4096, 128), (5120, 4096, 128),  # GELU: one round of 320x256 tiles
@@ -202,8 +203,8 @@ def test_linear_rows_do_not_depend_on_m(epi, n, k):
     the tiles the cost model picks up to 4,096 rows -- at N = 4096 128 x 128,
     160 x 128 or 192 x 128 (GELU), 192 x 128, 256 x 128 and 256 x 256, at N =
     1024 64 x 64, 128 x 128 and 160 x 128; 4896: 320 x 256 tiles with GELU,
-    256 x 256 + 128 x 128 without, 160 x 128 at N = 1024, also at K = 4096:
-    the FFN-down shape)."""
+    256 x 256 + 128 x 128 without, 160 x 128 at N = 1024 (eight waves of three
+    or two row groups), also at K = 4096: the FFN-down shape)."""
     r = np.random.default_rng(21)
     x = r.standard_normal((8192, k)).astype(np.float16)
     w = (r.standard_normal((n, k)) / np.sqrt(k)).astype(np.float16)
@@ -217,14 +218,15 @@ def test_linear_rows_do_not_depend_on_m(epi, n, k):
         np.testing.assert_array_equal(bits(fk().linear(dev(x[:m]), dev(w), dev(b), epilogue=epi)), full[:m])
 
 
-@pytest.mark.parametrize("m", [7, 32, 300])
-def test_linear_strided_operands(m):
+@pytest.mark.parametrize("m,n", [(7, 256), (32, 256), (300, 256), (4200, 1024)])
+def test_linear_strided_operands(m, n):
     """gd_linear with lda > k and ldc > n (the skinny tiles at 7 and 32 rows,
-    the 64 x 64 tiles at 300): the padding columns of A are never read into
-    the product and those of C are never written."""
+    the 64 x 64 tiles at 300, the eight-wave 160 x 128 tiles at 4,200): the
+    padding columns of A are never read into the product and those of C are
+    never written."""
     from gliner_decide import _native as N
     from gliner_decide.device import stream_handle
-    n, k, lda, ldc = 256, 256, 320, 288
+    k, lda, ldc = 256, 320, n + 32
     r = np.random.default_rng(m)
     x = r.standard_normal((m, lda)).astype(np.float16)
     x[:, k:] = np.float16(np.nan)  # read into the product, these would poison it
