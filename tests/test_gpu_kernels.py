@@ -139,6 +139,7 @@ def test_embedding_layer_norm():
                                    (160, 1024, 4096), (160, 4096, 1024), (37, 2048, 1024),
                                    (4096, 1024, 256), (4896, 1024, 4096),  # one round of 160x128 tiles
                                    (5000, 1024, 64), (4920, 1024, 128),  # ... 1-2 K steps, partial last tiles
+                                   (4896, 3072, 1024), (4200, 3072, 64), (5100, 3072, 128),  # QKV: one round of 256x256
                                    (8192, 3072, 1024), (8192, 4096, 1024),
                                    (4896, 4096, 256), (5500, 3072, 256),  # split: whole rounds + 128x128 rest
                                    (4100, 4096, 128), (5120, 4096, 128),  # GELU: one round of 320x256 tiles
@@ -192,19 +193,21 @@ def check_linear(out, x, w, b, epi):
         assert np.mean(out != O.f16(y)) < 5e-3
 
 
-@pytest.mark.parametrize("epi,n,k", [("bias", 4096, 1024), ("gelu", 4096, 1024), ("bias", 1024, 1024),
-                                     ("bias", 1024, 4096)])
+@pytest.mark.parametrize("epi,n,k", [("bias", 4096, 1024), ("gelu", 4096, 1024), ("bias", 3072, 1024),
+                                     ("bias", 1024, 1024), ("bias", 1024, 4096)])
 def test_linear_rows_do_not_depend_on_m(epi, n, k):
     """Every GEMM kernel accumulates an element over the same K slices in the
     same order and rounds it the same way: the first rows of an 8192-row
-    product (256 x 256 tiles at N = 4096, 256-row tiles at N = 1024) equal,
+    product (256 x 256 tiles at N = 4096, 256 x 192 at N = 3072, 256-row tiles
+    at N = 1024) equal,
     bit for bit, the same rows computed alone (7 and 32 rows: the 32 x 16
     tiles on 16 x 16 x 16 MFMAs; 160 rows: the 64 x 64 tiles; 792 to 3,500:
     the tiles the cost model picks up to 4,096 rows -- at N = 4096 128 x 128,
     160 x 128 or 192 x 128 (GELU), 192 x 128, 256 x 128 and 256 x 256, at N =
     1024 64 x 64, 128 x 128 and 160 x 128; 4896: 320 x 256 tiles with GELU,
-    256 x 256 + 128 x 128 without, 160 x 128 at N = 1024 (eight waves of three
-    or two row groups), also at K = 4096: the FFN-down shape)."""
+    256 x 256 + 128 x 128 without (one round of 256 x 256 at N = 3072, the
+    QKV shape), 160 x 128 at N = 1024 (eight waves of three or two row
+    groups), also at K = 4096: the FFN-down shape)."""
     r = np.random.default_rng(21)
     x = r.standard_normal((8192, k)).astype(np.float16)
     w = (r.standard_normal((n, k)) / np.sqrt(k)).astype(np.float16)
