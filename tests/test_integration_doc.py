@@ -1,5 +1,6 @@
-"""INTEGRATION.md's Swift binding against the C headers and the reference's
-public Swift surface (CPU only; nothing is compiled or launched).
+"""The Swift binding in the integration guide (the ```swift blocks of the
+Markdown file at DOC) against the C headers and the reference's public Swift
+surface (CPU only; nothing is compiled or launched).
 
 The binding is documentation a maintainer pastes into the reference package,
 so nothing else checks it: these tests fail when it calls a `gd_*` function
