@@ -4,7 +4,7 @@
 // gathers, additive key mask, SDPA) with the index math of :498-551.
 //
 // One work item = (batch b, head h, 128 queries), run by a workgroup of 8
-// waves, wave w owning queries q0 + 16w .. q0 + 16w + 15.  The LDS holds one
+// waves, each owning 16 consecutive queries.  The LDS holds one
 // workgroup per CU; up to L = 256 the grid has one workgroup per CU, each
 // looping over items and fetching the next item's first stage while it
 // finishes the current one.  Keys stream through LDS in chunks of 64.  The
@@ -195,6 +195,10 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   // Wave-uniform values live in scalar registers: branches on them are scalar
   // and their address arithmetic runs once per wave, not per lane.
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  // The wave's 16-query group: groups 0-3 go to waves 0, 3, 5 and 6, so the
+  // active waves of an item with few queries sit on distinct SIMDs whether a
+  // workgroup's waves are dealt to the SIMDs in turn or in pairs.
+  const int qgrp = (0x73261540 >> (4 * wave)) & 7;
   const int lc = lane & 15;  // MFMA output column: the lane's query
   const int g = lane >> 4;   // lane group
   const float inv_scale16 = 1.0f / scale16;  // correctly rounded fp32 reciprocal
@@ -322,7 +326,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   // count the DMA, which is inline assembly) then cannot wait for that DMA.
   auto setup_of = [&](const Item& it) -> Setup {
     Setup su;
-    const int q0 = it.qt * kQT, qw = q0 + 16 * wave;
+    const int q0 = it.qt * kQT, qw = q0 + 16 * qgrp;
     su.mval = mask[(int64_t)it.b * L + (t < L ? t : L - 1)];
     const int qr = qw + lc < it.klim ? qw + lc : it.klim - 1;
     const half_t* qrow = slice_base(Q, it.b, it.h, it.row0, qsb, qsh, qsl) + (int64_t)qr * qsl;
@@ -365,7 +369,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
       const int swz_hi = swz(lc, 4 + g);
       const int b = cur.b, h = cur.h;
       const int q0 = cur.qt * kQT;
-      const int qw = q0 + 16 * wave;
+      const int qw = q0 + 16 * qgrp;
       // Key tiles and chunks of this item: up to its row extent.  An item
       // whose queries all lie past the extent computes nothing; it runs one
       // chunk step (its first stage is already in flight) and loads no V.
@@ -471,8 +475,8 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
           // NOMASK: every key of the chunk is valid (its mask term is 0)
           constexpr bool NOMASK = decltype(nomask_c)::value;
           // c2p for this wave's 16 queries and the chunk's keys: window rows
-          // [16 wave, 16 wave + 80) (distances qw - kc - 63 .. qw - kc + 16)
-          const int crow0 = 16 * wave;
+          // [16 qgrp, 16 qgrp + 80) (distances qw - kc - 63 .. qw - kc + 16)
+          const int crow0 = 16 * qgrp;
           if constexpr (!B32) {  // the fp32 chains compute c2p per key tile instead
 #pragma unroll
           for (int tw = 0; tw < kC2PCols / 16; ++tw) {
@@ -490,7 +494,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
           }
 
           // Per 16-key tile tt: S^T = K Q^T (scores) and P2C over the 32 window
-          // rows [prow0, prow0 + 32) the tile needs (prow0 = 16 (wave - tt) +
+          // rows [prow0, prow0 + 32) the tile needs (prow0 = 16 (qgrp - tt) +
           // 48) into p2c_w.  Tiles are software-pipelined: tile tt's gathers are
           // issued before tile tt+1's MFMAs and p2c stores (the LDS executes a
           // wave's accesses in order, so one p2c buffer suffices), and tile tt is
@@ -502,7 +506,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
           // [prow0', prow0' + 16) (prow0 = prow0' - 16): kept from its fragments.
           auto prep_load = [&](int tt) {
             const int par = tt & 1;
-            const int prow0 = 16 * (wave - tt) + 48;
+            const int prow0 = 16 * (qgrp - tt) + 48;
             fk[par][0] = *reinterpret_cast<const half8_t*>(Ks + 16 * tt * kD + swz_lo);
             fk[par][1] = *reinterpret_cast<const half8_t*>(Ks + 16 * tt * kD + swz_hi);
             fq[par][0] = *reinterpret_cast<const half8_t*>(PQs + rr(prow0) + swz_lo);
@@ -547,7 +551,7 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
               // C2P^T = posK[the tile's 32 window rows] . Q^T, the same window
               // rows as the p2c fragments; lane holds (row 16 j + 4 g + i,
               // query lc).
-              const int prow0 = 16 * (wave - tt) + 48;
+              const int prow0 = 16 * (qgrp - tt) + 48;
 #pragma unroll
               for (int j = 0; j < 2; ++j) {
                 const half8_t a0 = *reinterpret_cast<const half8_t*>(PKs + rr(prow0 + 16 * j) + swz_lo);
