@@ -195,9 +195,10 @@ __global__ __launch_bounds__(kThreads) void deberta_attention_kernel(
   // Wave-uniform values live in scalar registers: branches on them are scalar
   // and their address arithmetic runs once per wave, not per lane.
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  // The wave's 16-query group: groups 0-3 go to waves 0, 3, 5 and 6, so the
-  // active waves of an item with few queries sit on distinct SIMDs whether a
-  // workgroup's waves are dealt to the SIMDs in turn or in pairs.
+  // The wave's 16-query group: groups 0-3 go to waves 0, 3, 5 and 6, then
+  // 1, 2, 4, 7.  Waves w and w + 4 share a SIMD (the HW_ID register read on
+  // the device), so up to four active groups sit on distinct SIMDs in this
+  // order as in wave order; this one measured 0.5% faster on the packed step.
   const int qgrp = (0x73261540 >> (4 * wave)) & 7;
   const int lc = lane & 15;  // MFMA output column: the lane's query
   const int g = lane >> 4;   // lane group

@@ -871,9 +871,10 @@ __global__ __launch_bounds__(512) void gemm_lds_split160_kernel(const half_t* __
       }
     }
   };
-  // Waves 0, 2, 5 and 7 take three row groups, 1, 3, 4 and 6 two: one of each
-  // on a SIMD whether a workgroup's waves are dealt to the SIMDs in turn or in
-  // pairs.
+  // Waves 0, 2, 5 and 7 take three row groups, 1, 3, 4 and 6 two: waves w
+  // and w + 4 share a SIMD (the HW_ID register read on the device), so each
+  // SIMD holds one of each (as it would with waves dealt to the SIMDs in
+  // pairs).
   if (((wave ^ (wave >> 2)) & 1) == 0) run(ic<3>{}, 0, 5 * wn);
   else run(ic<2>{}, 96, 5 * wn + 3);
 }
