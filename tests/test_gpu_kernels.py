@@ -207,7 +207,9 @@ def test_linear_rows_do_not_depend_on_m(epi, n, k):
     1024 64 x 64, 128 x 128 and 160 x 128; 4896: 320 x 256 tiles with GELU,
     256 x 256 + 128 x 128 without (one round of 256 x 256 at N = 3072, the
     QKV shape), 160 x 128 at N = 1024 (eight waves of three or two row
-    groups), also at K = 4096: the FFN-down shape)."""
+    groups), also at K = 4096: the FFN-down shape; 5100: the same kernels
+    with a last tile row of 140 rows, which ends inside the two-group waves'
+    rows of the 160 x 128 tiles)."""
     r = np.random.default_rng(21)
     x = r.standard_normal((8192, k)).astype(np.float16)
     w = (r.standard_normal((n, k)) / np.sqrt(k)).astype(np.float16)
@@ -217,7 +219,7 @@ def test_linear_rows_do_not_depend_on_m(epi, n, k):
         return t.cpu().numpy().view(np.uint16)
 
     full = bits(fk().linear(dev(x), dev(w), dev(b), epilogue=epi))
-    for m in (7, 32, 160, 792, 1100, 1500, 1800, 2600, 3500, 4896):
+    for m in (7, 32, 160, 792, 1100, 1500, 1800, 2600, 3500, 4896, 5100):
         np.testing.assert_array_equal(bits(fk().linear(dev(x[:m]), dev(w), dev(b), epilogue=epi)), full[:m])
 
 
