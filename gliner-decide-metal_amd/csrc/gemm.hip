@@ -323,30 +323,32 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
                 "epilogue staging must fit in the stage buffers");
   static_assert((NSTAGE - 1) * LPS < 64, "vmcnt range");
 
-  // The GELU epilogue reads the correctly rounded table from LDS.  For the
-  // 320-row tiles st0 holds all of it and the table's DMA replaces the
-  // redundant refill of st0 under the last K steps, so it lands while the
-  // last MFMAs run; C then goes through st1 (measured: 1.4 us off FFN-up at
-  // 4,896 rows; on 256 x 256 tiles the same is 0.6 us slower).  Otherwise the
-  // table is copied after the K loop into st1 (two stages: st1 sized for all
-  // of it; more stages: its first STAGE entries to st1, the rest to st2), and
-  // C goes through st0.  C passes take RPA rows, each wave's WM rows
-  // inside one pass (or, for 320-row tiles, one 32-row group of every wave
-  // row per pass).
+  // The GELU epilogue reads the correctly rounded table from LDS: the full
+  // 65,536-entry table where the joined stage buffers hold it (below), else
+  // the compact one, copied after the K loop into st1 (two stages: st1 sized
+  // for all of it; more stages: its first STAGE entries to st1, the rest to
+  // st2), with C through st0.  C passes take RPA rows, each wave's WM rows
+  // inside one pass (or, where they do not fit one, one 32-row group of every
+  // wave row per pass).
   constexpr bool GELU_TABLE = EPI == GD_EPI_BIAS_GELU && (RPA % WM == 0 || WAVES_M * 32 <= RPA) &&
                               (NSTAGE == 2 || 2 * STAGE >= kGeluEntries);
   static_assert(EPI != GD_EPI_BIAS_GELU || GELU_TABLE || NSTAGE * RPA >= BM, "GELU epilogue staging");
   // Tiles whose stage buffers hold 128 KiB (and whose GELU values all fit
   // the registers before C is staged) read the full 65,536-entry table:
   // the stages are then one array, the table lands in it after the K loop.
-  constexpr bool FULLTAB = GELU_TABLE && BM != 320 && RPA % WM == 0 && NSTAGE * STAGE >= 65536;
-  constexpr bool TAB0 = GELU_TABLE && NSTAGE == 2 && BM == 320;  // the table in st0, DMA'd under the K loop
+  // The 320-row tiles stage C one wave row (160 rows) per pass in that array
+  // (FFN-up at 4,896 rows 52.4-53.3 -> 51.4-52.7 us against the compact table
+  // DMA'd under the last K step; the packed step +1.3%, its FFN-down reading
+  // the plainly stored output).
+  constexpr int RPF = NSTAGE * STAGE / BN / WM * WM;  // whole wave rows that the joined stages hold
+  constexpr bool FULLTAB = GELU_TABLE && NSTAGE * STAGE >= 65536 && (BM == 320 ? RPF >= WM : RPA % WM == 0);
+  constexpr int RPP = FULLTAB && BM == 320 ? RPF : RPA;  // C rows per pass of the GELU epilogue
   constexpr int TAB1 = NSTAGE == 2 || kGeluEntries <= STAGE ? kGeluEntries : STAGE;  // entries in st1
   constexpr int kA = FULLTAB ? 16 : 1024;  // alignment of the separate buffers (unused with FULLTAB)
   __shared__ __attribute__((aligned(1024))) half_t stall[FULLTAB ? NSTAGE * STAGE : 8];
-  __shared__ __attribute__((aligned(kA))) half_t st0[FULLTAB ? 8 : (TAB0 && kGeluEntries > STAGE ? kGeluEntries : STAGE)];
+  __shared__ __attribute__((aligned(kA))) half_t st0[FULLTAB ? 8 : STAGE];
   __shared__ __attribute__((aligned(kA)))
-  half_t st1[FULLTAB ? 8 : (GELU_TABLE && !TAB0 && NSTAGE == 2 && kGeluEntries > STAGE ? kGeluEntries : STAGE)];
+  half_t st1[FULLTAB ? 8 : (GELU_TABLE && NSTAGE == 2 && kGeluEntries > STAGE ? kGeluEntries : STAGE)];
   __shared__ __attribute__((aligned(kA))) half_t st2[NSTAGE > 2 && !FULLTAB ? STAGE : 8];
   __shared__ __attribute__((aligned(kA))) half_t st3[NSTAGE > 3 && !FULLTAB ? STAGE : 8];
   __shared__ __attribute__((aligned(kA))) half_t st4[NSTAGE > 4 && !FULLTAB ? STAGE : 8];
@@ -393,13 +395,6 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
     const int n = tile_n * BN + blk * Lay::kRowsPerBlock + lane / Lay::kChunks;
     b_off[j] = (uint32_t)((int64_t)n * K + Lay::dma_chunk(lane, blk) * 8);
   }
-  // The GELU table into st0 as 1 KiB direct-to-LDS blocks, wave w taking
-  // blocks w, w + NW, ...
-  auto issue_table = [&]() {
-    constexpr int kBlocks = kGeluEntries / 512;
-    static_assert(kGeluEntries % 512 == 0, "whole blocks");
-    for (int j = wave; j < kBlocks; j += NW) load_lds16(g_gelu_table + j * 512 + lane * 8, st0 + j * 512);
-  };
   auto issue = [&](half_t* st, int k0) {
 #pragma unroll
     for (int j = 0; j < A_BLK; ++j) load_lds16(A + (a_off[j] + (uint32_t)k0), st + (wave * A_BLK + j) * 512);
@@ -489,13 +484,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
     // after it may stay in flight.
     wait_vmcnt<(NSTAGE - 2) * LPS>();
     stage_barrier();
-    if constexpr (TAB0) {
-      // (two stages: every wait is vmcnt(0), so a DMA of another size is fine)
-      if (kt + NSTAGE < nk) issue(stage(b), (kt + NSTAGE) * BK);
-      else if constexpr (B == 0) issue_table();  // st0's last K step has been read
-    } else {
-      issue(stage(b), min((kt + NSTAGE) * BK, last_k0));
-    }
+    issue(stage(b), min((kt + NSTAGE) * BK, last_k0));
     read_frags(stage(ic<(B + 1) % NSTAGE>{}), 0, 0);  // unused after the last step
     mma((S - 1) & 1);
     interleave();
@@ -558,19 +547,19 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
     }
   };
   if constexpr (GELU_TABLE) {
-    // ---- GELU epilogue: the table in st0 (two stages) or st1 + st2, C
-    // through the other buffer in passes ----
-    const half_t* tab = FULLTAB ? stall : (TAB0 ? st0 : st1);
+    // ---- GELU epilogue: the full table in the joined stages, or the
+    // compact one in st1 (+ st2), C through st0 in passes ----
+    const half_t* tab = FULLTAB ? stall : st1;
     const half_t* tab2 = stage(ic<2 % NSTAGE>{});
-    constexpr uint32_t kSplit = TAB0 ? kGeluEntries : TAB1;
-    half_t* const cst = FULLTAB ? stall : (TAB0 ? st1 : st0);
+    constexpr uint32_t kSplit = TAB1;
+    half_t* const cst = FULLTAB ? stall : st0;
     if constexpr (FULLTAB) {
       // the full table by DMA into the stage buffers (all read: the K loop's
       // last barrier), wave w taking 1 KiB blocks w, w + NW, ...
       for (int j = wave; j < 65536 / 512; j += NW) load_lds16(g_gelu_full + j * 512 + lane * 8, stall + j * 512);
       wait_vmcnt<0>();
       __syncthreads();
-    } else if constexpr (!TAB0) {
+    } else {
       // All of this thread's table pieces are loaded before any is stored,
       // so the L2 latency is paid once.
       constexpr int kPieces = kGeluEntries / 8;
@@ -601,7 +590,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
       }
       return r;
     };
-    if constexpr (RPA % WM == 0) {
+    if constexpr (RPP % WM == 0) {
       half4_t res[TM][TN][4];
 #pragma unroll
       for (int i = 0; i < TM; ++i)
@@ -610,11 +599,11 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
 #pragma unroll
           for (int q = 0; q < 4; ++q) res[i][j][q] = gelu_of(i, j, q);
       if constexpr (FULLTAB) __syncthreads();  // every wave's table reads precede the staging writes
-      constexpr int NPASS = (BM + RPA - 1) / RPA;
+      constexpr int NPASS = (BM + RPP - 1) / RPP;
 #pragma unroll
       for (int pass = 0; pass < NPASS; ++pass) {
-        const int row_lo = wm * WM - pass * RPA;  // this wave's first row within the pass
-        if (row_lo >= 0 && row_lo < RPA) {
+        const int row_lo = wm * WM - pass * RPP;  // this wave's first row within the pass
+        if (row_lo >= 0 && row_lo < RPP) {
 #pragma unroll
           for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -625,12 +614,13 @@ __global__ __launch_bounds__(64 * NW) void gemm_nt_lds_kernel(const half_t* __re
                     res[i][j][q];
         }
         __syncthreads();
-        const int pass_rows = BM - pass * RPA < RPA ? BM - pass * RPA : RPA;
-        store_rows(pass * RPA, pass_rows, [&](int r) { return cst + r * BN; });
+        const int pass_rows = BM - pass * RPP < RPP ? BM - pass * RPP : RPP;
+        store_rows(pass * RPP, pass_rows, [&](int r) { return cst + r * BN; });
         __syncthreads();
       }
     } else {
-      // A wave's rows do not fit one pass (320-row tiles): pass i takes the
+      // A wave's rows do not fit one pass (the 160- and 192-row tiles with the
+      // compact table): pass i takes the
       // i-th 32-row group of every wave row, WAVES_M x 32 rows through st0,
       // its GELU evaluated in the pass.
 #pragma unroll
@@ -897,8 +887,9 @@ int launch_lds_split160(const half_t* A, const half_t* W, const half_t* bias, ha
   return GD_OK;
 }
 
-// 320 x 256 tiles (two 64-deep stages, 144 KiB), GELU epilogue only: one
-// round over up to 320 rows per tile row where 256-row tiles need a second.
+// 320 x 256 tiles (two 64-deep stages, 144 KiB, the full GELU table in them
+// after the K loop), GELU epilogue only: one round over up to 320 rows per
+// tile row where 256-row tiles need a second.
 int launch_lds_tile_gelu320(const half_t* A, const half_t* W, const half_t* bias, half_t* C, int M, int N, int K,
                             int64_t lda, int64_t ldc, hipStream_t stream) {
   const int tiles_m = (M + 319) / 320;
@@ -1304,8 +1295,8 @@ int launch_linear(const void* a, const void* w, const void* bias, void* c, int64
       bm = 256, bn = 256;
       best = rounds(256, 256) * 1.5;
     }
-    // With GELU, 320 x 256 tiles (two stages, 144 KiB, the table under the K
-    // loop) at about 1.95 of a 256 x 128 tile: FFN-up on 8,193 to 10,240
+    // With GELU, 320 x 256 tiles (two stages, 144 KiB) at about 1.95 of a
+    // 256 x 128 tile: FFN-up on 8,193 to 10,240
     // rows takes two rounds of them against three of 256 x 256 (9,500 rows:
     // 105.3 -> 93.6 us).
     if (epilogue_kind == GD_EPI_BIAS_GELU && N % 256 == 0 && rounds(320, 256) * 1.95 < best)
